@@ -1,0 +1,150 @@
+/*
+ * h3attn.h - C ABI of the MI355X (gfx950) exact-attention library for the
+ * MiniMax-H3 video DiT: dense flash-attention forward, block-sparse forward,
+ * fused per-head qk-RMSNorm + split-half RoPE prologue.
+ *
+ * Conventions (every entry point):
+ *   - bf16 tensors are passed as raw device pointers (uint16_t storage).
+ *   - Strides are in ELEMENTS; the innermost (head_dim) stride is always 1.
+ *   - Device pointers and every outer stride must be 16-byte aligned
+ *     (strides multiple of 8 elements) so rows move as 128-bit accesses.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
+ *     and never synchronised.  No global mutable state: thread-safe.
+ *   - Return 0 (H3A_OK) on success, a non-zero H3A_ERR_* code otherwise;
+ *     h3a_last_error() then holds a thread-local message.  Argument checks run
+ *     before any HIP call, so bad arguments never reach the GPU.
+ *
+ * Reference surfaces replaced (paths relative to the reference checkout):
+ *   attn_sm80/fa3_sm80_h3.cu:460-470  fa3_sm80_h3_launch  -> h3a_attn_fwd
+ *   attn_sm80/fa3_sm80_h3.cu:472-482  fa3_pp_launch       -> h3a_attn_fwd
+ *   attn_sm80/fa3_sm80_h3.cu:485-512  kernel_attrs/pp_attrs -> h3a_kernel_attrs
+ *   attn_sm80/fa3_sm80_h3.cu:516-570  test_qk/test_pv     -> h3a_test_qk/h3a_test_pv
+ *   attn_sm80/fa3_sm80_h3.cu:584-593  pybind module       -> this header
+ *   custom_nodes/h3_sla/__init__.py:232-234 get_block_map + SLA _attention.apply
+ *                                     -> h3a_block_map_to_lut + h3a_attn_fwd_blocksparse
+ *   harness/sp_runtime.py:98, custom_nodes/h3_profiler/__init__.py:104-105
+ *     comfy.quant_ops.ck.rms_rope_split_half_  -> h3a_qk_rmsnorm_rope
+ */
+#ifndef H3ATTN_H
+#define H3ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define H3A_OK               0
+#define H3A_ERR_INVALID_ARG  1  /* null pointer, non-positive size, bad value   */
+#define H3A_ERR_UNSUPPORTED  2  /* head_dim != 128, unsupported tile size, ...  */
+#define H3A_ERR_ALIGNMENT    3  /* pointer or stride not 16-byte aligned        */
+#define H3A_ERR_HIP          4  /* a HIP runtime call or kernel launch failed   */
+
+/* hipStream_t, kept opaque so FFI callers need no HIP headers. */
+typedef void *h3a_stream_t;
+
+/* Library version string, e.g. "h3attn 0.1.0 gfx950". */
+const char *h3a_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *h3a_last_error(void);
+
+/*
+ * Dense non-causal attention forward:
+ *   O[b,h,i,:] = softmax_j(scale * Q[b,h,i,:] . K[b,h,j,:]) V[b,h,j,:]
+ * q: [B,H,Sq,D], k/v: [B,H,Skv,D], o: [B,H,Sq,D], all bf16, D == 128.
+ * *_strides = {batch, head, seq} in elements.  fp32 accumulation; P is
+ * rounded to bf16 before the PV product (as the reference kernel does,
+ * attn_sm80/fa3_sm80_h3.cu:405-420).  Sq != Skv is allowed (pad path,
+ * harness/sp_runtime.py:106-109).  scale > 0 (1/sqrt(128) for the DiT).
+ * Replaces fa3_sm80_h3_launch (attn_sm80/fa3_sm80_h3.cu:460-470), which
+ * ignored B, fixed the scale and launched on the legacy default stream.
+ */
+int h3a_attn_fwd(const void *q, const void *k, const void *v, void *o,
+                 int B, int H, int Sq, int Skv, int D,
+                 const int64_t q_strides[3], const int64_t k_strides[3],
+                 const int64_t v_strides[3], const int64_t o_strides[3],
+                 float scale, h3a_stream_t stream);
+
+/*
+ * Block-sparse attention forward (h3_sla path, custom_nodes/h3_sla/__init__.py:226-235).
+ * Query block qb of (b,h) attends only to the key blocks listed in
+ *   lut[((b*H + h)*nqb + qb)*max_k_blocks + 0 .. counts[(b*H+h)*nqb + qb]-1]
+ * (key-block indices in units of blk_k keys; nqb = ceil(Sq/blk_q)).
+ * Skipped blocks contribute nothing; a query block with no kept key block
+ * gets O = 0.  blk_q in {64,128}; blk_k in {64,128}.  Other arguments as
+ * h3a_attn_fwd.
+ */
+int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o,
+                             int B, int H, int Sq, int Skv, int D,
+                             const int64_t q_strides[3], const int64_t k_strides[3],
+                             const int64_t v_strides[3], const int64_t o_strides[3],
+                             const int32_t *lut, const int32_t *counts,
+                             int blk_q, int blk_k, int max_k_blocks,
+                             float scale, h3a_stream_t stream);
+
+/*
+ * Compact a boolean block map [B,H,nq,nk] (uint8, 0/1, contiguous) into the
+ * LUT form h3a_attn_fwd_blocksparse consumes: lut [B,H,nq,max_k_blocks]
+ * (kept key-block indices in ascending order, tail entries set to -1) and
+ * counts [B,H,nq].  Rows with more than max_k_blocks kept blocks are an
+ * error only if detected on the host; the device clamps to max_k_blocks.
+ * Replaces the (sparse_map, lut) pair returned by SLA's get_block_map
+ * (custom_nodes/h3_sla/__init__.py:232).
+ */
+int h3a_block_map_to_lut(const uint8_t *block_map, int B, int H, int nq, int nk,
+                         int32_t *lut, int32_t *counts, int max_k_blocks,
+                         h3a_stream_t stream);
+
+/*
+ * Fused per-head qk-RMSNorm + split-half RoPE, in place on q and k
+ * (comfy.quant_ops.ck.rms_rope_split_half_, called at harness/sp_runtime.py:98
+ * and custom_nodes/h3_profiler/__init__.py:104-105).
+ * q, k: [B,S,H,D] bf16 views; *_strides = {batch, seq, head} in elements
+ * (the DiT passes strided views of the fused QKV output: seq stride 3*H*D).
+ * For every (b,s,h) row x (fp32 math):
+ *   y = x * rsqrt(mean(x^2) + eps) * w            (w = qw or kw, bf16 [D])
+ *   for i < rot_dim/2, with R = rope[b,s,i] (2x2, row-major):
+ *     y'[i]           = R00*y[i] + R01*y[i+rot_dim/2]
+ *     y'[i+rot_dim/2] = R10*y[i] + R11*y[i+rot_dim/2]
+ *   dims >= rot_dim are only normalised; result rounded to bf16 (RNE).
+ * rope: fp32, element (b,s,i,r,c) at b*rope_sb + s*rope_ss + i*4 + r*2 + c
+ * (ComfyUI's rope_freqs [B,S,1,rot/2,2,2] layout; rope_sb may be 0).
+ * rot_dim: even, multiple of 16, <= D.  D == 128.
+ */
+int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D,
+                        const int64_t q_strides[3], const int64_t k_strides[3],
+                        const float *rope, int64_t rope_sb, int64_t rope_ss,
+                        int rot_dim, const void *qw, const void *kw, float eps,
+                        h3a_stream_t stream);
+
+/* Kernel identifiers for h3a_kernel_attrs. */
+#define H3A_KERNEL_ATTN_DENSE      0
+#define H3A_KERNEL_ATTN_SPARSE_128 1
+#define H3A_KERNEL_ATTN_SPARSE_64  2
+#define H3A_KERNEL_QK_ROPE         3
+
+/*
+ * out[6] = {VGPRs per thread, LDS bytes per workgroup, max resident
+ * workgroups per CU, device clock kHz, occupancy (resident waves / max
+ * waves per CU), threads per workgroup}.  Mirrors kernel_attrs/pp_attrs
+ * (attn_sm80/fa3_sm80_h3.cu:485-512).  Queries the current device.
+ */
+int h3a_kernel_attrs(int which, double out[6]);
+
+/*
+ * Fragment tests on one wavefront through the same LDS staging and MFMA
+ * fragment code as the attention kernel (counterparts of test_qk/test_pv,
+ * attn_sm80/fa3_sm80_h3.cu:516-570):
+ *   h3a_test_qk: S[32,64] (fp32) = Q[32,128] @ K[64,128]^T   (bf16 inputs)
+ *   h3a_test_pv: O[32,128] (fp32) = P[32,64] @ V[64,128]     (bf16 inputs)
+ * All buffers contiguous, row-major, device memory.
+ */
+int h3a_test_qk(const void *Q, const void *K, float *S, h3a_stream_t stream);
+int h3a_test_pv(const void *P, const void *V, float *O, h3a_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* H3ATTN_H */

@@ -1,0 +1,77 @@
+"""Build libh3attn.so (gfx950) in-tree from csrc/*.hip with hipcc.
+
+Usage: python build_lib.py [--verbose]
+
+The library lands next to the Python package (h3attn/libh3attn.so) so it
+travels with the source tree.  Every call rebuilds: compile each translation
+unit in parallel, then link.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+OUT_DIR = os.path.join(HERE, "h3attn")
+LIB_NAME = "libh3attn.so"
+BUILD_DIR = os.path.join(HERE, "_build")
+
+ARCH = "gfx950"
+# Packed-FP32 VALU ops are disabled for all device code.
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}",
+]
+
+
+def _hipcc() -> str:
+    p = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(p):
+        raise RuntimeError("hipcc not found; ROCm is required to build libh3attn")
+    return p
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless.
+    noise = [ln for ln in r.stderr.splitlines() if ln.strip() and "packed-fp32-ops" not in ln
+             and "is not a recognized feature" not in ln and not ln.startswith("1 warning")]
+    if verbose and noise:
+        print("\n".join(noise), flush=True)
+    return r
+
+
+def build(verbose: bool = False) -> str:
+    hipcc = _hipcc()
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+    objs = []
+    cmds = []
+    for s in srcs:
+        obj = os.path.join(BUILD_DIR, s[:-4] + ".o")
+        objs.append(obj)
+        cmds.append([hipcc, *CFLAGS, "-c", os.path.join(CSRC, s), "-o", obj])
+    workers = min(len(cmds), int(os.environ.get("MAX_JOBS", "8")))
+    with cf.ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    tmp = os.path.join(OUT_DIR, LIB_NAME + ".tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    final = os.path.join(OUT_DIR, LIB_NAME)
+    os.replace(tmp, final)
+    return final
+
+
+if __name__ == "__main__":
+    path = build(verbose="--verbose" in sys.argv)
+    print(path)

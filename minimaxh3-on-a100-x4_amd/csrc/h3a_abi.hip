@@ -1,0 +1,206 @@
+// extern "C" entry points of libh3attn (declared in include/h3attn.h):
+// argument validation, error reporting, dispatch to the kernel launchers.
+// Validation runs before any HIP call, so a bad argument never reaches the GPU.
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "h3a_internal.h"
+
+namespace h3a {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+int check_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(H3A_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+  return H3A_OK;
+}
+
+namespace {
+
+bool strides_ok(const int64_t s[3]) {
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || (s[i] & 7) != 0) return false;
+  return true;
+}
+
+// Checks shared by the dense and block-sparse attention entry points.
+int check_attn(const void *q, const void *k, const void *v, void *o, int B, int H, int Sq, int Skv,
+               int D, const int64_t *qs, const int64_t *ks, const int64_t *vs, const int64_t *os,
+               float scale) {
+  if (!q || !k || !v || !o) return fail(H3A_ERR_INVALID_ARG, "null tensor pointer");
+  if (!qs || !ks || !vs || !os) return fail(H3A_ERR_INVALID_ARG, "null stride array");
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
+  if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(H3A_ERR_INVALID_ARG, "softmax scale must be finite and > 0");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(H3A_ERR_ALIGNMENT, "tensor base pointers must be 16-byte aligned");
+  if (!strides_ok(qs) || !strides_ok(ks) || !strides_ok(vs) || !strides_ok(os))
+    return fail(H3A_ERR_ALIGNMENT, "strides must be non-negative multiples of 8 elements");
+  if (Skv > INT_MAX - 256 || Sq > INT_MAX - 256) return fail(H3A_ERR_INVALID_ARG, "sequence too long");
+  return H3A_OK;
+}
+
+void fill_attn_args(AttnArgs &a, const void *q, const void *k, const void *v, void *o, int B, int H,
+                    int Sq, int Skv, const int64_t *qs, const int64_t *ks, const int64_t *vs,
+                    const int64_t *os, float scale) {
+  a.q = static_cast<const uint16_t *>(q);
+  a.k = static_cast<const uint16_t *>(k);
+  a.v = static_cast<const uint16_t *>(v);
+  a.o = static_cast<uint16_t *>(o);
+  a.qsb = qs[0]; a.qsh = qs[1]; a.qss = qs[2];
+  a.ksb = ks[0]; a.ksh = ks[1]; a.kss = ks[2];
+  a.vsb = vs[0]; a.vsh = vs[1]; a.vss = vs[2];
+  a.osb = os[0]; a.osh = os[1]; a.oss = os[2];
+  a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv;
+  a.sl2 = scale * 1.4426950408889634f;
+  a.lut = nullptr; a.counts = nullptr; a.lut_stride = 0; a.sub = 1; a.blk_k = 64;
+}
+
+}  // namespace
+}  // namespace h3a
+
+using namespace h3a;
+
+extern "C" {
+
+const char *h3a_version(void) { return "h3attn 0.1.0 gfx950"; }
+
+const char *h3a_last_error(void) { return g_err; }
+
+int h3a_attn_fwd(const void *q, const void *k, const void *v, void *o, int B, int H, int Sq, int Skv,
+                 int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                 const int64_t v_strides[3], const int64_t o_strides[3], float scale,
+                 h3a_stream_t stream) {
+  clear_error();
+  int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
+  if (rc) return rc;
+  const int64_t nqt = (Sq + 127) / 128;
+  const int64_t total = (int64_t)B * H * nqt;
+  if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
+  AttnArgs a;
+  fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
+  a.nqt = (int)nqt;
+  a.total = (int)total;
+  return launch_attn_dense(a, as_stream(stream));
+}
+
+int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o, int B, int H,
+                             int Sq, int Skv, int D, const int64_t q_strides[3],
+                             const int64_t k_strides[3], const int64_t v_strides[3],
+                             const int64_t o_strides[3], const int32_t *lut, const int32_t *counts,
+                             int blk_q, int blk_k, int max_k_blocks, float scale,
+                             h3a_stream_t stream) {
+  clear_error();
+  int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
+  if (rc) return rc;
+  if (!lut || !counts) return fail(H3A_ERR_INVALID_ARG, "null lut/counts pointer");
+  if (blk_q != 64 && blk_q != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_q %d unsupported (64 or 128)", blk_q);
+  if (blk_k != 64 && blk_k != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_k %d unsupported (64 or 128)", blk_k);
+  const int64_t nkb = (Skv + blk_k - 1) / blk_k;
+  if (max_k_blocks <= 0 || max_k_blocks > nkb)
+    return fail(H3A_ERR_INVALID_ARG, "max_k_blocks %d outside [1, %lld]", max_k_blocks, (long long)nkb);
+  const int64_t nqt = (Sq + blk_q - 1) / blk_q;
+  const int64_t total = (int64_t)B * H * nqt;
+  if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
+  AttnArgs a;
+  fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
+  a.nqt = (int)nqt;
+  a.total = (int)total;
+  a.lut = lut;
+  a.counts = counts;
+  a.lut_stride = max_k_blocks;
+  a.blk_k = blk_k;
+  a.sub = blk_k / 64;
+  return launch_attn_sparse(a, blk_q, as_stream(stream));
+}
+
+int h3a_block_map_to_lut(const uint8_t *block_map, int B, int H, int nq, int nk, int32_t *lut,
+                         int32_t *counts, int max_k_blocks, h3a_stream_t stream) {
+  clear_error();
+  if (!block_map || !lut || !counts) return fail(H3A_ERR_INVALID_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || nq <= 0 || nk <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d nq=%d nk=%d)", B, H, nq, nk);
+  if (max_k_blocks <= 0 || max_k_blocks > nk)
+    return fail(H3A_ERR_INVALID_ARG, "max_k_blocks %d outside [1, %d]", max_k_blocks, nk);
+  const int64_t rows = (int64_t)B * H * nq;
+  if ((rows + 255) / 256 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "block map too large");
+  return launch_block_map_to_lut(block_map, B, H, nq, nk, lut, counts, max_k_blocks, as_stream(stream));
+}
+
+int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D, const int64_t q_strides[3],
+                        const int64_t k_strides[3], const float *rope, int64_t rope_sb,
+                        int64_t rope_ss, int rot_dim, const void *qw, const void *kw, float eps,
+                        h3a_stream_t stream) {
+  clear_error();
+  if (!q || !k || !qw || !kw) return fail(H3A_ERR_INVALID_ARG, "null tensor pointer");
+  if (!q_strides || !k_strides) return fail(H3A_ERR_INVALID_ARG, "null stride array");
+  if (B <= 0 || S <= 0 || H <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d S=%d H=%d)", B, S, H);
+  if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
+  if (rot_dim < 0 || rot_dim > D || (rot_dim % 16) != 0)
+    return fail(H3A_ERR_UNSUPPORTED, "rot_dim %d must be a multiple of 16 in [0, %d]", rot_dim, D);
+  if (rot_dim > 0 && !rope) return fail(H3A_ERR_INVALID_ARG, "null rope table with rot_dim > 0");
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(H3A_ERR_INVALID_ARG, "eps must be finite and >= 0");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(qw) || !aligned16(kw) || (rope && !aligned16(rope)))
+    return fail(H3A_ERR_ALIGNMENT, "pointers must be 16-byte aligned");
+  if (!strides_ok(q_strides) || !strides_ok(k_strides))
+    return fail(H3A_ERR_ALIGNMENT, "q/k strides must be non-negative multiples of 8 elements");
+  if (rot_dim > 0 && (rope_sb < 0 || rope_ss < 0 || (rope_sb & 3) || (rope_ss & 3)))
+    return fail(H3A_ERR_ALIGNMENT, "rope strides must be non-negative multiples of 4 floats");
+  const int64_t rows = (int64_t)B * S * H;
+  if ((rows + 15) / 16 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many rows");
+  RopeArgs a;
+  a.q = static_cast<uint16_t *>(q);
+  a.k = static_cast<uint16_t *>(k);
+  a.qsb = q_strides[0]; a.qss = q_strides[1]; a.qsh = q_strides[2];
+  a.ksb = k_strides[0]; a.kss = k_strides[1]; a.ksh = k_strides[2];
+  a.B = B; a.S = S; a.H = H;
+  a.rope = rope; a.rsb = rope_sb; a.rss = rope_ss; a.rot = rot_dim;
+  a.qw = static_cast<const uint16_t *>(qw);
+  a.kw = static_cast<const uint16_t *>(kw);
+  a.eps = eps;
+  a.rows = rows;
+  return launch_qk_rmsnorm_rope(a, as_stream(stream));
+}
+
+int h3a_kernel_attrs(int which, double out[6]) {
+  clear_error();
+  if (!out) return fail(H3A_ERR_INVALID_ARG, "null output array");
+  if (which == H3A_KERNEL_QK_ROPE) return rope_kernel_attrs(out);
+  if (which < H3A_KERNEL_ATTN_DENSE || which > H3A_KERNEL_ATTN_SPARSE_64)
+    return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
+  return attn_kernel_attrs(which, out);
+}
+
+int h3a_test_qk(const void *Q, const void *K, float *S, h3a_stream_t stream) {
+  clear_error();
+  if (!Q || !K || !S) return fail(H3A_ERR_INVALID_ARG, "null pointer");
+  if (!aligned16(Q) || !aligned16(K)) return fail(H3A_ERR_ALIGNMENT, "Q/K must be 16-byte aligned");
+  return launch_test_qk(static_cast<const uint16_t *>(Q), static_cast<const uint16_t *>(K), S,
+                        as_stream(stream));
+}
+
+int h3a_test_pv(const void *P, const void *V, float *O, h3a_stream_t stream) {
+  clear_error();
+  if (!P || !V || !O) return fail(H3A_ERR_INVALID_ARG, "null pointer");
+  if (!aligned16(P) || !aligned16(V)) return fail(H3A_ERR_ALIGNMENT, "P/V must be 16-byte aligned");
+  return launch_test_pv(static_cast<const uint16_t *>(P), static_cast<const uint16_t *>(V), O,
+                        as_stream(stream));
+}
+
+}  // extern "C"

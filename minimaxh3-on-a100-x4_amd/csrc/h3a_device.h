@@ -1,0 +1,63 @@
+// Device-side building blocks shared by the gfx950 kernels of libh3attn.
+//
+// MFMA fragment conventions (v_mfma_f32_32x32x16_bf16, one 64-lane wave):
+//   A operand (32 x 16, M x K): lane l holds A[l%32][k-slot (l/32, e)], e = 0..7
+//   B operand (16 x 32, K x N): lane l holds B[k-slot (l/32, e)][l%32]
+//   C/D (32 x 32, 16 fp32 per lane): lane l, register r holds
+//        C[8*(r/4) + 4*(l/32) + r%4][l%32]
+// A and B pair their k-slots by (l/32, e), so any assignment of the 16
+// contraction indices to slots works as long as A and B agree.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace h3a {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Two fp32 -> packed bf16 pair (round to nearest even; v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Value held by the lane 32 positions away (lanes l and l^32 exchange):
+// combine(x) over the pair is op(pair.x, pair.y) on both halves.
+__device__ __forceinline__ float half_swap_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X.  Remap
+// the dispatch index so each XCD walks one contiguous range of work items
+// (consecutive query tiles of the same head), which keeps that head's K/V
+// stream resident in the XCD's own L2.  Bijective for any total.
+__device__ __forceinline__ int xcd_remap(int i, int total) {
+  constexpr int kXcds = 8;
+  const int per = total / kXcds, rem = total % kXcds;
+  const int x = i % kXcds, idx = i / kXcds;
+  return x * per + (x < rem ? x : rem) + idx;
+}
+
+}  // namespace h3a

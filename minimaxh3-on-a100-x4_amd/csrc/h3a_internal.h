@@ -1,0 +1,66 @@
+// Host-side helpers shared by the libh3attn translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "h3attn.h"
+
+namespace h3a {
+
+// Record a formatted message for h3a_last_error() on this thread; returns code.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Map the last HIP launch status to an H3A code (H3A_OK when clean).
+int check_launch(const char *what);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline hipStream_t as_stream(h3a_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Kernel-side argument block of the attention kernels (passed by value).
+struct AttnArgs {
+  const uint16_t *q, *k, *v;
+  uint16_t *o;
+  int64_t qsb, qsh, qss;
+  int64_t ksb, ksh, kss;
+  int64_t vsb, vsh, vss;
+  int64_t osb, osh, oss;
+  int B, H, Sq, Skv;
+  int nqt;    // query tiles per (b,h)
+  int total;  // B*H*nqt workgroups
+  float sl2;  // softmax scale * log2(e)
+  // block-sparse only
+  const int32_t *lut;
+  const int32_t *counts;
+  int lut_stride;  // max_k_blocks
+  int sub;         // 64-key stages per key block (blk_k / 64)
+  int blk_k;
+};
+
+// Launchers implemented in h3a_attn.hip / h3a_prologue.hip.
+int launch_attn_dense(const AttnArgs &a, hipStream_t s);
+int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s);
+int launch_block_map_to_lut(const uint8_t *map, int B, int H, int nq, int nk, int32_t *lut,
+                            int32_t *counts, int max_k_blocks, hipStream_t s);
+int launch_test_qk(const uint16_t *Q, const uint16_t *K, float *S, hipStream_t s);
+int launch_test_pv(const uint16_t *P, const uint16_t *V, float *O, hipStream_t s);
+int attn_kernel_attrs(int which, double out[6]);
+
+struct RopeArgs {
+  uint16_t *q, *k;
+  int64_t qsb, qss, qsh;
+  int64_t ksb, kss, ksh;
+  int B, S, H;
+  const float *rope;
+  int64_t rsb, rss;
+  int rot;
+  const uint16_t *qw, *kw;
+  float eps;
+  int64_t rows;  // B*S*H
+};
+int launch_qk_rmsnorm_rope(const RopeArgs &a, hipStream_t s);
+int rope_kernel_attrs(double out[6]);
+
+}  // namespace h3a

@@ -1,0 +1,247 @@
+"""Tensor-level entry points over the libh3attn C ABI.
+
+PyTorch supplies device memory and the current HIP stream; all arithmetic runs
+in the gfx950 kernels of libh3attn.  Every function validates shapes/dtypes on
+the host, passes raw pointers + element strides + torch's current stream, and
+raises (ValueError for bad arguments, H3AError for HIP failures).  There is no
+CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import check, lib, strides3
+
+HEAD_DIM = 128
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _norm_stride(t: torch.Tensor, dim: int) -> int:
+    # A size-1 dimension is never stepped along; its stride is irrelevant.
+    return 0 if t.shape[dim] == 1 else t.stride(dim)
+
+
+def _kernel_ready(t: torch.Tensor, outer_dims) -> bool:
+    """Last dim unit-stride, base 16-byte aligned, outer strides multiples of 8."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        return False
+    return all(_norm_stride(t, d) % 8 == 0 and _norm_stride(t, d) >= 0 for d in outer_dims)
+
+
+def _as_kernel_input(name: str, t: torch.Tensor) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (libh3attn has no CPU path)")
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be 4-D [B,H,S,D], got shape {tuple(t.shape)}")
+    if t.shape[-1] != HEAD_DIM:
+        raise ValueError(f"{name}: head_dim {t.shape[-1]} unsupported (only {HEAD_DIM})")
+    # Layouts the kernel cannot stream directly are made contiguous (same HIP path).
+    return t if _kernel_ready(t, (0, 1, 2)) else t.contiguous()
+
+
+def _bhs(t: torch.Tensor):
+    return strides3(_norm_stride(t, 0), _norm_stride(t, 1), _norm_stride(t, 2))
+
+
+def _prepare_attn(q, k, v, out):
+    q = _as_kernel_input("q", q)
+    k = _as_kernel_input("k", k)
+    v = _as_kernel_input("v", v)
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    if tuple(k.shape) != (B, H, Skv, D) or tuple(v.shape) != (B, H, Skv, D):
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if Sq == 0 or Skv == 0 or B == 0 or H == 0:
+        raise ValueError("empty attention input")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, v must be on the same device")
+    if out is None:
+        out = torch.empty((B, H, Sq, D), dtype=torch.bfloat16, device=q.device)
+    else:
+        if tuple(out.shape) != (B, H, Sq, D) or out.dtype != torch.bfloat16 or out.device != q.device:
+            raise ValueError("out must be a bf16 [B,H,Sq,128] tensor on q's device")
+        if not _kernel_ready(out, (0, 1, 2)):
+            raise ValueError("out must have unit last stride, 16-byte alignment and strides multiple of 8")
+    return q, k, v, out, (B, H, Sq, Skv, D)
+
+
+def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """Dense non-causal attention, q [B,H,Sq,128], k/v [B,H,Skv,128] bf16 -> [B,H,Sq,128].
+
+    Any strides with a unit last dimension are read in place (e.g. the
+    [1,H,S,D] transposed views of a fused QKV projection); `out` may also be a
+    strided view (e.g. [1,S,H,D] memory seen as [1,H,S,D]).
+    """
+    q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    rc = lib().h3a_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                            B, H, Sq, Skv, D, _bhs(q), _bhs(k), _bhs(v), _bhs(out), sc, _stream(q))
+    check("h3a_attn_fwd", rc)
+    return out
+
+
+def attn_fwd_blocksparse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lut: torch.Tensor,
+                         counts: torch.Tensor, blk_q: int, blk_k: int, scale: float | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Block-sparse attention over the kept key blocks listed in `lut`.
+
+    lut: int32 [B,H,ceil(Sq/blk_q),max_k_blocks] ascending key-block indices;
+    counts: int32 [B,H,ceil(Sq/blk_q)] number of valid entries per row.
+    """
+    q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
+    nqb = -(-Sq // blk_q)
+    if lut.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise ValueError("lut and counts must be int32")
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, nqb):
+        raise ValueError(f"lut must be [B,H,{nqb},max_k], got {tuple(lut.shape)}")
+    if tuple(counts.shape) != (B, H, nqb):
+        raise ValueError(f"counts must be [B,H,{nqb}], got {tuple(counts.shape)}")
+    if lut.device != q.device or counts.device != q.device:
+        raise ValueError("lut/counts must be on q's device")
+    lut = lut.contiguous()
+    counts = counts.contiguous()
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    rc = lib().h3a_attn_fwd_blocksparse(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Skv, D,
+        _bhs(q), _bhs(k), _bhs(v), _bhs(out), lut.data_ptr(), counts.data_ptr(),
+        int(blk_q), int(blk_k), int(lut.shape[3]), sc, _stream(q))
+    check("h3a_attn_fwd_blocksparse", rc)
+    return out
+
+
+def block_map_to_lut(block_map: torch.Tensor, max_k_blocks: int | None = None):
+    """Boolean/uint8 block map [B,H,nq,nk] -> (lut int32 [B,H,nq,max_k], counts int32 [B,H,nq])."""
+    if block_map.dim() != 4 or not block_map.is_cuda:
+        raise ValueError("block_map must be a 4-D GPU tensor [B,H,nq,nk]")
+    m = block_map.to(torch.uint8).contiguous()
+    B, H, nq, nk = m.shape
+    if max_k_blocks is None:
+        max_k_blocks = max(1, int(m.sum(dim=-1, dtype=torch.int32).max().item()))
+    lut = torch.empty((B, H, nq, max_k_blocks), dtype=torch.int32, device=m.device)
+    counts = torch.empty((B, H, nq), dtype=torch.int32, device=m.device)
+    rc = lib().h3a_block_map_to_lut(m.data_ptr(), B, H, nq, nk, lut.data_ptr(), counts.data_ptr(),
+                                    int(max_k_blocks), _stream(m))
+    check("h3a_block_map_to_lut", rc)
+    return lut, counts
+
+
+def _rope_table(rope: torch.Tensor, B: int, S: int, rot_dim: int):
+    """Validate a ComfyUI-style rope_freqs tensor; return (tensor, batch stride, seq stride)."""
+    if rope.dtype != torch.float32:
+        raise ValueError(f"rope table must be float32, got {rope.dtype}")
+    if rope.dim() < 4 or tuple(rope.shape[-2:]) != (2, 2):
+        raise ValueError(f"rope table must end in [rot/2, 2, 2], got {tuple(rope.shape)}")
+    if rope.shape[-3] != rot_dim // 2:
+        raise ValueError(f"rope table has {rope.shape[-3]} frequencies, rot_dim {rot_dim} needs {rot_dim // 2}")
+    # Accepted leading layouts: [S,...], [Bt,S,...], [Bt,S,1,...] (head axis broadcast).
+    lead = list(rope.shape[:-3])
+    lead_strides = list(rope.stride()[:-3])
+    if len(lead) == 3:
+        if lead[2] != 1:
+            raise ValueError("rope table head axis must have size 1")
+        lead, lead_strides = lead[:2], lead_strides[:2]
+    if len(lead) == 1:
+        lead, lead_strides = [1] + lead, [0] + lead_strides
+    if len(lead) != 2 or lead[1] != S or lead[0] not in (1, B):
+        raise ValueError(f"rope table leading dims {tuple(rope.shape[:-3])} do not match B={B}, S={S}")
+    inner = rope.stride()[-3:]
+    if tuple(inner) != (4, 2, 1):
+        rope = rope.contiguous()
+        return _rope_table(rope, B, S, rot_dim)
+    sb = 0 if lead[0] == 1 else lead_strides[0]
+    ss = lead_strides[1]
+    if rope.data_ptr() % 16 or sb % 4 or ss % 4:
+        rope = rope.contiguous()
+        return _rope_table(rope, B, S, rot_dim)
+    return rope, sb, ss
+
+
+def qk_rmsnorm_rope_(q: torch.Tensor, k: torch.Tensor, rope: torch.Tensor | None, qw: torch.Tensor,
+                     kw: torch.Tensor, eps: float = 1e-6, rot_dim: int | None = None) -> None:
+    """In-place per-head RMSNorm (weights qw/kw over head_dim) + split-half RoPE on q, k [B,S,H,128].
+
+    q and k are typically strided views of the fused QKV projection output.
+    The rotation for frequency i < rot_dim/2 is rope[..., s, i, :, :] applied to
+    the pair (x[i], x[i + rot_dim/2]).
+    """
+    for name, t in (("q", q), ("k", k)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 4 or t.shape[-1] != HEAD_DIM:
+            raise ValueError(f"{name} must be a bf16 GPU tensor [B,S,H,128], got {t.dtype} {tuple(t.shape)}")
+        if not _kernel_ready(t, (0, 1, 2)):
+            raise ValueError(f"{name}: in-place update needs unit last stride, 16-byte alignment and "
+                             "outer strides that are multiples of 8 elements")
+    if tuple(q.shape) != tuple(k.shape):
+        raise ValueError("q and k must have the same shape")
+    B, S, H, D = q.shape
+    if rot_dim is None:
+        rot_dim = 0 if rope is None else int(rope.shape[-3]) * 2
+    rot_dim = int(rot_dim)
+    ws = []
+    for name, w in (("qw", qw), ("kw", kw)):
+        if w.numel() != D:
+            raise ValueError(f"{name} must have {D} elements")
+        w = w.reshape(D).to(device=q.device, dtype=torch.bfloat16).contiguous()
+        ws.append(w)
+    if rot_dim > 0:
+        if rope is None:
+            raise ValueError("rope table required when rot_dim > 0")
+        rope, rsb, rss = _rope_table(rope.to(q.device), B, S, rot_dim)
+        rptr = rope.data_ptr()
+    else:
+        rptr, rsb, rss = None, 0, 0
+    rc = lib().h3a_qk_rmsnorm_rope(
+        q.data_ptr(), k.data_ptr(), B, S, H, D,
+        strides3(_norm_stride(q, 0), _norm_stride(q, 1), _norm_stride(q, 2)),
+        strides3(_norm_stride(k, 0), _norm_stride(k, 1), _norm_stride(k, 2)),
+        rptr, int(rsb), int(rss), rot_dim, ws[0].data_ptr(), ws[1].data_ptr(), float(eps), _stream(q))
+    check("h3a_qk_rmsnorm_rope", rc)
+
+
+def rms_rope_split_half_(q, k, rope_freqs, qw, kw, epsilon: float = 1e-6, rot_dim: int | None = None):
+    """Signature-compatible stand-in for comfy.quant_ops.ck.rms_rope_split_half_ (in place).
+
+    Called at harness/sp_runtime.py:98 and custom_nodes/h3_profiler/__init__.py:104-105
+    as rms_rope_split_half_(q, k, rope_freqs, qw, kw, epsilon=eps, rot_dim=rot).
+    """
+    qk_rmsnorm_rope_(q, k, rope_freqs, qw, kw, eps=epsilon, rot_dim=rot_dim)
+
+
+def test_qk(Q: torch.Tensor, K: torch.Tensor) -> torch.Tensor:
+    """S[32,64] fp32 = Q[32,128] @ K[64,128]^T on one wavefront through the attention fragment code."""
+    if tuple(Q.shape) != (32, 128) or tuple(K.shape) != (64, 128):
+        raise ValueError("test_qk expects Q[32,128], K[64,128]")
+    Q = Q.to(torch.bfloat16).contiguous()
+    K = K.to(torch.bfloat16).contiguous()
+    S = torch.empty((32, 64), dtype=torch.float32, device=Q.device)
+    check("h3a_test_qk", lib().h3a_test_qk(Q.data_ptr(), K.data_ptr(), S.data_ptr(), _stream(Q)))
+    return S
+
+
+def test_pv(P: torch.Tensor, V: torch.Tensor) -> torch.Tensor:
+    """O[32,128] fp32 = P[32,64] @ V[64,128] on one wavefront through the attention fragment code."""
+    if tuple(P.shape) != (32, 64) or tuple(V.shape) != (64, 128):
+        raise ValueError("test_pv expects P[32,64], V[64,128]")
+    P = P.to(torch.bfloat16).contiguous()
+    V = V.to(torch.bfloat16).contiguous()
+    O = torch.empty((32, 128), dtype=torch.float32, device=P.device)
+    check("h3a_test_pv", lib().h3a_test_pv(P.data_ptr(), V.data_ptr(), O.data_ptr(), _stream(P)))
+    return O
+
+
+def kernel_attrs(which: int = _lib.KERNEL_ATTN_DENSE):
+    """[VGPRs, LDS bytes, max WGs/CU, clock kHz, occupancy, threads] for a kernel (current device)."""
+    out = (ctypes.c_double * 6)()
+    check("h3a_kernel_attrs", lib().h3a_kernel_attrs(int(which), out))
+    return [float(x) for x in out]

@@ -1,0 +1,148 @@
+"""Block-sparse attention for the h3_sla path (custom_nodes/h3_sla/__init__.py).
+
+The reference runs thu-ml/SLA's `get_block_map` (mean-pooled q.k^T scores,
+top-k key blocks per query block) and SLA's Triton `_attention` over the kept
+blocks (custom_nodes/h3_sla/__init__.py:226-235).  Here the block map is built
+with torch ops on the GPU (pooling + a small batched product + top-k), compacted
+to a LUT by libh3attn, and the attention runs in the gfx950 block-sparse kernel,
+which never touches a skipped key block.
+
+Also mirrors the node's per-layer keep schedule (PRESETS, parse_ranges,
+parse_layer_keep, resolve_schedule; custom_nodes/h3_sla/__init__.py:44-96),
+whose table of presets must stay identical to the reference's.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import ops
+
+# Per-layer keep presets; the table is the reference's
+# (custom_nodes/h3_sla/__init__.py:44-49): every layer not listed keeps default_keep.
+PRESETS = {
+    "quality": {"default_keep": 0.15, "layers": {0.25: "31-42,46-49"}, "research_name": "E8"},
+    "balanced": {"default_keep": 0.15, "layers": {0.25: "31-42,48-49"}, "research_name": "T2"},
+    "speed": {"default_keep": 0.15, "layers": {0.25: "34-42"}, "research_name": "E3"},
+}
+PRESET_CHOICES = ["off", "quality", "balanced", "speed", "custom"]
+
+
+def parse_ranges(spec) -> list[int]:
+    """'31-42,46,48-49' -> [31, ..., 42, 46, 48, 49] (custom_nodes/h3_sla/__init__.py:57-63)."""
+    layers: list[int] = []
+    for item in str(spec).split(","):
+        item = item.strip()
+        if not item:
+            continue
+        lo, sep, hi = item.partition("-")
+        first = int(lo)
+        last = int(hi) if sep and hi else first
+        layers.extend(range(first, last + 1))
+    return layers
+
+
+def parse_layer_keep(spec) -> dict[int, float]:
+    """'25:31-42,46-49;20:43' -> {layer: keep}; values > 1 are percentages (h3_sla:66-74)."""
+    out: dict[int, float] = {}
+    for part in str(spec).split(";"):
+        part = part.strip()
+        if not part:
+            continue
+        val, _, ranges = part.partition(":")
+        keep = float(val)
+        if keep > 1.0:
+            keep /= 100.0
+        for layer in parse_ranges(ranges):
+            out[layer] = keep
+    return out
+
+
+def resolve_schedule(preset="off", topk=0.35, layer_keep="", n_layers=50):
+    """-> (name, [keep per layer]) (custom_nodes/h3_sla/__init__.py:77-96)."""
+    name = (preset or "off").lower()
+    if name == "off":
+        return "off", [float(topk)] * n_layers
+    keeps = [float(topk)] * n_layers
+    if name == "custom":
+        for layer, keep in parse_layer_keep(layer_keep).items():
+            if 0 <= layer < n_layers:
+                keeps[layer] = keep
+        return "custom", keeps
+    if name not in PRESETS:
+        raise ValueError(f"unknown SLA preset {name!r}; choose one of {PRESET_CHOICES}")
+    spec = PRESETS[name]
+    keeps = [float(spec["default_keep"])] * n_layers
+    for keep, ranges in spec["layers"].items():
+        for layer in parse_ranges(ranges):
+            if 0 <= layer < n_layers:
+                keeps[layer] = float(keep)
+    return name, keeps
+
+
+# ---------------------------------------------------------------------------
+def _block_means(x: torch.Tensor, blk: int) -> torch.Tensor:
+    """Mean over the valid rows of each block of `blk` rows: [B,H,S,D] -> [B,H,ceil(S/blk),D] fp32."""
+    B, H, S, D = x.shape
+    nb = -(-S // blk)
+    pad = nb * blk - S
+    xf = x.float()
+    if pad:
+        xf = torch.nn.functional.pad(xf, (0, 0, 0, pad))
+    sums = xf.reshape(B, H, nb, blk, D).sum(dim=3)
+    counts = torch.full((nb,), float(blk), device=x.device)
+    counts[-1] = blk - pad
+    return sums / counts.view(1, 1, nb, 1)
+
+
+def keep_count(topk_ratio: float, nk: int) -> int:
+    """Key blocks kept by score per query block: floor(ratio * nk), at least 1, at most nk."""
+    return max(1, min(nk, int(math.floor(topk_ratio * nk + 1e-9))))
+
+
+def block_scores(q: torch.Tensor, k: torch.Tensor, blk_q: int, blk_k: int,
+                 smooth_k: bool = False) -> torch.Tensor:
+    """Mean-pooled block scores [B,H,nq,nk] (fp32): pooled_q . pooled_k."""
+    kk = k
+    pk = _block_means(kk, blk_k)
+    if smooth_k:
+        pk = pk - k.float().mean(dim=2, keepdim=True)
+    pq = _block_means(q, blk_q)
+    return torch.matmul(pq, pk.transpose(-1, -2).contiguous())
+
+
+def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int = 64, BLKK: int = 64,
+                  force_diag: bool = False, smooth_k: bool = True):
+    """Block map from mean-pooled scores -> (block_map uint8 [B,H,nq,nk], lut int32, counts int32).
+
+    Defaults follow SLA's get_block_map as the h3_sla node calls it
+    (custom_nodes/h3_sla/__init__.py:232): k centred by its sequence mean
+    before pooling, top floor(ratio*nk) key blocks, no forced diagonal.
+    The BASELINE block-sparse workload uses force_diag=True, smooth_k=False.
+    """
+    scores = block_scores(q, k, BLKQ, BLKK, smooth_k=smooth_k)
+    B, H, nq, nk = scores.shape
+    kc = keep_count(topk_ratio, nk)
+    idx = torch.topk(scores, kc, dim=-1, sorted=False).indices
+    bmap = torch.zeros((B, H, nq, nk), dtype=torch.uint8, device=q.device)
+    bmap.scatter_(-1, idx, 1)
+    if force_diag:
+        qb = torch.arange(nq, device=q.device)
+        diag = (qb * BLKQ) // BLKK
+        ok = diag < nk
+        bmap[:, :, qb[ok], diag[ok]] = 1
+    max_k = kc + (1 if force_diag else 0)
+    lut, counts = ops.block_map_to_lut(bmap, max_k_blocks=min(max_k, nk))
+    return bmap, lut, counts
+
+
+def sparse_attention(q, k, v, topk_ratio: float, blk: int = 64, force_diag: bool = False,
+                     smooth_k: bool = True):
+    """[1,H,S,D] -> [1,H,S,D] block-sparse attention (SLA sparse branch only; h3_sla:226-235)."""
+    out_dtype = q.dtype
+    q16, k16, v16 = (t.to(torch.bfloat16) for t in (q, k, v))
+    _, lut, counts = get_block_map(q16, k16, topk_ratio, blk, blk, force_diag=force_diag,
+                                   smooth_k=smooth_k)
+    o = ops.attn_fwd_blocksparse(q16, k16, v16, lut, counts, blk, blk)
+    return o.to(out_dtype)

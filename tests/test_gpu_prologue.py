@@ -1,0 +1,94 @@
+"""Parity of the fused qk-RMSNorm + split-half RoPE kernel (h3a_qk_rmsnorm_rope) with the oracle.
+
+Call contract: comfy.quant_ops.ck.rms_rope_split_half_(q, k, rope_freqs, qw, kw,
+epsilon, rot_dim) on [1,S,H,D] strided views (harness/sp_runtime.py:93-99,
+custom_nodes/h3_profiler/__init__.py:99-106).  Outputs are bf16: the kernel
+(fp32 math) and the oracle (fp64 math) must agree to within one bf16 ulp,
+with at least 99% of values bit-identical.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import h3attn
+import oracle
+from conftest import from_dev_bf16, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(rng, S, H, spread=True):
+    x = rng.standard_normal((2, S, H, 128)).astype(np.float32)
+    if spread:  # per-token dynamic range U(0.5, 4), as BASELINE config 2
+        x *= rng.uniform(0.5, 4.0, size=(2, S, 1, 1)).astype(np.float32)
+    w = (1.0 + 0.05 * rng.standard_normal((2, 128))).astype(np.float32)
+    return oracle.f32_to_bf16(x), oracle.f32_to_bf16(w)
+
+
+def _compare(got_bits, ref_bits, what):
+    g = oracle.bf16_to_f32(got_bits).reshape(got_bits.shape).astype(np.float64)
+    r = oracle.bf16_to_f32(ref_bits).reshape(ref_bits.shape).astype(np.float64)
+    exact = np.mean(got_bits == ref_bits)
+    ulp = np.maximum(np.abs(r) * 2.0 ** -7, 1e-30)  # one bf16 ulp is <= 2^-7 |r|
+    assert np.all(np.abs(g - r) <= ulp), f"{what}: a value differs by more than one bf16 ulp"
+    assert exact >= 0.99, f"{what}: only {exact:.4f} bit-exact"
+
+
+def _run_gpu(xq, xk, w, rope, rot, device, fused_layout):
+    S, H = xq.shape[0], xq.shape[1]
+    if fused_layout:
+        qkv = torch.zeros(S, 3 * H * 128, dtype=torch.bfloat16, device=device)
+        q = qkv[:, :H * 128].view(1, S, H, 128)
+        k = qkv[:, H * 128:2 * H * 128].view(1, S, H, 128)
+        vpart = qkv[:, 2 * H * 128:]
+        vpart.copy_(torch.full_like(vpart, 0.5))
+        q.copy_(to_dev_bf16(xq, device).view(1, S, H, 128))
+        k.copy_(to_dev_bf16(xk, device).view(1, S, H, 128))
+    else:
+        q = to_dev_bf16(xq, device).view(1, S, H, 128).clone()
+        k = to_dev_bf16(xk, device).view(1, S, H, 128).clone()
+        vpart = None
+    rope_t = None if rope is None else torch.from_numpy(rope).view(1, S, 1, rot // 2, 2, 2).to(device)
+    h3attn.rms_rope_split_half_(q, k, rope_t, to_dev_bf16(w[0], device), to_dev_bf16(w[1], device),
+                                epsilon=1e-6, rot_dim=rot)
+    torch.cuda.synchronize()
+    if vpart is not None:
+        assert torch.all(vpart == 0.5), "kernel wrote outside q/k"
+    return from_dev_bf16(q)[0], from_dev_bf16(k)[0]
+
+
+@pytest.mark.parametrize("S,H,rot,fused", [
+    (37, 3, 128, False), (37, 3, 64, True), (5, 1, 0, False), (200, 7, 128, True), (64, 56, 32, True),
+])
+def test_prologue_small(gpu, S, H, rot, fused):
+    rng = np.random.default_rng(S * 100 + rot)
+    x, w = _inputs(rng, S, H)
+    rope = oracle.rope_table(S, rot) if rot else None
+    gq, gk = _run_gpu(x[0], x[1], w, rope, rot, gpu, fused)
+    rq, rk = oracle.qk_rmsnorm_rope(x[0][None], x[1][None], rope, w[0], w[1], eps=1e-6, rot_dim=rot)
+    _compare(gq, rq[0], "q")
+    _compare(gk, rk[0], "k")
+
+
+def test_prologue_config2(gpu):
+    """S=8192, H=56 strided views of the fused QKV output, theta 10000."""
+    S, H = 8192, 56
+    rng = np.random.default_rng(8192)
+    x, w = _inputs(rng, S, H)
+    rope = oracle.rope_table(S, 128)
+    gq, gk = _run_gpu(x[0], x[1], w, rope, 128, gpu, True)
+    rq, rk = oracle.qk_rmsnorm_rope(x[0][None], x[1][None], rope, w[0], w[1], eps=1e-6, rot_dim=128)
+    _compare(gq, rq[0], "q")
+    _compare(gk, rk[0], "k")
+
+
+def test_prologue_rejects_bad_layout(gpu):
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16, device=gpu)
+    k = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16, device=gpu)
+    w = torch.ones(128, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        h3attn.qk_rmsnorm_rope_(q[..., ::2], k[..., ::2], None, w[:64], w[:64], rot_dim=0)
+    with pytest.raises(ValueError):
+        h3attn.qk_rmsnorm_rope_(q, k, None, w, w, rot_dim=24)

@@ -1,0 +1,126 @@
+"""Parity of the block-sparse kernel (h3a_attn_fwd_blocksparse) and the LUT builder.
+
+Reference: custom_nodes/h3_sla/__init__.py:226-235 (block map + sparse attention;
+skipped key blocks contribute nothing).  The sparse output is compared with dense
+attention masked to the same block map (the oracle), at the BASELINE tolerance.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import h3attn
+import oracle
+from conftest import assert_close_absmax, from_dev_bf16, randn_bf16, to_dev_bf16
+from h3attn import sla
+
+pytestmark = pytest.mark.gpu
+
+
+def _lut_np(bmap, max_k):
+    B, H, nq, nk = bmap.shape
+    lut = np.full((B, H, nq, max_k), -1, np.int32)
+    cnt = np.zeros((B, H, nq), np.int32)
+    for idx in np.ndindex(B, H, nq):
+        nz = np.flatnonzero(bmap[idx])
+        cnt[idx] = len(nz)
+        lut[idx][:len(nz)] = nz
+    return lut, cnt
+
+
+def test_block_map_to_lut(gpu):
+    rng = np.random.default_rng(3)
+    bmap = (rng.random((2, 3, 17, 29)) < 0.3).astype(np.uint8)
+    bmap[0, 0, 0] = 0  # an empty row
+    max_k = int(bmap.sum(-1).max())
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu), max_k)
+    rl, rc = _lut_np(bmap, max_k)
+    assert np.array_equal(cnt.cpu().numpy(), rc)
+    assert np.array_equal(lut.cpu().numpy(), rl)
+
+
+@pytest.mark.parametrize("blk,S,H", [(128, 1000, 2), (64, 1000, 2), (128, 1160, 1), (64, 777, 3)])
+def test_sparse_vs_masked_oracle(gpu, blk, S, H):
+    rng = np.random.default_rng(blk + S)
+    q, k, v = (randn_bf16(rng, (1, H, S, 128)) for _ in range(3))
+    nk = -(-S // blk)
+    bmap = oracle.block_map(q, k, blk, blk, keep=max(1, nk // 4), force_diag=True)
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, blk, blk)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
+    assert_close_absmax(got, ref, what=f"sparse blk={blk}")
+
+
+@pytest.mark.parametrize("blk_k", [64, 128])
+def test_all_blocks_kept_equals_dense(gpu, blk_k):
+    """A full block map visits the key stages in the dense order: bit-identical output."""
+    rng = np.random.default_rng(21)
+    S = 1000
+    q, k, v = (to_dev_bf16(randn_bf16(rng, (1, 2, S, 128)), gpu) for _ in range(3))
+    nq, nk = -(-S // 128), -(-S // blk_k)
+    lut, cnt = h3attn.block_map_to_lut(torch.ones(1, 2, nq, nk, dtype=torch.uint8, device=gpu))
+    o_s = h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, 128, blk_k)
+    o_d = h3attn.attn_fwd(q, k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(o_s, o_d)
+
+
+def test_empty_rows_give_zero(gpu):
+    rng = np.random.default_rng(22)
+    q, k, v = (to_dev_bf16(randn_bf16(rng, (1, 1, 256, 128)), gpu) for _ in range(3))
+    bmap = torch.zeros(1, 1, 2, 2, dtype=torch.uint8, device=gpu)
+    bmap[0, 0, 1, 1] = 1
+    lut, cnt = h3attn.block_map_to_lut(bmap, 1)
+    o = h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, 128, 128)
+    torch.cuda.synchronize()
+    assert torch.all(o[0, 0, :128] == 0)
+    assert torch.all(torch.isfinite(o.float()))
+
+
+def test_gpu_block_map_matches_oracle(gpu):
+    """Torch-on-GPU block map vs the oracle: identical except where scores tie within fp32 noise."""
+    rng = np.random.default_rng(23)
+    S, H, blk = 2000, 2, 128
+    q, k = randn_bf16(rng, (1, H, S, 128)), randn_bf16(rng, (1, H, S, 128))
+    nk = -(-S // blk)
+    keep = sla.keep_count(0.25, nk)
+    ref, scores = oracle.block_map(q, k, blk, blk, keep=keep, force_diag=True, return_scores=True)
+    bmap, lut, cnt = sla.get_block_map(to_dev_bf16(q, gpu), to_dev_bf16(k, gpu), 0.25, blk, blk,
+                                       force_diag=True, smooth_k=False)
+    got = bmap.cpu().numpy()
+    diff = np.argwhere(got != ref)
+    for b, h, i, j in diff:  # any disagreement must sit at the selection threshold
+        row = np.sort(scores[b, h, i])[::-1]
+        thr = row[keep - 1]
+        assert abs(scores[b, h, i, j] - thr) <= 1e-4 * max(1.0, abs(thr))
+    assert np.array_equal(cnt.cpu().numpy(), got.sum(-1))
+
+
+def test_config5_full_shape(gpu):
+    """H=56, S=42120, 128x128 tiles, top 25% + diagonal; checked on 2 heads."""
+    S, H, blk = 42120, 56, 128
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q = torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+    k = torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+    v = torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) * 4
+    bmap, lut, cnt = sla.get_block_map(q, k, 0.25, blk, blk, force_diag=True, smooth_k=False)
+    assert int(cnt.max()) <= 83 and int(cnt.min()) >= 82
+    o = h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk)
+    torch.cuda.synchronize()
+    scale = 1.0 / math.sqrt(128)
+    for h in (0, 55):
+        kt = k[0, h].float().t().contiguous()
+        vf = v[0, h].float()
+        keep = bmap[0, h].bool()  # [nq, nk]
+        for i0 in (0, 20480, 41984):
+            qi = q[0, h, i0:i0 + 128].float()
+            s = (qi @ kt) * scale
+            mask = keep[i0 // blk].repeat_interleave(blk)[:S]
+            s = s.masked_fill(~mask, float("-inf"))
+            ref = torch.softmax(s, -1) @ vf
+            assert_close_absmax(o[0, h, i0:i0 + 128].float().cpu().numpy(), ref.cpu().numpy(),
+                                what=f"h={h} q0={i0}")
