@@ -38,14 +38,14 @@ def _kernel_ready(t: torch.Tensor, outer_dims) -> bool:
 def _as_kernel_input(name: str, t: torch.Tensor) -> torch.Tensor:
     if not isinstance(t, torch.Tensor):
         raise ValueError(f"{name} must be a torch.Tensor")
-    if t.dtype != torch.bfloat16:
-        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
-    if not t.is_cuda:
-        raise ValueError(f"{name} must be a GPU tensor (libh3attn has no CPU path)")
     if t.dim() != 4:
         raise ValueError(f"{name} must be 4-D [B,H,S,D], got shape {tuple(t.shape)}")
     if t.shape[-1] != HEAD_DIM:
         raise ValueError(f"{name}: head_dim {t.shape[-1]} unsupported (only {HEAD_DIM})")
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (libh3attn has no CPU path)")
     # Layouts the kernel cannot stream directly are made contiguous (same HIP path).
     return t if _kernel_ready(t, (0, 1, 2)) else t.contiguous()
 

@@ -1,0 +1,125 @@
+"""The C ABI on the CPU: the library loads, exports every symbol include/h3attn.h
+declares, and rejects bad arguments with error codes before any HIP call (no
+compute calls here: this container has no GPU)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import threading
+
+import pytest
+
+from conftest import ROOT
+from h3attn import _lib
+
+HEADER = os.path.join(ROOT, "include", "h3attn.h")
+S3 = _lib.strides3
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(h3a_\w+)\s*\(", text, re.M)))
+
+
+def test_header_symbols_exported_and_bound():
+    L = _lib.lib()
+    syms = header_symbols()
+    assert len(syms) >= 9
+    for s in syms:
+        assert hasattr(L, s), f"{s} not exported by libh3attn.so"
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(syms)
+
+
+def test_version():
+    assert _lib.version().startswith("h3attn ")
+    assert "gfx950" in _lib.version()
+
+
+def _attn(L, q=16, k=16, v=16, o=16, B=1, H=1, Sq=4, Skv=4, D=128, qs=(0, 0, 0), scale=0.1):
+    z = S3(0, 0, 0)
+    return L.h3a_attn_fwd(q, k, v, o, B, H, Sq, Skv, D, S3(*qs), z, z, z, scale, None)
+
+
+def test_attn_argument_errors():
+    L = _lib.lib()
+    assert _attn(L, q=None) == _lib.H3A_ERR_INVALID_ARG
+    assert b"null" in L.h3a_last_error()
+    assert _attn(L, Sq=0) == _lib.H3A_ERR_INVALID_ARG
+    assert _attn(L, B=-1) == _lib.H3A_ERR_INVALID_ARG
+    assert _attn(L, D=64) == _lib.H3A_ERR_UNSUPPORTED
+    assert b"head_dim 64" in L.h3a_last_error()
+    assert _attn(L, scale=0.0) == _lib.H3A_ERR_INVALID_ARG
+    assert _attn(L, scale=float("nan")) == _lib.H3A_ERR_INVALID_ARG
+    assert _attn(L, q=24) == _lib.H3A_ERR_ALIGNMENT        # 8-byte aligned only
+    assert _attn(L, qs=(0, 0, 12)) == _lib.H3A_ERR_ALIGNMENT  # row stride not a multiple of 8
+    assert _attn(L, qs=(0, -8, 8)) == _lib.H3A_ERR_ALIGNMENT
+
+
+def test_blocksparse_argument_errors():
+    L = _lib.lib()
+    z = S3(0, 0, 0)
+
+    def call(lut=16, counts=16, bq=128, bk=128, maxk=1, Skv=300):
+        return L.h3a_attn_fwd_blocksparse(16, 16, 16, 16, 1, 1, 300, Skv, 128, z, z, z, z, lut, counts,
+                                          bq, bk, maxk, 0.1, None)
+
+    assert call(lut=None) == _lib.H3A_ERR_INVALID_ARG
+    assert call(bq=32) == _lib.H3A_ERR_UNSUPPORTED
+    assert call(bk=256) == _lib.H3A_ERR_UNSUPPORTED
+    assert call(maxk=0) == _lib.H3A_ERR_INVALID_ARG
+    assert call(maxk=4) == _lib.H3A_ERR_INVALID_ARG  # 300 keys = 3 blocks of 128
+    assert b"max_k_blocks" in L.h3a_last_error()
+
+
+def test_lut_and_prologue_argument_errors():
+    L = _lib.lib()
+    assert L.h3a_block_map_to_lut(None, 1, 1, 2, 2, 16, 16, 1, None) == _lib.H3A_ERR_INVALID_ARG
+    assert L.h3a_block_map_to_lut(16, 1, 1, 2, 2, 16, 16, 3, None) == _lib.H3A_ERR_INVALID_ARG
+    z = S3(0, 0, 0)
+
+    def rope(rot=128, ropep=16, D=128, eps=1e-6, qs=(0, 0, 0), rss=64):
+        return L.h3a_qk_rmsnorm_rope(16, 16, 1, 4, 2, D, S3(*qs), z, ropep, 0, rss, rot, 16, 16, eps, None)
+
+    assert rope(D=64) == _lib.H3A_ERR_UNSUPPORTED
+    assert rope(rot=24) == _lib.H3A_ERR_UNSUPPORTED
+    assert rope(rot=144) == _lib.H3A_ERR_UNSUPPORTED
+    assert rope(ropep=None) == _lib.H3A_ERR_INVALID_ARG
+    assert rope(eps=-1.0) == _lib.H3A_ERR_INVALID_ARG
+    assert rope(qs=(0, 3, 0)) == _lib.H3A_ERR_ALIGNMENT
+    assert rope(rss=6) == _lib.H3A_ERR_ALIGNMENT
+    assert L.h3a_kernel_attrs(0, None) == _lib.H3A_ERR_INVALID_ARG
+    out = (ctypes.c_double * 6)()
+    assert L.h3a_kernel_attrs(99, out) == _lib.H3A_ERR_INVALID_ARG
+    assert L.h3a_test_qk(None, 16, 16, None) == _lib.H3A_ERR_INVALID_ARG
+    assert L.h3a_test_pv(16, 24, 16, None) == _lib.H3A_ERR_ALIGNMENT
+
+
+def test_last_error_is_thread_local_and_cleared():
+    L = _lib.lib()
+    assert _attn(L, D=64) == _lib.H3A_ERR_UNSUPPORTED
+    seen = {}
+
+    def other():
+        seen["before"] = L.h3a_last_error()
+        _attn(L, q=None)
+        seen["after"] = L.h3a_last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["before"] == b""
+    assert b"null" in seen["after"]
+    assert b"head_dim" in L.h3a_last_error()  # this thread's message is untouched
+    L.h3a_block_map_to_lut(None, 1, 1, 1, 1, 16, 16, 1, None)
+    assert b"null" in L.h3a_last_error()
+
+
+def test_python_check_raises_typed_errors():
+    L = _lib.lib()
+    rc = _attn(L, D=64)
+    with pytest.raises(ValueError):
+        _lib.check("h3a_attn_fwd", rc)
+    with pytest.raises(_lib.H3AError):
+        _lib.check("h3a_attn_fwd", _lib.H3A_ERR_HIP)

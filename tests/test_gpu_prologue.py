@@ -28,11 +28,22 @@ def _inputs(rng, S, H, spread=True):
 
 
 def _compare(got_bits, ref_bits, what):
+    """Kernel (fp32 math) vs oracle (fp64 math), both rounded once to bf16.
+
+    Allowed per value: one bf16 ulp of the result (<= 2^-7 |r|) plus the fp32
+    error of the rotation before rounding, ~1e-6 * (|y_i| + |y_{i+rot/2}|)
+    with |y| <= ~8 here, taken as an absolute 1e-5.  The second term only
+    matters where the rotation cancels to a value near zero.
+    """
     g = oracle.bf16_to_f32(got_bits).reshape(got_bits.shape).astype(np.float64)
     r = oracle.bf16_to_f32(ref_bits).reshape(ref_bits.shape).astype(np.float64)
     exact = np.mean(got_bits == ref_bits)
-    ulp = np.maximum(np.abs(r) * 2.0 ** -7, 1e-30)  # one bf16 ulp is <= 2^-7 |r|
-    assert np.all(np.abs(g - r) <= ulp), f"{what}: a value differs by more than one bf16 ulp"
+    tol = np.abs(r) * 2.0 ** -7 + 1e-5
+    bad = np.abs(g - r) > tol
+    if bad.any():
+        i = np.unravel_index(np.argmax(np.abs(g - r) - tol), r.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} values off by more than 1 ulp + 1e-5; "
+                             f"worst at {i}: got {g[i]!r} want {r[i]!r}")
     assert exact >= 0.99, f"{what}: only {exact:.4f} bit-exact"
 
 

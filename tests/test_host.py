@@ -1,0 +1,195 @@
+"""Host-side logic on the CPU: the attn_sm80 drop-in shim, argument validation of
+the tensor ops, the h3_sla schedule mirror, and the hook plumbing on a stand-in
+DiT attention module (with torch callables injected in place of the kernels)."""
+from __future__ import annotations
+
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import attn_sm80
+import h3attn
+import oracle
+import standin_dit
+from conftest import ROOT
+from h3attn import hooks, sla
+
+
+# ----------------------------------------------------------------------------- attn_sm80 shim
+def test_shim_backends_and_errors():
+    """attn(q,k,v,backend) dispatch (attn_sm80/attn_sm80.py:37-42): unknown name -> ValueError(name)."""
+    q = k = v = torch.randn(1, 2, 16, 128)
+    with pytest.raises(ValueError, match="nope"):
+        attn_sm80.attn(q, k, v, backend="nope")
+    o = attn_sm80.attn(q, k, v, backend="sdpa")
+    assert torch.allclose(o, torch.nn.functional.scaled_dot_product_attention(q, k, v))
+    # the HIP backends refuse CPU tensors instead of computing on the CPU
+    for name in ("hip", "fa3_sm80_h3", "fa3_pp"):
+        with pytest.raises(ValueError, match="GPU"):
+            attn_sm80.attn(q.bfloat16(), k.bfloat16(), v.bfloat16(), backend=name)
+
+
+def test_shim_build_exposes_reference_extension_names():
+    ext = attn_sm80._build()
+    for name in ("fa3", "fa3_pp", "kernel_attrs", "pp_attrs", "get_prof", "reset_prof", "test_qk", "test_pv"):
+        assert callable(getattr(ext, name))
+    assert attn_sm80._build() is ext
+    assert torch.equal(ext.get_prof(), torch.zeros(5, dtype=torch.float64))
+
+
+def test_ops_validate_before_any_gpu_call():
+    q = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        h3attn.attn_fwd(q, q, q)
+    with pytest.raises(ValueError, match="bfloat16"):
+        h3attn.attn_fwd(q.float(), q.float(), q.float())
+    with pytest.raises(ValueError, match="head_dim"):
+        h3attn.attn_fwd(q[..., :64], q[..., :64], q[..., :64])
+    with pytest.raises(ValueError, match="4-D"):
+        h3attn.attn_fwd(q[0], q[0], q[0])
+    with pytest.raises(ValueError):
+        h3attn.qk_rmsnorm_rope_(q, q, None, torch.ones(128), torch.ones(128), rot_dim=0)
+
+
+def test_rope_table_layout():
+    t = h3attn.rope_freqs(10, 64)
+    assert tuple(t.shape) == (1, 10, 1, 32, 2, 2) and t.dtype == torch.float32
+    assert np.allclose(t[0, :, 0].numpy(), oracle.rope_table(10, 64), atol=1e-7)
+    assert torch.allclose(t[0, 3, 0, 2], torch.tensor([[t[0, 3, 0, 2, 0, 0], -t[0, 3, 0, 2, 1, 0]],
+                                                      [t[0, 3, 0, 2, 1, 0], t[0, 3, 0, 2, 0, 0]]]))
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, f"{ROOT}/bench.py", "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode == 2
+    assert "one MI355X" in r.stderr
+
+
+# ----------------------------------------------------------------------------- h3_sla schedule
+def test_schedule_parsing():
+    assert sla.parse_ranges("31-42,46,48-49") == list(range(31, 43)) + [46, 48, 49]
+    assert sla.parse_ranges("") == []
+    m = sla.parse_layer_keep("25:31-33;0.2:43; ")
+    assert m == {31: 0.25, 32: 0.25, 33: 0.25, 43: 0.2}
+
+
+def test_resolve_schedule_presets():
+    name, keeps = sla.resolve_schedule("off", topk=0.35)
+    assert name == "off" and keeps == [0.35] * 50
+    name, keeps = sla.resolve_schedule("quality")
+    assert [l for l, k in enumerate(keeps) if k == 0.25] == list(range(31, 43)) + [46, 47, 48, 49]
+    assert all(k == 0.15 for l, k in enumerate(keeps) if not (31 <= l <= 42 or 46 <= l <= 49))
+    assert sla.resolve_schedule("speed")[1].count(0.25) == 9
+    assert sla.resolve_schedule("balanced")[1].count(0.25) == 14
+    name, keeps = sla.resolve_schedule("custom", topk=0.3, layer_keep="25:0-1;99:60")
+    assert keeps[:3] == [0.25, 0.25, 0.3] and len(keeps) == 50
+    with pytest.raises(ValueError):
+        sla.resolve_schedule("fastest")
+
+
+def test_keep_count():
+    assert sla.keep_count(0.25, 330) == 82
+    assert sla.keep_count(0.01, 10) == 1
+    assert sla.keep_count(1.0, 7) == 7
+
+
+# ----------------------------------------------------------------------------- hooks (CPU plumbing)
+def _cpu_attention(q, k, v, heads, mask=None, skip_reshape=True, **_):
+    return standin_dit._attention_impl(q, k, v, heads, skip_reshape=skip_reshape)
+
+
+def _model(seed=0):
+    torch.manual_seed(seed)
+    m = standin_dit.Attention(256, 2)
+    with torch.no_grad():
+        m.q_norm.weight.mul_(1.1)
+        m.k_norm.weight.mul_(0.9)
+    return m
+
+
+class _Attn(standin_dit.Attention):
+    """Subclass so patching the class attribute does not leak into other tests."""
+
+
+def test_install_patch_matches_stock_forward_and_is_idempotent():
+    m = _model()
+    m.__class__ = _Attn
+    x = torch.randn(10, 256)
+    rope = h3attn.rope_freqs(10, 128)
+    with torch.no_grad():
+        want = m(x, rope_freqs=rope)
+        want_norope = m(x)
+        assert hooks.install(_Attn, prologue=standin_dit.rms_rope_split_half_, attention=_cpu_attention)
+        assert not hooks.install(_Attn, prologue=standin_dit.rms_rope_split_half_, attention=_cpu_attention)
+        got = m(x, rope_freqs=rope)
+        got_norope = m(x)  # rope_freqs=None falls through to the original forward
+        assert hooks.uninstall(_Attn) and not hooks.uninstall(_Attn)
+    assert torch.equal(got, want)
+    assert torch.equal(got_norope, want_norope)
+
+
+def test_override_gate_and_fallback():
+    calls = []
+
+    def func(*a, **kw):
+        calls.append("func")
+        return "dense"
+
+    def boom(*a, **kw):
+        raise RuntimeError("kernel unavailable")
+
+    logs = []
+    ov = hooks.make_override(attention=lambda *a, **kw: "fast", log=logs.append)
+    q4 = torch.zeros(1, 2, 4, 128)
+    assert ov(func, q4, q4, q4, 2, mask=None, skip_reshape=True) == "fast"
+    assert ov(func, q4, q4, q4, 2, mask=torch.ones(1), skip_reshape=True) == "dense"      # masked call
+    assert ov(func, q4[..., :64], q4[..., :64], q4[..., :64], 2, skip_reshape=True) == "dense"  # D != 128
+    assert ov(func, q4[0], q4[0], q4[0], 2, skip_reshape=False) == "dense"               # 3-D
+    ov2 = hooks.make_override(attention=boom, log=logs.append)
+    assert ov2(func, q4, q4, q4, 2, mask=None, skip_reshape=True) == "dense"
+    assert any("kernel unavailable" in s for s in logs)
+    assert ov.h3sla is None
+
+
+def test_sla_override_scope_schedule_and_fallback():
+    class _A(standin_dit.Attention):
+        pass
+
+    hooks.install_scope_patch(_A)
+    f1 = _A.forward
+    hooks.install_scope_patch(_A)  # idempotent
+    assert _A.forward is f1
+    seen = {}
+
+    def func(q, k, v, heads, **kw):
+        seen["in_scope"] = hooks.in_dit_scope()
+        return standin_dit._attention_impl(q, k, v, heads, **kw)
+
+    sched = hooks.Schedule("custom", [1.0] * 50, blk=64)
+    logs = []
+    ov = hooks.make_sla_override(schedule=sched, log=logs.append)
+    assert ov.h3sla is sched
+    assert hooks.get_schedule({"optimized_attention_override": ov}) is sched
+    assert hooks.get_schedule({}) is None
+    torch.manual_seed(1)
+    m = _A(256, 2)
+    m._h3sla_layer = 3
+    x = torch.randn(12, 256)
+    opts = {"optimized_attention_override": lambda fn, *a, **kw: ov(func, *a, **kw)}
+    with torch.no_grad():
+        m(x, rope_freqs=h3attn.rope_freqs(12, 128), transformer_options=opts)
+    assert seen["in_scope"] is True and not hooks.in_dit_scope()
+    # keep < 1 on CPU tensors: the sparse kernel refuses them -> logged fallback to dense
+    sched.keeps[3] = 0.25
+    with torch.no_grad():
+        m(x, rope_freqs=h3attn.rope_freqs(12, 128), transformer_options=opts)
+    assert any("fell back" in s for s in logs)
+    # outside DiT scope (rope_freqs=None): the override passes straight to func
+    logs.clear()
+    with torch.no_grad():
+        m(x, transformer_options=opts)
+    assert logs == [] and seen["in_scope"] is False
+    assert sched.keep_for(None) == sched.default_keep and sched.keep_for(99) == sched.default_keep
