@@ -80,6 +80,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the timed region, run one device copy of this many MiB "
+                         "(reference kernel for scaling FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
@@ -126,6 +129,14 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
+    if args.calib_copy_mib > 0:
+        src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     kern_ms = [a.elapsed_time(b) for st in evs for a, b in st]
     avg_kernel_ms = sum(kern_ms) / len(kern_ms)
     ms_per_step = wall * 1e3 / args.steps
@@ -153,7 +164,7 @@ def main():
         "ms_per_layer": round(avg_kernel_ms, 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": "attn_fwd_kernel<4,false>",
+                     "traffic": None, "kernel": "attn_fwd_kernel<8,false>",
                      "flop_per_launch": flops_per_layer(),
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     }

@@ -27,6 +27,9 @@ ARCH = "gfx950"
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # No kernel relies on NaN semantics; without this, every fmaxf is preceded
+    # by a NaN-canonicalising v_max_f32 in IEEE mode.
+    "-fno-honor-nans",
     "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
@@ -52,26 +55,31 @@ def _run(cmd, verbose):
     return r
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, defines=(), out: str | None = None) -> str:
+    """Compile and link; `defines` are extra -D tuning knobs, `out` an alternative .so path."""
     hipcc = _hipcc()
-    os.makedirs(BUILD_DIR, exist_ok=True)
+    tag = "_".join(d.replace("=", "") for d in defines)
+    bdir = os.path.join(BUILD_DIR, tag) if tag else BUILD_DIR
+    os.makedirs(bdir, exist_ok=True)
     srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
     objs = []
     cmds = []
     for s in srcs:
-        obj = os.path.join(BUILD_DIR, s[:-4] + ".o")
+        obj = os.path.join(bdir, s[:-4] + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *CFLAGS, "-c", os.path.join(CSRC, s), "-o", obj])
+        cmds.append([hipcc, *CFLAGS, *[f"-D{d}" for d in defines], "-c", os.path.join(CSRC, s), "-o", obj])
     workers = min(len(cmds), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
-    tmp = os.path.join(OUT_DIR, LIB_NAME + ".tmp")
+    final = out or os.path.join(OUT_DIR, LIB_NAME)
+    tmp = final + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
-    final = os.path.join(OUT_DIR, LIB_NAME)
     os.replace(tmp, final)
     return final
 
 
 if __name__ == "__main__":
-    path = build(verbose="--verbose" in sys.argv)
-    print(path)
+    args = sys.argv[1:]
+    defs = [a[2:] for a in args if a.startswith("-D")]
+    outp = next((a.split("=", 1)[1] for a in args if a.startswith("--out=")), None)
+    print(build(verbose="--verbose" in args, defines=defs, out=outp))

@@ -89,13 +89,8 @@ int h3a_attn_fwd(const void *q, const void *k, const void *v, void *o, int B, in
   clear_error();
   int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
   if (rc) return rc;
-  const int64_t nqt = (Sq + 127) / 128;
-  const int64_t total = (int64_t)B * H * nqt;
-  if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
   AttnArgs a;
   fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
-  a.nqt = (int)nqt;
-  a.total = (int)total;
   return launch_attn_dense(a, as_stream(stream));
 }
 

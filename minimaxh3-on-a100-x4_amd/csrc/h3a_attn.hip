@@ -12,100 +12,95 @@
 //    32 query rows as the B operand of v_mfma_f32_32x32x16_bf16 in VGPRs.
 //  * The score tile is produced transposed, S^T = K Q^T, so every lane owns a
 //    single query row (column l%32) and 32 of the 64 keys of a stage.  Row
-//    max is an in-register reduction plus one v_permlane32_swap with the
+//    max is an in-register v_max3 chain plus one v_permlane32_swap with the
 //    partner lane; the row sum needs no cross-lane traffic until the end.
-//  * That layout is already the B operand of O^T += V^T P^T: the P tile goes
-//    from the score accumulators straight into the PV MFMA (no LDS round
-//    trip).  V is staged transposed in LDS with keys ordered to match the
-//    score accumulator's key order (see vt_pos).
+//  * That layout is already the B operand of O^T += V^T P^T: P goes from the
+//    score accumulators straight into the PV MFMA (no LDS round trip).  V
+//    stays row-major in LDS and its A operand is read with ds_read_b64_tr_b16
+//    (LDS transpose reads), addressed so that the key order matches the
+//    score accumulator's.
 //  * K/V stages of 64 keys are double-buffered in LDS; the next stage is
-//    fetched with 128-bit global loads into registers while the current one
-//    is consumed, so one barrier per stage suffices.
-//  * exp2-based softmax with scale*log2(e) folded into one FMA.
+//    fetched with 128-bit buffer loads into registers while the current one
+//    is consumed (one barrier per stage).  The buffer resource is rebased per
+//    stage so rows past Skv read as zeros and offsets are loop-invariant; the
+//    loop is unrolled by two so every LDS address is a base + immediate.
+//  * exp2-based softmax with scale*log2(e) folded into one FMA; the running
+//    max is refreshed only when a row outgrows it by 2^8 (lazy rescale).
 //  * Workgroup ids are remapped XCD-aware (xcd_remap).
+#include <climits>
+#include <type_traits>
+
 #include "h3a_device.h"
 #include "h3a_internal.h"
 
 namespace h3a {
 
+#ifndef H3A_LAZY_RESCALE
+#define H3A_LAZY_RESCALE 1
+#endif
+#ifndef H3A_XCD_REMAP
+#define H3A_XCD_REMAP 1
+#endif
+// Waves (32 query rows each) per dense workgroup.
+#ifndef H3A_DENSE_WAVES
+#define H3A_DENSE_WAVES 8
+#endif
+// Row sum from the bf16-rounded P (v_dot2, 16 ops) instead of the unrounded
+// p (32 adds).  Off by default: the reference sums unrounded p.
+#ifndef H3A_ROWSUM_BF16
+#define H3A_ROWSUM_BF16 0
+#endif
+
 constexpr int kD = 128;
-constexpr int kBN = 64;             // keys per pipeline stage
-constexpr int kKStride = kD + 8;    // K stage row stride in LDS (elements), padded
-constexpr int kVtStride = kBN;      // V^T stage row stride (elements), chunk-swizzled
+constexpr int kBN = 64;               // keys per pipeline stage
+constexpr float kRescaleSlack = 8.f;  // log2 headroom before the running max is refreshed
+// LDS row strides (elements).  K rows of 272 B: 128-bit reads by 16
+// consecutive rows hit distinct banks.  V rows of 320 B: the 4 rows x 64 bytes
+// gathered by each 32-lane half of a transpose read land on distinct banks.
+constexpr int kKStride = kD + 8;
+constexpr int kVStride = kD + 32;
+constexpr int kKTile = kBN * kKStride;
+constexpr int kVTile = kBN * kVStride;
 
-// ---------------------------------------------------------------------------
-// V^T stage layout.  For the PV product the k-slot (g = lane/32, e = 0..7)
-// of 16-key step ks carries key 16*ks + 8*(e/4) + 4*g + e%4 (the order in
-// which the S^T accumulator holds keys).  Storing key k of a stage at
-// position vt_pos(k) (bits 2 and 3 swapped) makes the 8 keys one lane needs
-// contiguous: positions 16*ks + 8*g .. +7.
-__device__ __forceinline__ int vt_pos(int key) {
-  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
-}
-// 16-byte chunk swizzle of a V^T row: conflict-free 128-bit reads by 8
-// consecutive rows and 64-bit transposing writes by rows 8 apart.
-__device__ __forceinline__ int vt_swz(int d) { return (d + (d >> 3)) & 7; }
-__device__ __forceinline__ int vt_off(int d, int pos) {
-  return d * kVtStride + ((((pos >> 3) ^ vt_swz(d)) << 3) | (pos & 7));
-}
-
-// One 64-key K/V stage moving HBM -> registers -> LDS.
+// 64-key K and V stages moving HBM -> registers -> LDS (both row-major).  K
+// runs one stage ahead of V, so the two halves are loaded and stored apart.
 template <int NT>
 struct KvStage {
-  static constexpr int KL = (kBN * kD / 8) / NT;         // 16-byte K chunks per thread
-  static constexpr int VL = (kBN / 4) * (kD / 8) / NT;   // (4-key, 8-dim) V blocks per thread
-  static_assert(KL * NT == kBN * kD / 8, "K stage must split evenly");
-  static_assert(VL * NT == (kBN / 4) * (kD / 8), "V stage must split evenly");
-  u32x4 kr[KL];
-  u32x4 vr[VL][4];
+  static constexpr int L = (kBN * kD / 8) / NT;  // 16-byte chunks of K (and of V) per thread
+  static_assert(L * NT == kBN * kD / 8, "stage must split evenly");
+  u32x4 kr[L];
+  u32x4 vr[L];
 
-  // Rows >= Skv (or < 0) load as zeros so masked keys never carry NaN/Inf.
-  __device__ __forceinline__ void load(const uint16_t *Kb, int64_t kss, const uint16_t *Vb,
-                                       int64_t vss, int key0, int Skv, int tid) {
+  // Buffer loads against a resource rebased on the stage's first key whose
+  // range covers exactly the stage's valid rows: rows >= Skv come back as
+  // zeros from the hardware (masked keys never carry NaN/Inf), there is no
+  // predication, and the per-thread byte offsets are loop-invariant.
+  __device__ __forceinline__ static void load_rows(u32x4 (&r)[L], const uint16_t *base, int64_t ss,
+                                                   int key0, int Skv, int tid) {
+    const int rows = Skv - key0 >= kBN ? kBN : (Skv > key0 ? Skv - key0 : 0);
+    const __amdgpu_buffer_rsrc_t res = stage_rsrc(base + (int64_t)key0 * ss, ss, rows);
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int idx = tid + i * NT, row = idx >> 4, ch = idx & 15, key = key0 + row;
-      kr[i] = (key >= 0 && key < Skv) ? *(const u32x4 *)(Kb + (int64_t)key * kss + ch * 8)
-                                      : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int idx = tid + i * NT, kq = idx >> 4, dc = idx & 15;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = key0 + 4 * kq + r;
-        vr[i][r] = (key >= 0 && key < Skv) ? *(const u32x4 *)(Vb + (int64_t)key * vss + dc * 8)
-                                           : u32x4{0, 0, 0, 0};
-      }
-    }
-  }
-
-  __device__ __forceinline__ void store(uint16_t *sK, uint16_t *sVt, int tid) const {
-#pragma unroll
-    for (int i = 0; i < KL; ++i) {
+    for (int i = 0; i < L; ++i) {
       const int idx = tid + i * NT, row = idx >> 4, ch = idx & 15;
-      *(u32x4 *)(sK + row * kKStride + ch * 8) = kr[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int idx = tid + i * NT, kq = idx >> 4, dc = idx & 15;
-      const int pos0 = vt_pos(4 * kq);  // 4 consecutive keys stay consecutive
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int w = j >> 1;
-        const uint32_t a0 = vr[i][0][w], a1 = vr[i][1][w], a2 = vr[i][2][w], a3 = vr[i][3][w];
-        u32x2 val;
-        if (j & 1) {
-          val.x = (a0 >> 16) | (a1 & 0xffff0000u);
-          val.y = (a2 >> 16) | (a3 & 0xffff0000u);
-        } else {
-          val.x = (a0 & 0xffffu) | (a1 << 16);
-          val.y = (a2 & 0xffffu) | (a3 << 16);
-        }
-        *(u32x2 *)(sVt + vt_off(dc * 8 + j, pos0)) = val;
-      }
+      r[i] = buffer_load_b128(res, (uint32_t)((row * ss + ch * 8) * 2));
     }
   }
+  template <int kStride>
+  __device__ __forceinline__ static void store_rows(const u32x4 (&r)[L], uint16_t *dst, int tid) {
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      const int idx = tid + i * NT, row = idx >> 4, ch = idx & 15;
+      *(u32x4 *)(dst + row * kStride + ch * 8) = r[i];
+    }
+  }
+  __device__ __forceinline__ void load_k(const uint16_t *Kb, int64_t kss, int key0, int Skv, int tid) {
+    load_rows(kr, Kb, kss, key0, Skv, tid);
+  }
+  __device__ __forceinline__ void load_v(const uint16_t *Vb, int64_t vss, int key0, int Skv, int tid) {
+    load_rows(vr, Vb, vss, key0, Skv, tid);
+  }
+  __device__ __forceinline__ void store_k(uint16_t *dst, int tid) const { store_rows<kKStride>(kr, dst, tid); }
+  __device__ __forceinline__ void store_v(uint16_t *dst, int tid) const { store_rows<kVStride>(vr, dst, tid); }
 };
 
 // S^T (64 keys x 32 queries of this wave) = K_stage Q^T.  s0: keys 0-31, s1: 32-63.
@@ -125,6 +120,7 @@ __device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&q
 }
 
 // P^T fragments for the 4 sixteen-key steps, straight from the S^T registers.
+// Step ks, k-slot (g = lane/32, e) carries key 16*ks + 8*(e/4) + 4*g + e%4.
 __device__ __forceinline__ void pack_p(const f32x16 &s0, const f32x16 &s1, u32x4 (&pf)[4]) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -135,16 +131,47 @@ __device__ __forceinline__ void pack_p(const f32x16 &s0, const f32x16 &s1, u32x4
   }
 }
 
+// Per-lane base of the V transpose reads.  Within each 16-lane group a
+// ds_read_b64_tr_b16 gives lane j element j%4 of the 4 consecutive bf16 that
+// lanes 4k + j/4 address (k = 0..3).  Lane i of group t points at row
+// 4*(t/2) + i/4 (+16*ks, +8 for k-slots 4..7) and columns 16*(t%2) + 4*(i%4)
+// (+32*dt), so lane l receives V[key][32*dt + l%32] for the 4 keys of its
+// k-slots, in the score accumulator's key order.
+__device__ __forceinline__ int v_tr_base(int lane) {
+  return (4 * (lane >> 5) + ((lane & 15) >> 2)) * kVStride + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+}
+
 // O^T (128 dims x 32 queries) += V^T_stage P^T.
-__device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[4], int l32, int g,
+__device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[4], int vbase,
                                         f32x16 (&o)[4]) {
+  const uint16_t *b = vbuf + vbase;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const u32x4 av = *(const u32x4 *)(vbuf + vt_off(dt * 32 + l32, ks * 16 + 8 * g));
-      o[dt] = mfma_32x32x16(av, pf[ks], o[dt]);
+      const u32x2 lo = lds_read_tr16_b64(b + (16 * ks) * kVStride + 32 * dt);
+      const u32x2 hi = lds_read_tr16_b64(b + (16 * ks + 8) * kVStride + 32 * dt);
+      o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[ks], o[dt]);
     }
+  }
+}
+
+// Row max of a masked score tile (both 32-key halves, both lane halves), in
+// scale*log2(e) units.
+__device__ __forceinline__ float tile_max(const f32x16 &s0, const f32x16 &s1, float sl2) {
+  float mx = kNegInf;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mx = fmaxf(fmaxf(mx, s0[r]), s1[r]);
+  return half_swap_max(mx) * sl2;
+}
+
+// Keys >= Skv of the stage starting at key0 -> -inf (tail stage only).
+__device__ __forceinline__ void mask_tail(f32x16 &s0, f32x16 &s1, int key0, int Skv, int g) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int kk = key0 + 8 * (r >> 2) + 4 * g + (r & 3);
+    if (kk >= Skv) s0[r] = kNegInf;
+    if (kk + 32 >= Skv) s1[r] = kNegInf;
   }
 }
 
@@ -153,13 +180,17 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 attn_fwd_kernel(AttnArgs a) {
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kBN * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][kD * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kKTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kVTile];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
 
+#if H3A_XCD_REMAP
   const int w = xcd_remap(blockIdx.x, a.total);
+#else
+  const int w = blockIdx.x;
+#endif
   const int qt = w % a.nqt, bh = w / a.nqt;
   const int h = bh % a.H, b = bh / a.H;
 
@@ -178,9 +209,10 @@ attn_fwd_kernel(AttnArgs a) {
   } else {
     niter = (a.Skv + kBN - 1) / kBN;
   }
-  // First key of stage j.  A LUT entry outside the key range maps to Skv:
-  // the stage then loads nothing and is fully masked.
+  // First key of stage j.  Prefetches past the last stage and LUT entries
+  // outside the key range map to Skv: such a stage loads nothing (zeros).
   auto key_base = [&](int j) -> int {
+    if (j >= niter) return a.Skv;
     if constexpr (kSparse) {
       const int kb = lut_row[j / a.sub];
       const int key0 = kb * a.blk_k + (j % a.sub) * kBN;
@@ -191,6 +223,17 @@ attn_fwd_kernel(AttnArgs a) {
   };
 
   const int qrow = qt * BM + wave * 32 + l32;
+  if (niter == 0) {
+    // No key block to attend to (block-sparse row with an empty LUT): O = 0.
+    // Leaving before any load also keeps every path into the stage loop free
+    // of outstanding loads, so the loop needs no waits on the Q fragments.
+    if (qrow < a.Sq) {
+      uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
+    }
+    return;
+  }
   u32x4 qf[8];
   if (qrow < a.Sq) {
     const uint16_t *p = Qb + (int64_t)qrow * a.qss + 8 * g;
@@ -206,57 +249,86 @@ attn_fwd_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
+  const int vbase = v_tr_base(lane);
 
+  // Software pipeline: K runs one stage ahead of V.  Entering stage j, LDS
+  // holds V(j) in vbuf[j&1] and K(j+1) in kbuf[(j+1)&1], and the registers
+  // hold the masked scores S(j).  Stage j computes S(j+1) = K(j+1) Q^T while
+  // the softmax of S(j) runs (independent work the scheduler interleaves),
+  // then O += V(j) P(j), and parks the prefetched K(j+2) and V(j+1).
   KvStage<NT> st;
-  if (niter > 0) {
-    st.load(Kb, a.kss, Vb, a.vss, key_base(0), a.Skv, tid);
-    st.store(sK[0], sVt[0], tid);
-  }
+  st.load_k(Kb, a.kss, key_base(0), a.Skv, tid);
+  st.load_v(Vb, a.vss, key_base(0), a.Skv, tid);
+  st.store_k(kbuf[0], tid);
+  st.store_v(vbuf[0], tid);
+  __syncthreads();
+  st.load_k(Kb, a.kss, key_base(1), a.Skv, tid);
+  f32x16 s0, s1;
+  score_tile(kbuf[0], qf, l32, g, s0, s1);
+  if (key_base(0) + kBN > a.Skv) mask_tail(s0, s1, key_base(0), a.Skv, g);
+  st.store_k(kbuf[1], tid);
   __syncthreads();
 
-  for (int j = 0; j < niter; ++j) {
-    const int buf = j & 1;
-    const int key0 = key_base(j);
-    if (j + 1 < niter) st.load(Kb, a.kss, Vb, a.vss, key_base(j + 1), a.Skv, tid);
+  auto stage = [&](auto parity, int j) {
+    constexpr int P = decltype(parity)::value;  // j & 1
+    st.load_k(Kb, a.kss, key_base(j + 2), a.Skv, tid);
+    st.load_v(Vb, a.vss, key_base(j + 1), a.Skv, tid);
 
-    f32x16 s0, s1;
-    score_tile(sK[buf], qf, l32, g, s0, s1);
-
-    if (key0 + kBN > a.Skv) {
+    const float mx = tile_max(s0, s1, a.sl2);
+#if H3A_LAZY_RESCALE
+    // The reference max only has to bound the exponents: keep the stale max
+    // while this stage's row max exceeds it by at most kRescaleSlack (p stays
+    // <= 2^kRescaleSlack, exact in the fp32 sums and bf16-rounded like any p),
+    // and rescale O and l only when some row of the wave outgrows it.
+    if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0) {
+#else
+    {
+#endif
+      const float mnew = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - ((mnew == kNegInf) ? 0.f : mnew));
+      m = mnew;
+      lsum *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kk = key0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (kk >= a.Skv) s0[r] = kNegInf;
-        if (kk + 32 >= a.Skv) s1[r] = kNegInf;
-      }
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
     }
+    const float muse = (m == kNegInf) ? 0.f : m;
 
-    float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-    mx = half_swap_max(mx);
-    const float mnew = fmaxf(m, mx * a.sl2);
-    const float muse = (mnew == kNegInf) ? 0.f : mnew;
-    const float alpha = fast_exp2(m - muse);
-    m = mnew;
-
-    float rs = 0.f;
+    // S(j+1) on the MFMA pipe, softmax(j) on the VALU: no dependence between them.
+    f32x16 n0, n1;
+    score_tile(kbuf[P ^ 1], qf, l32, g, n0, n1);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       s0[r] = fast_exp2(fmaf(s0[r], a.sl2, -muse));
       s1[r] = fast_exp2(fmaf(s1[r], a.sl2, -muse));
-      rs += s0[r] + s1[r];
     }
-    lsum = fmaf(lsum, alpha, rs);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-
     u32x4 pf[4];
     pack_p(s0, s1, pf);
-    pv_tile(sVt[buf], pf, l32, g, o);
+#if H3A_ROWSUM_BF16
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) lsum = dot2_bf16_ones(pf[ks][c], lsum);
+#else
+    float rs = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
+    lsum += rs;
+#endif
+    pv_tile(vbuf[P], pf, vbase, o);
 
-    if (j + 1 < niter) st.store(sK[buf ^ 1], sVt[buf ^ 1], tid);
+    const int knext = key_base(j + 1);
+    if (knext + kBN > a.Skv) mask_tail(n0, n1, knext, a.Skv, g);
+    s0 = n0;
+    s1 = n1;
+
+    st.store_k(kbuf[P], tid);
+    st.store_v(vbuf[P ^ 1], tid);
     __syncthreads();
+  };
+
+  for (int j = 0; j < niter; j += 2) {
+    stage(std::integral_constant<int, 0>{}, j);
+    if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
   }
 
   const float ltot = half_swap_sum(lsum);
@@ -278,18 +350,17 @@ attn_fwd_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Fragment tests: one wave, the same staging and fragment code as above.
 __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const uint16_t *K, float *S) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kBN * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[kD * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t kb[kKTile];
   const int tid = threadIdx.x, g = tid >> 5, l32 = tid & 31;
   KvStage<64> st;
-  st.load(K, kD, K, kD, 0, kBN, tid);
-  st.store(sK, sVt, tid);
+  st.load_k(K, kD, 0, kBN, tid);
+  st.store_k(kb, tid);
   __syncthreads();
   u32x4 qf[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const u32x4 *)(Q + l32 * kD + ks * 16 + 8 * g);
   f32x16 s0, s1;
-  score_tile(sK, qf, l32, g, s0, s1);
+  score_tile(kb, qf, l32, g, s0, s1);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = 8 * (r >> 2) + 4 * g + (r & 3);
@@ -299,12 +370,11 @@ __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const ui
 }
 
 __global__ void __launch_bounds__(64) test_pv_kernel(const uint16_t *P, const uint16_t *V, float *O) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kBN * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[kD * kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vb[kVTile];
   const int tid = threadIdx.x, g = tid >> 5, l32 = tid & 31;
   KvStage<64> st;
-  st.load(V, kD, V, kD, 0, kBN, tid);
-  st.store(sK, sVt, tid);
+  st.load_v(V, kD, 0, kBN, tid);
+  st.store_v(vb, tid);
   __syncthreads();
   // Place P[q][key] where the score accumulators would hold it.
   f32x16 s0, s1;
@@ -319,7 +389,7 @@ __global__ void __launch_bounds__(64) test_pv_kernel(const uint16_t *P, const ui
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
-  pv_tile(sVt, pf, l32, g, o);
+  pv_tile(vb, pf, v_tr_base(tid), o);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -348,8 +418,13 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 }
 
 // ---------------------------------------------------------------------------
-int launch_attn_dense(const AttnArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((attn_fwd_kernel<4, false>), dim3(a.total), dim3(256), 0, s, a);
+int launch_attn_dense(AttnArgs a, hipStream_t s) {
+  constexpr int NW = H3A_DENSE_WAVES;
+  a.nqt = (a.Sq + 32 * NW - 1) / (32 * NW);
+  const int64_t total = (int64_t)a.B * a.H * a.nqt;
+  if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
+  a.total = (int)total;
+  hipLaunchKernelGGL((attn_fwd_kernel<NW, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
   return check_launch("attn_fwd_kernel<dense>");
 }
 
@@ -404,7 +479,8 @@ static int fill_attrs(const void *fn, int threads, double out[6]) {
 int attn_kernel_attrs(int which, double out[6]) {
   switch (which) {
     case H3A_KERNEL_ATTN_DENSE:
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, false>), 256, out);
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<H3A_DENSE_WAVES, false>),
+                        64 * H3A_DENSE_WAVES, out);
     case H3A_KERNEL_ATTN_SPARSE_128:
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, true>), 256, out);
     case H3A_KERNEL_ATTN_SPARSE_64:

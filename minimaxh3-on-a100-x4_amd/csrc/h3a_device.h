@@ -49,6 +49,37 @@ __device__ __forceinline__ float half_swap_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer resource (V#) over `rows` rows of `stride` elements, each row
+// holding 128 bf16: num_records is the exact byte extent, so any access past
+// the last valid row returns zeros.  Word 3 is the gfx9-family default config.
+constexpr int kBufferConfig = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stage_rsrc(const uint16_t *base, int64_t stride,
+                                                             int rows) {
+  const uint32_t bytes = rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + 128) * 2) : 0u;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), (short)0, (int)bytes,
+                                           kBufferConfig);
+}
+
+__device__ __forceinline__ u32x4 buffer_load_b128(__amdgpu_buffer_rsrc_t res, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(res, (int)byte_off, 0, 0);
+}
+
+// ds_read_b64_tr_b16 (LDS transpose read).  Within each group of 16 lanes,
+// lane j receives element j%4 of the 4 consecutive 16-bit values addressed by
+// lanes 4k + j/4, for k = 0..3 (result element k).  `p` must point into LDS.
+__device__ __forceinline__ u32x2 lds_read_tr16_b64(const uint16_t *p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 *lds_s16x4_ptr;
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(const_cast<uint16_t *>(p)));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// acc + lo(w) + hi(w) for a packed bf16 pair (v_dot2 with (1, 1)).
+__device__ __forceinline__ float dot2_bf16_ones(uint32_t w, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X.  Remap
 // the dispatch index so each XCD walks one contiguous range of work items
 // (consecutive query tiles of the same head), which keeps that head's K/V

@@ -40,7 +40,7 @@ struct AttnArgs {
 };
 
 // Launchers implemented in h3a_attn.hip / h3a_prologue.hip.
-int launch_attn_dense(const AttnArgs &a, hipStream_t s);
+int launch_attn_dense(AttnArgs a, hipStream_t s);  // sets nqt/total from its tile height
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s);
 int launch_block_map_to_lut(const uint8_t *map, int B, int H, int nq, int nk, int32_t *lut,
                             int32_t *counts, int max_k_blocks, hipStream_t s);

@@ -29,7 +29,7 @@ def _run(q_bits, k_bits, v_bits, device):
 def test_version_and_attrs(gpu):
     assert h3attn.version().startswith("h3attn")
     regs, lds, blocks, clk, occ, threads = h3attn.kernel_attrs(0)
-    assert threads == 256 and regs > 0 and lds > 0 and blocks >= 1
+    assert threads in (256, 512) and regs > 0 and lds > 0 and blocks >= 1
 
 
 def test_fragment_qk(gpu):
