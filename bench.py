@@ -22,6 +22,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "minimaxh3-on-a100-x4_amd"))
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
+# HBM bytes per launch of the dense kernel at this shape, from the rocprofv3
+# FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0) passes recorded in
+# profiles/attn_dense_h56_s42120_counters.txt (scales from a 2048 MiB copy).
+MEASURED_TRAFFIC_BYTES = 8.632e9
 B, H, S, D, LAYERS = 1, 56, 42120, 128, 50
 
 
@@ -164,7 +168,7 @@ def main():
         "ms_per_layer": round(avg_kernel_ms, 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": "attn_fwd_kernel<8,false>",
+                     "traffic": MEASURED_TRAFFIC_BYTES, "kernel": "attn_fwd_kernel<8,false>",
                      "flop_per_launch": flops_per_layer(),
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     }
