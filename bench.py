@@ -44,7 +44,7 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(budget_s: float = 12.0):
+def cpu_baseline(budget_s: float = 12.0, heads: int = H):
     """The reference's attention call (torch SDPA, attn_sm80/attn_sm80.py:33-35 and
     harness/sp_runtime.py:119-121) on bf16 CPU tensors, on a head subset at full S,
     extrapolated linearly in H (heads are independent)."""
@@ -63,31 +63,302 @@ def cpu_baseline(budget_s: float = 12.0):
     for _ in range(reps):
         torch.nn.functional.scaled_dot_product_attention(q, k, v)
     per_head = (time.perf_counter() - t0) / reps
-    layer_s = per_head * H
+    layer_s = per_head * heads
     return {
-        "value": round(flops_per_layer() / layer_s / 1e12, 4),
+        "value": round(flops_per_layer(h=heads) / layer_s / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "reference",
         "sample": (f"torch SDPA (CPU, bf16) on {hs} head x {reps} reps at S={S}, D={D}; "
-                   f"{per_head * 1e3:.0f} ms/head, extrapolated x{H} heads = "
+                   f"{per_head * 1e3:.0f} ms/head, extrapolated x{heads} heads = "
                    f"{layer_s:.2f} s/layer, {layer_s * LAYERS:.0f} s per 50-layer step; "
                    f"CPU: {cpu_model()}"),
         "ms_per_layer": round(layer_s * 1e3, 1),
     }
 
 
-def main():
+def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--workload", default="dense",
+                    choices=["dense", "h14", "sparse", "prologue", "fused"],
+                    help="dense: the headline (H=56, S=42120, 50 layers); h14: one GPU's share of "
+                         "4-way head parallelism (H=14); sparse: block-sparse top-25%%+diagonal at "
+                         "128x128 tiles; prologue: qk-RMSNorm+RoPE at S=8192, H=56 (GB/s); fused: "
+                         "prologue + attention on the fused QKV layout at S=8192, H=56")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run one device copy of this many MiB "
                          "(reference kernel for scaling FETCH_SIZE/WRITE_SIZE counters)")
-    args = ap.parse_args()
+    return ap.parse_args()
+
+
+def _timed(step, steps, warmup, n_launch, torch, stream):
+    """Run warm-up, then exactly `steps` timed steps bracketed by synchronisation;
+    HIP events on the launch stream around every launch give the per-kernel average."""
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(n_launch)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s_ in range(steps):
+        step(evs[s_])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = [a.elapsed_time(b) for st in evs for a, b in st]
+    return wall, sum(kern_ms) / len(kern_ms)
+
+
+def _calib_copy(args, torch, dev):
+    if args.calib_copy_mib > 0:
+        src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+
+def _base(args, metric, value, unit, ms_per_step, config, higher=True):
+    return {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
+            "higher_is_better": higher, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded device RNG, resident in HBM)", "config": config}
+
+
+def run_dense(args, torch, h3attn, dev, heads=H):
+    L = args.layers
+    qs, ks, vs = [], [], []
+    for layer in range(L):
+        g = torch.Generator(device=dev).manual_seed(1000 + layer)
+        qs.append(torch.randn(B, heads, S, D, generator=g, device=dev, dtype=torch.bfloat16))
+        ks.append(torch.randn(B, heads, S, D, generator=g, device=dev, dtype=torch.bfloat16))
+        vs.append(torch.randn(B, heads, S, D, generator=g, device=dev, dtype=torch.bfloat16).mul_(4))
+    out = torch.empty(B, heads, S, D, device=dev, dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+
+    def step(events):
+        for layer in range(L):
+            if events is not None:
+                events[layer][0].record(stream)
+            h3attn.attn_fwd(qs[layer], ks[layer], vs[layer], out=out)
+            if events is not None:
+                events[layer][1].record(stream)
+
+    wall, avg_kernel_ms = _timed(step, args.steps, args.warmup, L, torch, stream)
+    _calib_copy(args, torch, dev)
+    fpl = flops_per_layer(h=heads)
+    value = fpl * L * args.steps / wall / 1e12
+    achieved = fpl / (avg_kernel_ms * 1e-3) / 1e12
+    if heads == H:
+        metric = "attn TFLOP/s & % bf16 MFMA peak at H=56,S=42120,D=128; ms per 50-layer step"
+        workload = f"dense exact non-causal attention, {L} layers per step"
+    else:
+        metric = f"attn TFLOP/s & % bf16 MFMA peak at H={heads},S=42120,D=128 (one GPU's head share)"
+        workload = f"dense exact non-causal attention, H={heads} share, {L} layers per step"
+    res = _base(args, metric, value, "TFLOP/s", wall * 1e3 / args.steps,
+                {"workload": workload, "B": B, "H": heads, "S": S, "D": D, "layers": L,
+                 "segments": "text 512 + cond 256 + audio 2048 + video 39304"})
+    res["data"] = "synthetic (seeded device RNG, fresh q/k/v per layer, resident in HBM)"
+    res.update({
+        "pct_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "ms_per_layer": round(avg_kernel_ms, 3),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES if heads == H else None,
+                     "kernel": "attn_fwd_kernel<8,false>", "flop_per_launch": fpl,
+                     "avg_launch_ms": round(avg_kernel_ms, 3)},
+    })
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(heads=heads)
+    return res
+
+
+def run_sparse(args, torch, h3attn, dev):
+    """Block-sparse (h3_sla path): 128x128 tiles, top floor(0.25*330)=82 key tiles per query
+    tile from mean-pooled scores plus the diagonal; FLOPs counted exactly from the map."""
+    from h3attn import sla
+    L, blk = args.layers, 128
+    items = []
+    map_ms = []
+    for layer in range(L):
+        g = torch.Generator(device=dev).manual_seed(2000 + layer)
+        q = torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+        k = torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+        v = torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16).mul_(4)
+        a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        bmap, lut, cnt = sla.get_block_map(q, k, 0.25, blk, blk, force_diag=True, smooth_k=False)
+        b_.record()
+        torch.cuda.synchronize()
+        map_ms.append(a.elapsed_time(b_))
+        nq = bmap.shape[2]
+        valid = torch.full((nq,), blk, dtype=torch.float64, device=dev)
+        valid[-1] = S - (nq - 1) * blk
+        pairs = (bmap.double() * valid.view(1, 1, nq, 1) * valid.view(1, 1, 1, nq)).sum().item()
+        items.append((q, k, v, lut, cnt, 4.0 * D * pairs))
+    out = torch.empty(B, H, S, D, device=dev, dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+
+    def step(events):
+        for i, (q, k, v, lut, cnt, _) in enumerate(items):
+            if events is not None:
+                events[i][0].record(stream)
+            h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk, out=out)
+            if events is not None:
+                events[i][1].record(stream)
+
+    wall, avg_kernel_ms = _timed(step, args.steps, args.warmup, L, torch, stream)
+    flops = sum(it[5] for it in items) / L
+    value = flops * L * args.steps / wall / 1e12
+    achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
+    res = _base(args, "block-sparse attn TFLOP/s (exact kept-tile FLOPs) at H=56,S=42120,D=128, "
+                      "128x128 tiles, top-25%+diagonal", value, "TFLOP/s", wall * 1e3 / args.steps,
+                {"workload": f"block-sparse attention, {L} layers per step", "B": B, "H": H, "S": S,
+                 "D": D, "blk_q": blk, "blk_k": blk, "keep": "82 of 330 key tiles + diagonal"})
+    res.update({
+        "ms_per_layer": round(avg_kernel_ms, 3),
+        "kept_fraction": round(flops / flops_per_layer(), 4),
+        "dense_equivalent_tflops": round(flops_per_layer() / (avg_kernel_ms * 1e-3) / 1e12, 1),
+        "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "attn_fwd_kernel<4,true>", "flop_per_launch": flops,
+                     "avg_launch_ms": round(avg_kernel_ms, 3)},
+    })
+    return res
+
+
+def _prologue_inputs(torch, dev, s_len, heads, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    qkv = torch.randn(s_len, 3 * heads * D, generator=g, device=dev, dtype=torch.float32)
+    spread = torch.empty(s_len, 1, device=dev).uniform_(0.5, 4.0, generator=g)
+    qkv[:, :2 * heads * D] *= spread
+    qkv = qkv.to(torch.bfloat16)
+    qw = (1 + 0.05 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kw = (1 + 0.05 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    return qkv, qw, kw
+
+
+def prologue_bytes(s_len=8192, heads=H, rot=128):
+    return 4.0 * s_len * heads * D * 2 + s_len * (rot // 2) * 16 + 2 * D * 2
+
+
+def run_prologue(args, torch, h3attn, dev):
+    """qk-RMSNorm+RoPE in place on [S, 3*H*D] fused QKV views, S=8192, H=56, rot 128."""
+    s_len, rot = 8192, 128
+    qkv, qw, kw = _prologue_inputs(torch, dev, s_len, H, 7)
+    rope = h3attn.rope_freqs(s_len, rot, device=dev)
+    q = qkv[:, :H * D].view(1, s_len, H, D)
+    k = qkv[:, H * D:2 * H * D].view(1, s_len, H, D)
+    stream = torch.cuda.current_stream(dev)
+    n = 20
+
+    def step(events):
+        for i in range(n):
+            if events is not None:
+                events[i][0].record(stream)
+            h3attn.rms_rope_split_half_(q, k, rope, qw, kw, epsilon=1e-6, rot_dim=rot)
+            if events is not None:
+                events[i][1].record(stream)
+
+    wall, avg_kernel_ms = _timed(step, args.steps, args.warmup, n, torch, stream)
+    _calib_copy(args, torch, dev)
+    nbytes = prologue_bytes(s_len, H, rot)
+    gbs = nbytes / (avg_kernel_ms * 1e-3) / 1e9
+    res = _base(args, "qk-RMSNorm+RoPE prologue GB/s (algorithmic bytes) at S=8192,H=56,D=128",
+                nbytes * n * args.steps / wall / 1e9, "GB/s", wall * 1e3 / args.steps,
+                {"workload": f"in-place qk-RMSNorm + split-half RoPE on fused-QKV views, {n} calls per step",
+                 "S": s_len, "H": H, "D": D, "rot_dim": rot, "qkv_row_stride": 3 * H * D})
+    res.update({
+        "us_per_call": round(avg_kernel_ms * 1e3, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(gbs / 8000.0, 4), "traffic": None,
+                     "kernel": "qk_rmsnorm_rope_kernel", "bytes_per_launch": nbytes,
+                     "avg_launch_ms": round(avg_kernel_ms, 4)},
+    })
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_prologue_baseline(torch, s_len, rot)
+    return res
+
+
+def run_fused(args, torch, h3attn, dev):
+    """One H3 block's attention on the fused QKV layout: prologue in place, then attention
+    reading strided views and writing [S, H*D], S=8192, H=56."""
+    s_len, rot = 8192, 128
+    qkv, qw, kw = _prologue_inputs(torch, dev, s_len, H, 9)
+    rope = h3attn.rope_freqs(s_len, rot, device=dev)
+    base = qkv.clone()
+    q = qkv[:, :H * D].view(1, s_len, H, D)
+    k = qkv[:, H * D:2 * H * D].view(1, s_len, H, D)
+    v = qkv[:, 2 * H * D:].view(1, s_len, H, D)
+    out = torch.empty(1, s_len, H, D, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+    n = 10
+
+    def step(events):
+        for i in range(n):
+            qkv.copy_(base)  # fresh pre-norm inputs each call (outside the timed events)
+            if events is not None:
+                events[i][0].record(stream)
+            h3attn.rms_rope_split_half_(q, k, rope, qw, kw, epsilon=1e-6, rot_dim=rot)
+            h3attn.attn_fwd(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                            out=out.transpose(1, 2))
+            if events is not None:
+                events[i][1].record(stream)
+
+    wall, avg_ms = _timed(step, args.steps, args.warmup, n, torch, stream)
+    fl = flops_per_layer(h=H, s=s_len)
+    tf = fl / (avg_ms * 1e-3) / 1e12
+    res = _base(args, "fused block attention (prologue + attention) TFLOP/s at S=8192,H=56,D=128",
+                tf, "TFLOP/s", wall * 1e3 / args.steps,
+                {"workload": f"prologue + attention on fused [S,3HD] views, O as [S,HD], {n} calls per step",
+                 "S": s_len, "H": H, "D": D, "rot_dim": rot})
+    res.update({"ms_per_block": round(avg_ms, 3),
+                "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                             "kernel": "qk_rmsnorm_rope_kernel + attn_fwd_kernel<8,false>",
+                             "flop_per_launch": fl, "avg_launch_ms": round(avg_ms, 3)}})
+    return res
+
+
+def cpu_prologue_baseline(torch, s_len, rot):
+    """A torch fp32 CPU restatement of the prologue (the reference has no CPU path)."""
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, s_len, H, D, generator=g).to(torch.bfloat16)
+    w = torch.ones(D)
+    half = rot // 2
+    ang = torch.arange(s_len, dtype=torch.float32)[:, None] * (10000.0 ** (-2.0 * torch.arange(half) / rot))
+    c, s_ = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+
+    def once():
+        y = x.float()
+        y = y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + 1e-6) * w
+        a, b_ = y[..., :half], y[..., half:rot]
+        return torch.cat([a * c - b_ * s_, a * s_ + b_ * c, y[..., rot:]], -1).to(torch.bfloat16)
+
+    once()
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        once()
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(prologue_bytes(s_len, H, rot) / dt / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port", "sample": f"torch fp32 CPU restatement, full S={s_len} H={H}, {reps} reps, "
+                                      f"{dt * 1e3:.0f} ms/call; CPU: {cpu_model()}"}
+
+
+def main():
+    args = _parse()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
               "(the attention path is single-GPU; see DESIGN.md for how it shards)", file=sys.stderr)
@@ -98,82 +369,16 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    L = args.layers
-    qs, ks, vs = [], [], []
-    for layer in range(L):
-        g = torch.Generator(device=dev).manual_seed(1000 + layer)
-        qs.append(torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16))
-        ks.append(torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16))
-        vs.append(torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16).mul_(4))
-    out = torch.empty(B, H, S, D, device=dev, dtype=torch.bfloat16)
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream(dev)
-
-    def step(events=None):
-        for layer in range(L):
-            if events is not None:
-                events[layer][0].record(stream)
-            h3attn.attn_fwd(qs[layer], ks[layer], vs[layer], out=out)
-            if events is not None:
-                events[layer][1].record(stream)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # Timed region: exactly `steps` steps, synchronised on both sides.  HIP events
-    # bracket every launch on the launch stream for the per-kernel average.
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(L)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        step(evs[s])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-
-    if args.calib_copy_mib > 0:
-        src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-
-    kern_ms = [a.elapsed_time(b) for st in evs for a, b in st]
-    avg_kernel_ms = sum(kern_ms) / len(kern_ms)
-    ms_per_step = wall * 1e3 / args.steps
-    total_flops = flops_per_layer() * L * args.steps
-    value = total_flops / wall / 1e12
-    achieved = flops_per_layer() / (avg_kernel_ms * 1e-3) / 1e12
-
-    res = {
-        "metric": "attn TFLOP/s & % bf16 MFMA peak at H=56,S=42120,D=128; ms per 50-layer step",
-        "value": round(value, 2),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded device RNG, fresh q/k/v per layer, resident in HBM)",
-        "config": {"workload": f"dense exact non-causal attention, {L} layers per step",
-                   "B": B, "H": H, "S": S, "D": D, "layers": L,
-                   "segments": "text 512 + cond 256 + audio 2048 + video 39304"},
-        "pct_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
-        "ms_per_layer": round(avg_kernel_ms, 3),
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES, "kernel": "attn_fwd_kernel<8,false>",
-                     "flop_per_launch": flops_per_layer(),
-                     "avg_launch_ms": round(avg_kernel_ms, 3)},
-    }
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline()
+    if args.workload == "dense":
+        res = run_dense(args, torch, h3attn, dev)
+    elif args.workload == "h14":
+        res = run_dense(args, torch, h3attn, dev, heads=14)
+    elif args.workload == "sparse":
+        res = run_sparse(args, torch, h3attn, dev)
+    elif args.workload == "prologue":
+        res = run_prologue(args, torch, h3attn, dev)
+    else:
+        res = run_fused(args, torch, h3attn, dev)
     print(json.dumps(res), flush=True)
 
 

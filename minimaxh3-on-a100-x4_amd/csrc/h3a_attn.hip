@@ -41,6 +41,10 @@ namespace h3a {
 #ifndef H3A_XCD_REMAP
 #define H3A_XCD_REMAP 1
 #endif
+// Scheduling-group hints interleaving MFMA / LDS reads / VALU in the stage body.
+#ifndef H3A_SCHED_HINTS
+#define H3A_SCHED_HINTS 0
+#endif
 // Waves (32 query rows each) per dense workgroup.
 #ifndef H3A_DENSE_WAVES
 #define H3A_DENSE_WAVES 8
@@ -265,7 +269,6 @@ attn_fwd_kernel(AttnArgs a) {
   st.load_k(Kb, a.kss, key_base(1), a.Skv, tid);
   f32x16 s0, s1;
   score_tile(kbuf[0], qf, l32, g, s0, s1);
-  if (key_base(0) + kBN > a.Skv) mask_tail(s0, s1, key_base(0), a.Skv, g);
   st.store_k(kbuf[1], tid);
   __syncthreads();
 
@@ -274,6 +277,10 @@ attn_fwd_kernel(AttnArgs a) {
     st.load_k(Kb, a.kss, key_base(j + 2), a.Skv, tid);
     st.load_v(Vb, a.vss, key_base(j + 1), a.Skv, tid);
 
+    // The two rare branches (tail mask, rescale) come first, so everything
+    // after them is one basic block the scheduler can interleave freely.
+    const int key0 = key_base(j);
+    if (key0 + kBN > a.Skv) mask_tail(s0, s1, key0, a.Skv, g);
     const float mx = tile_max(s0, s1, a.sl2);
 #if H3A_LAZY_RESCALE
     // The reference max only has to bound the exponents: keep the stale max
@@ -315,11 +322,18 @@ attn_fwd_kernel(AttnArgs a) {
     lsum += rs;
 #endif
     pv_tile(vbuf[P], pf, vbase, o);
-
-    const int knext = key_base(j + 1);
-    if (knext + kBN > a.Skv) mask_tail(n0, n1, knext, a.Skv, g);
     s0 = n0;
     s1 = n1;
+#if H3A_SCHED_HINTS
+    // Interleave the block: each MFMA followed by LDS reads and VALU work
+    // that can issue in its 32-cycle shadow.
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+    }
+#endif
 
     st.store_k(kbuf[P], tid);
     st.store_v(vbuf[P ^ 1], tid);
