@@ -97,6 +97,29 @@ int h3a_block_map_to_lut(const uint8_t *block_map, int B, int H, int nq, int nk,
                          h3a_stream_t stream);
 
 /*
+ * Block means for the block map: out[b,h,j,:] = mean of x[b,h,r,:] over the
+ * valid rows r of block j (blocks of blk rows; the last may be partial).
+ * x: bf16 [B,H,S,D] with strides {batch, head, seq} (elements), D == 128.
+ * out: fp32 [B,H,ceil(S/blk),128], contiguous.  The pooling step of SLA's
+ * get_block_map (custom_nodes/h3_sla/__init__.py:232).
+ */
+int h3a_block_pool(const void *x, int B, int H, int S, int D, const int64_t strides[3], int blk,
+                   float *out, h3a_stream_t stream);
+
+/*
+ * Top-k block selection from pooled blocks: score(i,j) = pq[i] . pk[j]; query
+ * block i keeps the `keep` highest-scoring key blocks (ties: lower index
+ * first) plus, if force_diag, key block floor(i*blk_q/blk_k).  Writes the
+ * kept indices ascending into lut [B,H,nq,max_k_blocks] (-1 padded), their
+ * number into counts [B,H,nq], and, if block_map is not NULL, the 0/1 map
+ * [B,H,nq,nk].  pq: fp32 [B,H,nq,128], pk: fp32 [B,H,nk,128], contiguous.
+ * The selection step of SLA's get_block_map (custom_nodes/h3_sla/__init__.py:232).
+ */
+int h3a_block_select(const float *pq, const float *pk, int B, int H, int nq, int nk, int keep,
+                     int force_diag, int blk_q, int blk_k, int32_t *lut, int32_t *counts,
+                     int max_k_blocks, uint8_t *block_map, h3a_stream_t stream);
+
+/*
  * Fused per-head qk-RMSNorm + split-half RoPE, in place on q and k
  * (comfy.quant_ops.ck.rms_rope_split_half_, called at harness/sp_runtime.py:98
  * and custom_nodes/h3_profiler/__init__.py:104-105).

@@ -137,6 +137,37 @@ int h3a_block_map_to_lut(const uint8_t *block_map, int B, int H, int nq, int nk,
   return launch_block_map_to_lut(block_map, B, H, nq, nk, lut, counts, max_k_blocks, as_stream(stream));
 }
 
+int h3a_block_pool(const void *x, int B, int H, int S, int D, const int64_t strides[3], int blk,
+                   float *out, h3a_stream_t stream) {
+  clear_error();
+  if (!x || !out || !strides) return fail(H3A_ERR_INVALID_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || S <= 0 || blk <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d S=%d blk=%d)", B, H, S, blk);
+  if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
+  if (!aligned16(x) || !aligned16(out)) return fail(H3A_ERR_ALIGNMENT, "pointers must be 16-byte aligned");
+  if (!strides_ok(strides)) return fail(H3A_ERR_ALIGNMENT, "strides must be non-negative multiples of 8 elements");
+  const int64_t items = (int64_t)B * H * ((S + blk - 1) / blk);
+  if ((items + 3) / 4 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many blocks");
+  return launch_block_pool(static_cast<const uint16_t *>(x), strides, B, H, S, blk, out, as_stream(stream));
+}
+
+int h3a_block_select(const float *pq, const float *pk, int B, int H, int nq, int nk, int keep,
+                     int force_diag, int blk_q, int blk_k, int32_t *lut, int32_t *counts,
+                     int max_k_blocks, uint8_t *block_map, h3a_stream_t stream) {
+  clear_error();
+  if (!pq || !pk || !lut || !counts) return fail(H3A_ERR_INVALID_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || nq <= 0 || nk <= 0 || blk_q <= 0 || blk_k <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive");
+  if (nk > 7000) return fail(H3A_ERR_UNSUPPORTED, "nk %d too large (max 7000 key blocks)", nk);
+  if (keep < 0 || keep > nk) return fail(H3A_ERR_INVALID_ARG, "keep %d outside [0, %d]", keep, nk);
+  if (max_k_blocks <= 0 || max_k_blocks > nk)
+    return fail(H3A_ERR_INVALID_ARG, "max_k_blocks %d outside [1, %d]", max_k_blocks, nk);
+  if (!aligned16(pq) || !aligned16(pk)) return fail(H3A_ERR_ALIGNMENT, "pq/pk must be 16-byte aligned");
+  if ((int64_t)B * H * nq > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query blocks");
+  return launch_block_select(pq, pk, B, H, nq, nk, keep, force_diag ? 1 : 0, blk_q, blk_k, lut, counts,
+                             max_k_blocks, block_map, as_stream(stream));
+}
+
 int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D, const int64_t q_strides[3],
                         const int64_t k_strides[3], const float *rope, int64_t rope_sb,
                         int64_t rope_ss, int rot_dim, const void *qw, const void *kw, float eps,
@@ -158,7 +189,8 @@ int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D, const int6
   if (rot_dim > 0 && (rope_sb < 0 || rope_ss < 0 || (rope_sb & 3) || (rope_ss & 3)))
     return fail(H3A_ERR_ALIGNMENT, "rope strides must be non-negative multiples of 4 floats");
   const int64_t rows = (int64_t)B * S * H;
-  if ((rows + 15) / 16 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many rows");
+  const int64_t items = (int64_t)B * S * ((H + 15) / 16);  // (token, 16-head chunk) work items
+  if ((items + 3) / 4 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many tokens");
   RopeArgs a;
   a.q = static_cast<uint16_t *>(q);
   a.k = static_cast<uint16_t *>(k);

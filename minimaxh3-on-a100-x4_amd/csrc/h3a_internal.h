@@ -44,6 +44,11 @@ int launch_attn_dense(AttnArgs a, hipStream_t s);  // sets nqt/total from its ti
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s);
 int launch_block_map_to_lut(const uint8_t *map, int B, int H, int nq, int nk, int32_t *lut,
                             int32_t *counts, int max_k_blocks, hipStream_t s);
+int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int S, int blk,
+                      float *out, hipStream_t s);
+int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, int nk, int keep,
+                        int force_diag, int blk_q, int blk_k, int32_t *lut, int32_t *counts,
+                        int max_k, uint8_t *map, hipStream_t s);
 int launch_test_qk(const uint16_t *Q, const uint16_t *K, float *S, hipStream_t s);
 int launch_test_pv(const uint16_t *P, const uint16_t *V, float *O, hipStream_t s);
 int attn_kernel_attrs(int which, double out[6]);

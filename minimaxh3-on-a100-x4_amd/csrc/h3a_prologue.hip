@@ -6,12 +6,15 @@
 // the fused QKV projection output.  It is HBM-bound: every q/k row is read
 // once and written once (4*S*H*D*2 bytes) plus one rope row per token.
 //
-// Layout of the work: 16 lanes own one (b,s,h) row of q AND the same row of
-// k, 8 consecutive dims (one 128-bit access) per lane, so a 64-lane wave moves
-// four full 256-byte rows of each tensor per access.  The sum of squares is
-// reduced across the 16 lanes with xor shuffles; the RoPE partner dims
-// (i, i+rot/2) sit rot/16 lanes apart and are fetched with one shuffle per
-// value.
+// Layout of the work: one wave owns one (b,s) token and a chunk of 16 heads.
+// Its four 16-lane groups walk the chunk one head each per step; within a
+// group each lane holds 8 consecutive dims (one 128-bit access), so one wave
+// access moves four whole 256-byte head rows (1 KB contiguous in the fused
+// QKV layout).  The token's RoPE matrices and the two weight vectors are
+// loaded into registers once per wave and reused for all 2 x 16 rows; the
+// 8 row loads of the chunk are issued before any math.  The sum of squares
+// is reduced across the 16 lanes with xor shuffles; the RoPE partner dims
+// (i, i+rot/2) sit rot/16 lanes apart and are fetched with one shuffle each.
 #include "h3a_device.h"
 #include "h3a_internal.h"
 
@@ -40,9 +43,12 @@ __device__ __forceinline__ u32x4 pack8(const float (&x)[8]) {
                pack_bf16x2(x[6], x[7])};
 }
 
-// y = rmsnorm(x) * w, then rotate pairs (i, i+rot/2) with the 2x2 matrices.
+constexpr int kHeadsPerWave = 16;
+constexpr int kSteps = kHeadsPerWave / 4;  // heads per 16-lane group
+
+// y = rmsnorm(x) * w, then rotate pairs (i, i+rot/2) with the lane's 2x2 matrices.
 __device__ __forceinline__ void norm_rope_row(float (&x)[8], const float (&w)[8], float eps,
-                                              const float *rope_row, int c, int rot) {
+                                              const float4 (&R)[8], int c, int rot) {
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
@@ -59,44 +65,64 @@ __device__ __forceinline__ void norm_rope_row(float (&x)[8], const float (&w)[8]
 #pragma unroll
   for (int e = 0; e < 8; ++e) xp[e] = __shfl(x[e], partner, 16);
   if (rotated) {
-    const int i0 = (first ? c : c - nh) * 8;  // frequency index of x[0]
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float4 R = *(const float4 *)(rope_row + (i0 + e) * 4);
-      x[e] = first ? fmaf(R.x, x[e], R.y * xp[e]) : fmaf(R.z, xp[e], R.w * x[e]);
-    }
+    for (int e = 0; e < 8; ++e)
+      x[e] = first ? fmaf(R[e].x, x[e], R[e].y * xp[e]) : fmaf(R[e].z, xp[e], R[e].w * x[e]);
   }
 }
 
 __global__ void __launch_bounds__(256) qk_rmsnorm_rope_kernel(RopeArgs a) {
-  const int tid = threadIdx.x, c = tid & 15;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (tid >> 4);
-  if (row >= a.rows) return;  // whole 16-lane groups leave together
-  const int h = (int)(row % a.H);
-  const int64_t bs = row / a.H;
+  const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, c = lane & 15;
+  const int nchunk = (a.H + kHeadsPerWave - 1) / kHeadsPerWave;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (tid >> 6);  // (token, head chunk)
+  if (item >= (int64_t)a.B * a.S * nchunk) return;            // whole waves leave together
+  const int chunk = (int)(item % nchunk);
+  const int64_t bs = item / nchunk;
   const int s = (int)(bs % a.S), b = (int)(bs / a.S);
 
-  uint16_t *qp = a.q + b * a.qsb + s * a.qss + h * a.qsh + c * 8;
-  uint16_t *kp = a.k + b * a.ksb + s * a.kss + h * a.ksh + c * 8;
-  const u32x4 qv = *(const u32x4 *)qp;
-  const u32x4 kv = *(const u32x4 *)kp;
-  const u32x4 qwv = *(const u32x4 *)(a.qw + c * 8);
-  const u32x4 kwv = *(const u32x4 *)(a.kw + c * 8);
-  const float *rope_row = a.rot > 0 ? a.rope + b * a.rsb + s * a.rss : nullptr;
+  float wq[8], wk[8];
+  unpack8(*(const u32x4 *)(a.qw + c * 8), wq);
+  unpack8(*(const u32x4 *)(a.kw + c * 8), wk);
+  float4 R[8];
+  const int nh = a.rot >> 4;
+  if (c < 2 * nh) {
+    const float *rope_row = a.rope + b * a.rsb + s * a.rss + (c < nh ? c : c - nh) * 8 * 4;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) R[e] = *(const float4 *)(rope_row + e * 4);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) R[e] = float4{1.f, 0.f, 0.f, 1.f};
+  }
 
-  float xq[8], xk[8], wq[8], wk[8];
-  unpack8(qv, xq);
-  unpack8(kv, xk);
-  unpack8(qwv, wq);
-  unpack8(kwv, wk);
-  norm_rope_row(xq, wq, a.eps, rope_row, c, a.rot);
-  norm_rope_row(xk, wk, a.eps, rope_row, c, a.rot);
-  *(u32x4 *)qp = pack8(xq);
-  *(u32x4 *)kp = pack8(xk);
+  uint16_t *qrow = a.q + b * a.qsb + s * a.qss + c * 8;
+  uint16_t *krow = a.k + b * a.ksb + s * a.kss + c * 8;
+  int heads[kSteps];
+  u32x4 qv[kSteps], kv[kSteps];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    const int h = chunk * kHeadsPerWave + i * 4 + grp;
+    heads[i] = h;
+    const int hc = h < a.H ? h : a.H - 1;  // past-the-end groups recompute the last head, store nothing
+    qv[i] = *(const u32x4 *)(qrow + hc * a.qsh);
+    kv[i] = *(const u32x4 *)(krow + hc * a.ksh);
+  }
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    float xq[8], xk[8];
+    unpack8(qv[i], xq);
+    unpack8(kv[i], xk);
+    norm_rope_row(xq, wq, a.eps, R, c, a.rot);
+    norm_rope_row(xk, wk, a.eps, R, c, a.rot);
+    if (heads[i] < a.H) {
+      *(u32x4 *)(qrow + heads[i] * a.qsh) = pack8(xq);
+      *(u32x4 *)(krow + heads[i] * a.ksh) = pack8(xk);
+    }
+  }
 }
 
 int launch_qk_rmsnorm_rope(const RopeArgs &a, hipStream_t s) {
-  const int64_t blocks = (a.rows + 15) / 16;
+  const int64_t items = (int64_t)a.B * a.S * ((a.H + kHeadsPerWave - 1) / kHeadsPerWave);
+  const int64_t blocks = (items + 3) / 4;
   hipLaunchKernelGGL(qk_rmsnorm_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
   return check_launch("qk_rmsnorm_rope_kernel");
 }

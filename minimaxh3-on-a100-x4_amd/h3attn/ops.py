@@ -137,6 +137,40 @@ def block_map_to_lut(block_map: torch.Tensor, max_k_blocks: int | None = None):
     return lut, counts
 
 
+def block_pool(x: torch.Tensor, blk: int) -> torch.Tensor:
+    """Block means over the valid rows of each block: bf16 [B,H,S,128] -> fp32 [B,H,ceil(S/blk),128]."""
+    x = _as_kernel_input("x", x)
+    B, H, S, D = x.shape
+    out = torch.empty((B, H, -(-S // blk), D), dtype=torch.float32, device=x.device)
+    rc = lib().h3a_block_pool(x.data_ptr(), B, H, S, D, _bhs(x), int(blk), out.data_ptr(), _stream(x))
+    check("h3a_block_pool", rc)
+    return out
+
+
+def block_select(pq: torch.Tensor, pk: torch.Tensor, keep: int, blk_q: int, blk_k: int,
+                 force_diag: bool = True, max_k_blocks: int | None = None, want_map: bool = True):
+    """Top-`keep` key blocks per query block by pooled score (+ diagonal) -> (map|None, lut, counts)."""
+    for name, t in (("pq", pq), ("pk", pk)):
+        if t.dtype != torch.float32 or not t.is_cuda or t.dim() != 4 or t.shape[-1] != HEAD_DIM:
+            raise ValueError(f"{name} must be an fp32 GPU tensor [B,H,n,128]")
+    pq, pk = pq.contiguous(), pk.contiguous()
+    B, H, nq, _ = pq.shape
+    nk = pk.shape[2]
+    if tuple(pk.shape[:2]) != (B, H):
+        raise ValueError("pq and pk must share [B,H]")
+    if max_k_blocks is None:
+        max_k_blocks = min(nk, int(keep) + (1 if force_diag else 0))
+    lut = torch.empty((B, H, nq, max_k_blocks), dtype=torch.int32, device=pq.device)
+    counts = torch.empty((B, H, nq), dtype=torch.int32, device=pq.device)
+    bmap = torch.empty((B, H, nq, nk), dtype=torch.uint8, device=pq.device) if want_map else None
+    rc = lib().h3a_block_select(pq.data_ptr(), pk.data_ptr(), B, H, nq, nk, int(keep),
+                                1 if force_diag else 0, int(blk_q), int(blk_k), lut.data_ptr(),
+                                counts.data_ptr(), int(max_k_blocks),
+                                None if bmap is None else bmap.data_ptr(), _stream(pq))
+    check("h3a_block_select", rc)
+    return bmap, lut, counts
+
+
 def _rope_table(rope: torch.Tensor, B: int, S: int, rot_dim: int):
     """Validate a ComfyUI-style rope_freqs tensor; return (tensor, batch stride, seq stride)."""
     if rope.dtype != torch.float32:

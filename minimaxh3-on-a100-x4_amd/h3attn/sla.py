@@ -2,10 +2,9 @@
 
 The reference runs thu-ml/SLA's `get_block_map` (mean-pooled q.k^T scores,
 top-k key blocks per query block) and SLA's Triton `_attention` over the kept
-blocks (custom_nodes/h3_sla/__init__.py:226-235).  Here the block map is built
-with torch ops on the GPU (pooling + a small batched product + top-k), compacted
-to a LUT by libh3attn, and the attention runs in the gfx950 block-sparse kernel,
-which never touches a skipped key block.
+blocks (custom_nodes/h3_sla/__init__.py:226-235).  Here libh3attn pools q and k
+per block, selects the kept key blocks straight into the LUT form, and runs the
+gfx950 block-sparse kernel, which never touches a skipped key block.
 
 Also mirrors the node's per-layer keep schedule (PRESETS, parse_ranges,
 parse_layer_keep, resolve_schedule; custom_nodes/h3_sla/__init__.py:44-96),
@@ -82,59 +81,29 @@ def resolve_schedule(preset="off", topk=0.35, layer_keep="", n_layers=50):
 
 
 # ---------------------------------------------------------------------------
-def _block_means(x: torch.Tensor, blk: int) -> torch.Tensor:
-    """Mean over the valid rows of each block of `blk` rows: [B,H,S,D] -> [B,H,ceil(S/blk),D] fp32."""
-    B, H, S, D = x.shape
-    nb = -(-S // blk)
-    pad = nb * blk - S
-    xf = x.float()
-    if pad:
-        xf = torch.nn.functional.pad(xf, (0, 0, 0, pad))
-    sums = xf.reshape(B, H, nb, blk, D).sum(dim=3)
-    counts = torch.full((nb,), float(blk), device=x.device)
-    counts[-1] = blk - pad
-    return sums / counts.view(1, 1, nb, 1)
-
-
 def keep_count(topk_ratio: float, nk: int) -> int:
     """Key blocks kept by score per query block: floor(ratio * nk), at least 1, at most nk."""
     return max(1, min(nk, int(math.floor(topk_ratio * nk + 1e-9))))
 
 
-def block_scores(q: torch.Tensor, k: torch.Tensor, blk_q: int, blk_k: int,
-                 smooth_k: bool = False) -> torch.Tensor:
-    """Mean-pooled block scores [B,H,nq,nk] (fp32): pooled_q . pooled_k."""
-    kk = k
-    pk = _block_means(kk, blk_k)
-    if smooth_k:
-        pk = pk - k.float().mean(dim=2, keepdim=True)
-    pq = _block_means(q, blk_q)
-    return torch.matmul(pq, pk.transpose(-1, -2).contiguous())
-
-
 def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int = 64, BLKK: int = 64,
-                  force_diag: bool = False, smooth_k: bool = True):
-    """Block map from mean-pooled scores -> (block_map uint8 [B,H,nq,nk], lut int32, counts int32).
+                  force_diag: bool = False, smooth_k: bool = True, want_map: bool = True):
+    """Block map from mean-pooled scores -> (block_map uint8 [B,H,nq,nk] or None, lut int32, counts int32).
 
     Defaults follow SLA's get_block_map as the h3_sla node calls it
-    (custom_nodes/h3_sla/__init__.py:232): k centred by its sequence mean
-    before pooling, top floor(ratio*nk) key blocks, no forced diagonal.
-    The BASELINE block-sparse workload uses force_diag=True, smooth_k=False.
+    (custom_nodes/h3_sla/__init__.py:232): top floor(ratio*nk) key blocks by
+    pooled score, no forced diagonal.  SLA centres k by its sequence mean
+    first (smooth_k); that shifts every score of a query block by the same
+    amount and cannot change which key blocks are kept, so the selection is
+    computed without it.  The BASELINE block-sparse workload uses
+    force_diag=True.  Pooling and selection run in libh3attn; ties are broken
+    towards the lower key-block index.
     """
-    scores = block_scores(q, k, BLKQ, BLKK, smooth_k=smooth_k)
-    B, H, nq, nk = scores.shape
-    kc = keep_count(topk_ratio, nk)
-    idx = torch.topk(scores, kc, dim=-1, sorted=False).indices
-    bmap = torch.zeros((B, H, nq, nk), dtype=torch.uint8, device=q.device)
-    bmap.scatter_(-1, idx, 1)
-    if force_diag:
-        qb = torch.arange(nq, device=q.device)
-        diag = (qb * BLKQ) // BLKK
-        ok = diag < nk
-        bmap[:, :, qb[ok], diag[ok]] = 1
-    max_k = kc + (1 if force_diag else 0)
-    lut, counts = ops.block_map_to_lut(bmap, max_k_blocks=min(max_k, nk))
-    return bmap, lut, counts
+    del smooth_k  # selection-invariant, see above
+    pq = ops.block_pool(q, BLKQ)
+    pk = ops.block_pool(k, BLKK)
+    kc = keep_count(topk_ratio, pk.shape[2])
+    return ops.block_select(pq, pk, kc, BLKQ, BLKK, force_diag=force_diag, want_map=want_map)
 
 
 def sparse_attention(q, k, v, topk_ratio: float, blk: int = 64, force_diag: bool = False,
@@ -143,6 +112,6 @@ def sparse_attention(q, k, v, topk_ratio: float, blk: int = 64, force_diag: bool
     out_dtype = q.dtype
     q16, k16, v16 = (t.to(torch.bfloat16) for t in (q, k, v))
     _, lut, counts = get_block_map(q16, k16, topk_ratio, blk, blk, force_diag=force_diag,
-                                   smooth_k=smooth_k)
+                                   smooth_k=smooth_k, want_map=False)
     o = ops.attn_fwd_blocksparse(q16, k16, v16, lut, counts, blk, blk)
     return o.to(out_dtype)

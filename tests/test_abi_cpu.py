@@ -89,6 +89,15 @@ def test_lut_and_prologue_argument_errors():
     assert rope(eps=-1.0) == _lib.H3A_ERR_INVALID_ARG
     assert rope(qs=(0, 3, 0)) == _lib.H3A_ERR_ALIGNMENT
     assert rope(rss=6) == _lib.H3A_ERR_ALIGNMENT
+    assert L.h3a_block_pool(None, 1, 1, 10, 128, z, 64, 16, None) == _lib.H3A_ERR_INVALID_ARG
+    assert L.h3a_block_pool(16, 1, 1, 10, 64, z, 64, 16, None) == _lib.H3A_ERR_UNSUPPORTED
+    assert L.h3a_block_pool(16, 1, 1, 10, 128, z, 0, 16, None) == _lib.H3A_ERR_INVALID_ARG
+    assert L.h3a_block_pool(24, 1, 1, 10, 128, z, 64, 16, None) == _lib.H3A_ERR_ALIGNMENT
+    sel = L.h3a_block_select
+    assert sel(None, 16, 1, 1, 4, 4, 2, 1, 64, 64, 16, 16, 3, None, None) == _lib.H3A_ERR_INVALID_ARG
+    assert sel(16, 16, 1, 1, 4, 4, 5, 1, 64, 64, 16, 16, 3, None, None) == _lib.H3A_ERR_INVALID_ARG  # keep > nk
+    assert sel(16, 16, 1, 1, 4, 4, 2, 1, 64, 64, 16, 16, 5, None, None) == _lib.H3A_ERR_INVALID_ARG  # max_k > nk
+    assert sel(16, 16, 1, 1, 4, 9000, 2, 1, 64, 64, 16, 16, 3, None, None) == _lib.H3A_ERR_UNSUPPORTED
     assert L.h3a_kernel_attrs(0, None) == _lib.H3A_ERR_INVALID_ARG
     out = (ctypes.c_double * 6)()
     assert L.h3a_kernel_attrs(99, out) == _lib.H3A_ERR_INVALID_ARG

@@ -15,7 +15,7 @@ import torch
 import h3attn
 import oracle
 from conftest import assert_close_absmax, from_dev_bf16, randn_bf16, to_dev_bf16
-from h3attn import sla
+from h3attn import ops, sla
 
 pytestmark = pytest.mark.gpu
 
@@ -82,7 +82,7 @@ def test_empty_rows_give_zero(gpu):
 
 
 def test_gpu_block_map_matches_oracle(gpu):
-    """Torch-on-GPU block map vs the oracle: identical except where scores tie within fp32 noise."""
+    """GPU block map (pool + select) vs the oracle: identical except at fp32-level score ties."""
     rng = np.random.default_rng(23)
     S, H, blk = 2000, 2, 128
     q, k = randn_bf16(rng, (1, H, S, 128)), randn_bf16(rng, (1, H, S, 128))
@@ -98,6 +98,38 @@ def test_gpu_block_map_matches_oracle(gpu):
         thr = row[keep - 1]
         assert abs(scores[b, h, i, j] - thr) <= 1e-4 * max(1.0, abs(thr))
     assert np.array_equal(cnt.cpu().numpy(), got.sum(-1))
+
+
+def test_block_pool_matches_means(gpu):
+    """GPU block means over valid rows (partial last block), strided input."""
+    rng = np.random.default_rng(24)
+    S, H, blk = 1000, 3, 128
+    x = randn_bf16(rng, (1, S, H, 128))                     # [B,S,H,D] memory
+    xd = to_dev_bf16(x, gpu).transpose(1, 2)                 # [B,H,S,D] view
+    got = ops.block_pool(xd, blk).cpu().numpy()
+    xf = oracle.bf16_to_f32(x).reshape(x.shape).transpose(0, 2, 1, 3).astype(np.float64)
+    nb = -(-S // blk)
+    want = np.stack([xf[:, :, j * blk:min(S, (j + 1) * blk)].mean(2) for j in range(nb)], 2)
+    assert np.abs(got - want).max() <= 1e-5
+
+
+@pytest.mark.parametrize("blk,keep,diag", [(128, 3, True), (64, 5, False), (64, 1, True)])
+def test_block_select_matches_oracle(gpu, blk, keep, diag):
+    """Selection (rank by score, ties to the lower index, optional diagonal) vs the oracle."""
+    rng = np.random.default_rng(25 + blk + keep)
+    S, H = 1500, 2
+    q, k = randn_bf16(rng, (1, H, S, 128)), randn_bf16(rng, (1, H, S, 128))
+    ref, scores = oracle.block_map(q, k, blk, blk, keep=keep, force_diag=diag, return_scores=True)
+    pq = ops.block_pool(to_dev_bf16(q, gpu), blk)
+    pk = ops.block_pool(to_dev_bf16(k, gpu), blk)
+    bmap, lut, cnt = ops.block_select(pq, pk, keep, blk, blk, force_diag=diag)
+    got = bmap.cpu().numpy()
+    for b, h, i, j in np.argwhere(got != ref):  # only fp32-vs-fp64 near-ties may differ
+        thr = np.sort(scores[b, h, i])[::-1][keep - 1]
+        assert abs(scores[b, h, i, j] - thr) <= 1e-4 * max(1.0, abs(thr))
+    rl, rc = _lut_np(got, lut.shape[-1])
+    assert np.array_equal(cnt.cpu().numpy(), rc)
+    assert np.array_equal(lut.cpu().numpy(), rl)
 
 
 def test_config5_full_shape(gpu):
