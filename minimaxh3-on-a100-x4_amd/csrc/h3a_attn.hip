@@ -19,11 +19,13 @@
 //    stays row-major in LDS and its A operand is read with ds_read_b64_tr_b16
 //    (LDS transpose reads), addressed so that the key order matches the
 //    score accumulator's.
-//  * K/V stages of 64 keys are double-buffered in LDS; the next stage is
-//    fetched with 128-bit buffer loads into registers while the current one
-//    is consumed (one barrier per stage).  The buffer resource is rebased per
-//    stage so rows past Skv read as zeros and offsets are loop-invariant; the
-//    loop is unrolled by two so every LDS address is a base + immediate.
+//  * K/V stages of 64 keys are double-buffered in LDS and fetched by LDS DMA
+//    (buffer_load_dwordx4 ... lds: HBM/L2 -> LDS with no VGPR staging and no
+//    ds_write) while the current stage is consumed (one barrier per stage).
+//    Rows are 256 B, XOR-swizzled at 16-byte granularity for conflict-free
+//    MFMA operand reads.  The buffer resource is rebased per stage so rows
+//    past Skv arrive as zeros and offsets are loop-invariant; the loop is
+//    unrolled by two so every LDS address is a base + immediate.
 //  * exp2-based softmax with scale*log2(e) folded into one FMA; the running
 //    max is refreshed only when a row outgrows it by 2^8 (lazy rescale).
 //  * Workgroup ids are remapped XCD-aware (xcd_remap).
@@ -58,66 +60,67 @@ namespace h3a {
 constexpr int kD = 128;
 constexpr int kBN = 64;               // keys per pipeline stage
 constexpr float kRescaleSlack = 8.f;  // log2 headroom before the running max is refreshed
-// LDS row strides (elements).  K rows of 272 B: 128-bit reads by 16
-// consecutive rows hit distinct banks.  V rows of 320 B: the 4 rows x 64 bytes
-// gathered by each 32-lane half of a transpose read land on distinct banks.
-constexpr int kKStride = kD + 8;
-constexpr int kVStride = kD + 32;
-constexpr int kKTile = kBN * kKStride;
-constexpr int kVTile = kBN * kVStride;
+constexpr int kRowBytes = kD * 2;     // 256-byte LDS rows, no padding
+constexpr int kTile = kBN * kD;       // elements of one K or V stage in LDS (16 KiB)
 
-// 64-key K and V stages moving HBM -> registers -> LDS (both row-major).  K
-// runs one stage ahead of V, so the two halves are loaded and stored apart.
-template <int NT>
-struct KvStage {
-  static constexpr int L = (kBN * kD / 8) / NT;  // 16-byte chunks of K (and of V) per thread
-  static_assert(L * NT == kBN * kD / 8, "stage must split evenly");
-  u32x4 kr[L];
-  u32x4 vr[L];
+// LDS layout of a stage: 64 rows of 256 bytes; the 16-byte chunk c of row r
+// sits in slot c ^ swz(r) of that row.
+//   K: swz(r) = r & 15.  A 128-bit read of one chunk by 16 consecutive rows
+//      (the A operand of the score MFMA) hits 16 distinct bank groups.
+//   V: swz(r) = 4 * (r & 3).  A transpose read by 32 lanes covers 4 rows x
+//      4 chunks, which land on 16 distinct bank groups: all 64 banks once.
+__device__ __forceinline__ int k_swz(int r) { return r & 15; }
+__device__ __forceinline__ int v_swz(int r) { return 4 * (r & 3); }
 
-  // Buffer loads against a resource rebased on the stage's first key whose
-  // range covers exactly the stage's valid rows: rows >= Skv come back as
-  // zeros from the hardware (masked keys never carry NaN/Inf), there is no
-  // predication, and the per-thread byte offsets are loop-invariant.
-  __device__ __forceinline__ static void load_rows(u32x4 (&r)[L], const uint16_t *base, int64_t ss,
-                                                   int key0, int Skv, int tid) {
+// Global -> LDS staging of one 64-key K or V stage by LDS DMA.  A stage is
+// 16 KiB = 16 DMA instructions of 64 lanes x 16 bytes; instruction t fills
+// slots 64t..64t+63 (rows 4t..4t+3), and each lane fetches the global chunk
+// that its slot holds under the swizzle.  The NW waves of the workgroup issue
+// 16/NW instructions each.  The buffer resource is rebased on the stage's
+// first key and covers exactly its valid rows, so rows >= Skv arrive as zeros
+// (masked keys never carry NaN/Inf) and the per-lane offsets are loop-invariant.
+template <int NW, bool kIsV>
+struct TileDma {
+  static constexpr int kInst = 16 / NW;
+  static_assert(kInst * NW == 16, "16 DMA instructions per stage must split evenly");
+  uint32_t off[kInst];
+  int wave;  // wave-uniform
+
+  __device__ __forceinline__ void init(int64_t ss, int wave_uniform, int lane) {
+    wave = wave_uniform;
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) {
+      const int row = 4 * (wave + i * NW) + (lane >> 4);
+      const int chunk = (lane & 15) ^ (kIsV ? v_swz(row) : k_swz(row));
+      off[i] = (uint32_t)(((int64_t)row * ss + chunk * 8) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const uint16_t *base, int64_t ss, int key0, int Skv,
+                                        uint16_t *tile) const {
     const int rows = Skv - key0 >= kBN ? kBN : (Skv > key0 ? Skv - key0 : 0);
     const __amdgpu_buffer_rsrc_t res = stage_rsrc(base + (int64_t)key0 * ss, ss, rows);
 #pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const int idx = tid + i * NT, row = idx >> 4, ch = idx & 15;
-      r[i] = buffer_load_b128(res, (uint32_t)((row * ss + ch * 8) * 2));
-    }
+    for (int i = 0; i < kInst; ++i) buffer_load_lds_b128(res, off[i], tile + (wave + i * NW) * 512);
   }
-  template <int kStride>
-  __device__ __forceinline__ static void store_rows(const u32x4 (&r)[L], uint16_t *dst, int tid) {
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const int idx = tid + i * NT, row = idx >> 4, ch = idx & 15;
-      *(u32x4 *)(dst + row * kStride + ch * 8) = r[i];
-    }
-  }
-  __device__ __forceinline__ void load_k(const uint16_t *Kb, int64_t kss, int key0, int Skv, int tid) {
-    load_rows(kr, Kb, kss, key0, Skv, tid);
-  }
-  __device__ __forceinline__ void load_v(const uint16_t *Vb, int64_t vss, int key0, int Skv, int tid) {
-    load_rows(vr, Vb, vss, key0, Skv, tid);
-  }
-  __device__ __forceinline__ void store_k(uint16_t *dst, int tid) const { store_rows<kKStride>(kr, dst, tid); }
-  __device__ __forceinline__ void store_v(uint16_t *dst, int tid) const { store_rows<kVStride>(vr, dst, tid); }
 };
 
+// Byte offset, within a K stage, of this lane's A-operand chunk for k-step 0
+// (row l32, chunk g); k-step ks reads chunk 2*ks + g, i.e. offset k_rd ^ (32*ks).
+__device__ __forceinline__ int k_read_base(int l32, int g) {
+  return l32 * kRowBytes + 32 * ((l32 >> 1) & 7) + 16 * (g ^ (l32 & 1));
+}
+
 // S^T (64 keys x 32 queries of this wave) = K_stage Q^T.  s0: keys 0-31, s1: 32-63.
-__device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&qf)[8], int l32,
-                                           int g, f32x16 &s0, f32x16 &s1) {
+__device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&qf)[8], int k_rd,
+                                           f32x16 &s0, f32x16 &s1) {
   s0 = f32x16{0.f};
   s1 = f32x16{0.f};
-  const uint16_t *r0 = kbuf + l32 * kKStride + 8 * g;
-  const uint16_t *r1 = r0 + 32 * kKStride;
+  const char *kb = reinterpret_cast<const char *>(kbuf);
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    const u32x4 a0 = *(const u32x4 *)(r0 + ks * 16);
-    const u32x4 a1 = *(const u32x4 *)(r1 + ks * 16);
+    const char *p = kb + (k_rd ^ (32 * ks));
+    const u32x4 a0 = *(const u32x4 *)p;
+    const u32x4 a1 = *(const u32x4 *)(p + 32 * kRowBytes);
     s0 = mfma_32x32x16(a0, qf[ks], s0);
     s1 = mfma_32x32x16(a1, qf[ks], s1);
   }
@@ -135,26 +138,32 @@ __device__ __forceinline__ void pack_p(const f32x16 &s0, const f32x16 &s1, u32x4
   }
 }
 
-// Per-lane base of the V transpose reads.  Within each 16-lane group a
+// Per-lane byte offset of the V transpose reads.  Within each 16-lane group a
 // ds_read_b64_tr_b16 gives lane j element j%4 of the 4 consecutive bf16 that
 // lanes 4k + j/4 address (k = 0..3).  Lane i of group t points at row
 // 4*(t/2) + i/4 (+16*ks, +8 for k-slots 4..7) and columns 16*(t%2) + 4*(i%4)
 // (+32*dt), so lane l receives V[key][32*dt + l%32] for the 4 keys of its
-// k-slots, in the score accumulator's key order.
-__device__ __forceinline__ int v_tr_base(int lane) {
-  return (4 * (lane >> 5) + ((lane & 15) >> 2)) * kVStride + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+// k-slots, in the score accumulator's key order.  Column block dt is chunk
+// 4*dt + c of the row, stored in slot (4*dt + c) ^ 4*(row & 3): the offset for
+// dt is v_rd ^ (64*dt), and the row steps are multiples of 256 bytes.
+__device__ __forceinline__ int v_read_base(int lane) {
+  const int i = (lane & 15) >> 2;
+  const int row = 4 * (lane >> 5) + i;
+  const int c = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  return row * kRowBytes + 64 * i + 16 * c + 8 * (lane & 1);
 }
 
 // O^T (128 dims x 32 queries) += V^T_stage P^T.
-__device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[4], int vbase,
+__device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[4], int v_rd,
                                         f32x16 (&o)[4]) {
-  const uint16_t *b = vbuf + vbase;
+  const char *vb = reinterpret_cast<const char *>(vbuf);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const u32x2 lo = lds_read_tr16_b64(b + (16 * ks) * kVStride + 32 * dt);
-      const u32x2 hi = lds_read_tr16_b64(b + (16 * ks + 8) * kVStride + 32 * dt);
+      const char *p = vb + (v_rd ^ (64 * dt)) + 16 * ks * kRowBytes;
+      const u32x2 lo = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p));
+      const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * kRowBytes));
       o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[ks], o[dt]);
     }
   }
@@ -182,10 +191,9 @@ __device__ __forceinline__ void mask_tail(f32x16 &s0, f32x16 &s1, int key0, int 
 template <int NW, bool kSparse>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_kernel(AttnArgs a) {
-  constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kKTile];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kVTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t kbuf[2][kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t vbuf[2][kTile];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -253,29 +261,34 @@ attn_fwd_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
-  const int vbase = v_tr_base(lane);
+  const int k_rd = k_read_base(l32, g);
+  const int v_rd = v_read_base(lane);
 
   // Software pipeline: K runs one stage ahead of V.  Entering stage j, LDS
   // holds V(j) in vbuf[j&1] and K(j+1) in kbuf[(j+1)&1], and the registers
-  // hold the masked scores S(j).  Stage j computes S(j+1) = K(j+1) Q^T while
-  // the softmax of S(j) runs (independent work the scheduler interleaves),
-  // then O += V(j) P(j), and parks the prefetched K(j+2) and V(j+1).
-  KvStage<NT> st;
-  st.load_k(Kb, a.kss, key_base(0), a.Skv, tid);
-  st.load_v(Vb, a.vss, key_base(0), a.Skv, tid);
-  st.store_k(kbuf[0], tid);
-  st.store_v(vbuf[0], tid);
+  // hold the masked scores S(j).  Stage j starts the DMA of K(j+2) and V(j+1)
+  // into the buffers stage j-1 finished with, computes S(j+1) = K(j+1) Q^T
+  // while the softmax of S(j) runs (independent work the scheduler
+  // interleaves), then O += V(j) P(j); the DMA has the whole stage to land.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  TileDma<NW, false> kdma;
+  TileDma<NW, true> vdma;
+  kdma.init(a.kss, wave_u, lane);
+  vdma.init(a.vss, wave_u, lane);
+  kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
+  vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+  wait_vmem_all();
   __syncthreads();
-  st.load_k(Kb, a.kss, key_base(1), a.Skv, tid);
+  kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
   f32x16 s0, s1;
-  score_tile(kbuf[0], qf, l32, g, s0, s1);
-  st.store_k(kbuf[1], tid);
+  score_tile(kbuf[0], qf, k_rd, s0, s1);
+  wait_vmem_all();
   __syncthreads();
 
   auto stage = [&](auto parity, int j) {
     constexpr int P = decltype(parity)::value;  // j & 1
-    st.load_k(Kb, a.kss, key_base(j + 2), a.Skv, tid);
-    st.load_v(Vb, a.vss, key_base(j + 1), a.Skv, tid);
+    kdma.issue(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
+    vdma.issue(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
 
     // The two rare branches (tail mask, rescale) come first, so everything
     // after them is one basic block the scheduler can interleave freely.
@@ -302,7 +315,7 @@ attn_fwd_kernel(AttnArgs a) {
 
     // S(j+1) on the MFMA pipe, softmax(j) on the VALU: no dependence between them.
     f32x16 n0, n1;
-    score_tile(kbuf[P ^ 1], qf, l32, g, n0, n1);
+    score_tile(kbuf[P ^ 1], qf, k_rd, n0, n1);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       s0[r] = fast_exp2(fmaf(s0[r], a.sl2, -muse));
@@ -321,7 +334,7 @@ attn_fwd_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
     lsum += rs;
 #endif
-    pv_tile(vbuf[P], pf, vbase, o);
+    pv_tile(vbuf[P], pf, v_rd, o);
     s0 = n0;
     s1 = n1;
 #if H3A_SCHED_HINTS
@@ -335,8 +348,7 @@ attn_fwd_kernel(AttnArgs a) {
     }
 #endif
 
-    st.store_k(kbuf[P], tid);
-    st.store_v(vbuf[P ^ 1], tid);
+    wait_vmem_all();
     __syncthreads();
   };
 
@@ -364,17 +376,18 @@ attn_fwd_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Fragment tests: one wave, the same staging and fragment code as above.
 __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const uint16_t *K, float *S) {
-  __shared__ __attribute__((aligned(16))) uint16_t kb[kKTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t kb[kTile];
   const int tid = threadIdx.x, g = tid >> 5, l32 = tid & 31;
-  KvStage<64> st;
-  st.load_k(K, kD, 0, kBN, tid);
-  st.store_k(kb, tid);
+  TileDma<1, false> dma;
+  dma.init(kD, 0, tid);
+  dma.issue(K, kD, 0, kBN, kb);
+  wait_vmem_all();
   __syncthreads();
   u32x4 qf[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const u32x4 *)(Q + l32 * kD + ks * 16 + 8 * g);
   f32x16 s0, s1;
-  score_tile(kb, qf, l32, g, s0, s1);
+  score_tile(kb, qf, k_read_base(l32, g), s0, s1);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = 8 * (r >> 2) + 4 * g + (r & 3);
@@ -384,11 +397,12 @@ __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const ui
 }
 
 __global__ void __launch_bounds__(64) test_pv_kernel(const uint16_t *P, const uint16_t *V, float *O) {
-  __shared__ __attribute__((aligned(16))) uint16_t vb[kVTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t vb[kTile];
   const int tid = threadIdx.x, g = tid >> 5, l32 = tid & 31;
-  KvStage<64> st;
-  st.load_v(V, kD, 0, kBN, tid);
-  st.store_v(vb, tid);
+  TileDma<1, true> dma;
+  dma.init(kD, 0, tid);
+  dma.issue(V, kD, 0, kBN, vb);
+  wait_vmem_all();
   __syncthreads();
   // Place P[q][key] where the score accumulators would hold it.
   f32x16 s0, s1;
@@ -403,7 +417,7 @@ __global__ void __launch_bounds__(64) test_pv_kernel(const uint16_t *P, const ui
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
-  pv_tile(vb, pf, v_tr_base(tid), o);
+  pv_tile(vb, pf, v_read_base(tid), o);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll

@@ -64,6 +64,27 @@ __device__ __forceinline__ u32x4 buffer_load_b128(__amdgpu_buffer_rsrc_t res, ui
   return __builtin_amdgcn_raw_buffer_load_b128(res, (int)byte_off, 0, 0);
 }
 
+// LDS DMA (buffer_load_dwordx4 ... lds): each lane's 16 bytes at `byte_off`
+// go straight to LDS at lds_dst + 16 * lane, with no VGPR staging.  lds_dst
+// must be wave-uniform (it is passed in M0).  Lanes past the resource's range
+// write zeros.  Completion is counted by vmcnt like any vector-memory load.
+//
+// Issued as inline asm on purpose: the compiler cannot tell which LDS bytes a
+// DMA writes, and with the builtin it waits for every DMA in flight before
+// any later LDS read, including reads of the other buffer.  The caller owns
+// completion: wait_vmem_all() and a barrier before the LDS bytes are read.
+// The compiler's own vmcnt waits stay correct, since extra loads issued
+// after one of its loads only make a wait for that load more conservative.
+__device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t res, uint32_t byte_off,
+                                                     void *lds_dst) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_dst;
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(res), "{m0}"(m0) : "memory");
+}
+
+// s_waitcnt vmcnt(0): every vector-memory load of this wave (LDS DMA
+// included) has landed.  The other counters are left alone.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // ds_read_b64_tr_b16 (LDS transpose read).  Within each group of 16 lanes,
 // lane j receives element j%4 of the 4 consecutive 16-bit values addressed by
 // lanes 4k + j/4, for k = 0..3 (result element k).  `p` must point into LDS.
