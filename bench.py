@@ -172,7 +172,7 @@ def run_dense(args, torch, h3attn, dev, heads=H):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES if heads == H else None,
-                     "kernel": "attn_fwd_kernel<8,false>", "flop_per_launch": fpl,
+                     "kernel": "attn_fwd_pingpong_kernel", "flop_per_launch": fpl,
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     })
     if not args.no_cpu_baseline:
@@ -230,7 +230,7 @@ def run_sparse(args, torch, h3attn, dev):
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "attn_fwd_kernel<4,true>", "flop_per_launch": flops,
+                     "kernel": "attn_fwd_kernel<4,2,true>", "flop_per_launch": flops,
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     })
     return res
@@ -324,7 +324,7 @@ def run_fused(args, torch, h3attn, dev):
     res.update({"ms_per_block": round(avg_ms, 3),
                 "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                             "kernel": "qk_rmsnorm_rope_kernel + attn_fwd_kernel<8,false>",
+                             "kernel": "qk_rmsnorm_rope_kernel + attn_fwd_pingpong_kernel",
                              "flop_per_launch": fl, "avg_launch_ms": round(avg_ms, 3)}})
     return res
 

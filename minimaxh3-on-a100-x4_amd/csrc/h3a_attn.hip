@@ -51,6 +51,20 @@ namespace h3a {
 #ifndef H3A_DENSE_WAVES
 #define H3A_DENSE_WAVES 8
 #endif
+// Dense path: ping-pong wave groups (attn_fwd_pingpong_kernel, 8 waves)
+// instead of attn_fwd_kernel.
+#ifndef H3A_DENSE_PINGPONG
+#define H3A_DENSE_PINGPONG 1
+#endif
+// LDS operand reads issued ahead of the first MFMA of a ping-pong matrix
+// cluster (0: leave the order to the scheduler).
+#ifndef H3A_PP_READ_AHEAD
+#define H3A_PP_READ_AHEAD 6
+#endif
+// LDS stages per operand in the dense attn_fwd_kernel (2 or 3).
+#ifndef H3A_DENSE_STAGES
+#define H3A_DENSE_STAGES 2
+#endif
 // Row sum from the bf16-rounded P (v_dot2, 16 ops) instead of the unrounded
 // p (32 adds).  Off by default: the reference sums unrounded p.
 #ifndef H3A_ROWSUM_BF16
@@ -188,12 +202,17 @@ __device__ __forceinline__ void mask_tail(f32x16 &s0, f32x16 &s1, int key0, int 
   }
 }
 
-template <int NW, bool kSparse>
+// NS = LDS stages per operand (2 or 3): with 3, the DMA runs two stages ahead
+// and a stage's barrier waits only for the loads issued one stage earlier.
+template <int NW, int NS, bool kSparse>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_kernel(AttnArgs a) {
+  static_assert(NS == 2 || NS == 3, "2 or 3 LDS stages");
   constexpr int BM = NW * 32;
-  __shared__ __attribute__((aligned(1024))) uint16_t kbuf[2][kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t vbuf[2][kTile];
+  // DMA instructions per wave still allowed in flight at a stage barrier.
+  constexpr int kInFlight = (NS - 2) * 2 * TileDma<NW, false>::kInst;
+  __shared__ __attribute__((aligned(1024))) uint16_t kbuf[NS][kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t vbuf[NS][kTile];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -265,30 +284,34 @@ attn_fwd_kernel(AttnArgs a) {
   const int v_rd = v_read_base(lane);
 
   // Software pipeline: K runs one stage ahead of V.  Entering stage j, LDS
-  // holds V(j) in vbuf[j&1] and K(j+1) in kbuf[(j+1)&1], and the registers
-  // hold the masked scores S(j).  Stage j starts the DMA of K(j+2) and V(j+1)
-  // into the buffers stage j-1 finished with, computes S(j+1) = K(j+1) Q^T
-  // while the softmax of S(j) runs (independent work the scheduler
-  // interleaves), then O += V(j) P(j); the DMA has the whole stage to land.
+  // holds V(j) in vbuf[j%NS] and K(j+1) in kbuf[(j+1)%NS], and the registers
+  // hold the masked scores S(j).  Stage j starts the DMA of K(j+NS) and
+  // V(j+NS-1) into the buffers stage j-1 finished with, computes
+  // S(j+1) = K(j+1) Q^T while the softmax of S(j) runs (independent work the
+  // scheduler interleaves), then O += V(j) P(j).  Its closing barrier needs
+  // only K(j+2) and V(j+1), issued NS-2 stages earlier.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   TileDma<NW, false> kdma;
   TileDma<NW, true> vdma;
   kdma.init(a.kss, wave_u, lane);
   vdma.init(a.vss, wave_u, lane);
-  kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
-  vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
-  wait_vmem_all();
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) {
+    kdma.issue(Kb, a.kss, key_base(t), a.Skv, kbuf[t]);
+    vdma.issue(Vb, a.vss, key_base(t), a.Skv, vbuf[t]);
+  }
+  wait_vmem_le<kInFlight>();  // K(0), V(0) landed
   __syncthreads();
-  kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+  kdma.issue(Kb, a.kss, key_base(NS - 1), a.Skv, kbuf[NS - 1]);
   f32x16 s0, s1;
   score_tile(kbuf[0], qf, k_rd, s0, s1);
-  wait_vmem_all();
+  wait_vmem_le<kInFlight>();  // K(1) landed
   __syncthreads();
 
-  auto stage = [&](auto parity, int j) {
-    constexpr int P = decltype(parity)::value;  // j & 1
-    kdma.issue(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
-    vdma.issue(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
+  auto stage = [&](auto phase, int j) {
+    constexpr int P = decltype(phase)::value;  // j % NS
+    kdma.issue(Kb, a.kss, key_base(j + NS), a.Skv, kbuf[P]);
+    vdma.issue(Vb, a.vss, key_base(j + NS - 1), a.Skv, vbuf[(P + NS - 1) % NS]);
 
     // The two rare branches (tail mask, rescale) come first, so everything
     // after them is one basic block the scheduler can interleave freely.
@@ -315,7 +338,7 @@ attn_fwd_kernel(AttnArgs a) {
 
     // S(j+1) on the MFMA pipe, softmax(j) on the VALU: no dependence between them.
     f32x16 n0, n1;
-    score_tile(kbuf[P ^ 1], qf, k_rd, n0, n1);
+    score_tile(kbuf[(P + 1) % NS], qf, k_rd, n0, n1);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       s0[r] = fast_exp2(fmaf(s0[r], a.sl2, -muse));
@@ -348,13 +371,200 @@ attn_fwd_kernel(AttnArgs a) {
     }
 #endif
 
-    wait_vmem_all();
+    wait_vmem_le<kInFlight>();
     __syncthreads();
   };
 
-  for (int j = 0; j < niter; j += 2) {
+  for (int j = 0; j < niter; j += NS) {
     stage(std::integral_constant<int, 0>{}, j);
     if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
+    if constexpr (NS == 3) {
+      if (j + 2 < niter) stage(std::integral_constant<int, 2>{}, j + 2);
+    }
+  }
+
+  const float ltot = half_swap_sum(lsum);
+  const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+  if (qrow < a.Sq) {
+    uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const u32x2 val = {pack_bf16x2(o[dt][4 * rr + 0] * inv, o[dt][4 * rr + 1] * inv),
+                           pack_bf16x2(o[dt][4 * rr + 2] * inv, o[dt][4 * rr + 3] * inv)};
+        *(u32x2 *)(p + dt * 32 + 8 * rr) = val;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax of one 64-key score stage, in place: S -> P (bf16 pairs in pf), the
+// running max m (refreshed lazily, as in attn_fwd_kernel) and this lane's
+// share of the row sum of the unrounded p; O and l are rescaled when the max
+// moves.  VALU work only.
+__device__ __forceinline__ void softmax_stage(f32x16 &s0, f32x16 &s1, int key0, int Skv, int g,
+                                              float sl2, float &m, float &lsum, f32x16 (&o)[4],
+                                              u32x4 (&pf)[4]) {
+  if (key0 + kBN > Skv) mask_tail(s0, s1, key0, Skv, g);
+  const float mx = tile_max(s0, s1, sl2);
+  if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0) {
+    const float mnew = fmaxf(m, mx);
+    const float alpha = fast_exp2(m - ((mnew == kNegInf) ? 0.f : mnew));
+    m = mnew;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+  }
+  const float muse = (m == kNegInf) ? 0.f : m;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    s0[r] = fast_exp2(fmaf(s0[r], sl2, -muse));
+    s1[r] = fast_exp2(fmaf(s1[r], sl2, -muse));
+  }
+  pack_p(s0, s1, pf);
+  float rs = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
+  lsum += rs;
+}
+
+// Workgroup barrier that the instruction scheduler does not move work across.
+__device__ __forceinline__ void slot_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Dense kernel with ping-pong wave groups.  8 waves x 32 query rows; waves
+// 0-3 (group A) and 4-7 (group B) sit one of each per SIMD.  Every stage is
+// split into a matrix-core cluster, MFMA(j): S(j+1) = K(j+1) Q^T and
+// O += V(j) P(j), and a softmax cluster, SOFT(j): S(j+1) -> P(j+1), with a
+// workgroup barrier after each.  Group B runs one cluster behind group A, so
+// on every SIMD one wave issues MFMAs while the other issues the softmax's
+// VALU work and the two pipes overlap.
+//
+// Barrier slots after the prologue (both groups pass the same barriers):
+//   slot 2j+1:  A: DMA(j), MFMA(j)            B: DMA(j), SOFT(j-1)
+//   slot 2j+2:  A: SOFT(j), wait for DMA      B: MFMA(j), wait for DMA
+// DMA(j) fetches K(j+2) into kbuf[j&1] and V(j+1) into vbuf[(j+1)&1].  Those
+// buffers were last read by MFMA(j-1), which both groups finished by the end
+// of slot 2j; the data is read by MFMA(j+1) from slot 2j+3 on, after every
+// wave waited for its share of the DMA at the end of slot 2j+2.
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+attn_fwd_pingpong_kernel(AttnArgs a) {
+  constexpr int NW = 8;
+  constexpr int BM = NW * 32;
+  __shared__ __attribute__((aligned(1024))) uint16_t kbuf[2][kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t vbuf[2][kTile];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+#if H3A_XCD_REMAP
+  const int w = xcd_remap(blockIdx.x, a.total);
+#else
+  const int w = blockIdx.x;
+#endif
+  const int qt = w % a.nqt, bh = w / a.nqt;
+  const int h = bh % a.H, b = bh / a.H;
+  const uint16_t *Qb = a.q + b * a.qsb + h * a.qsh;
+  const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
+  const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
+  uint16_t *Ob = a.o + b * a.osb + h * a.osh;
+
+  const int niter = (a.Skv + kBN - 1) / kBN;  // >= 1
+  auto key_base = [&](int j) -> int { return j < niter ? j * kBN : a.Skv; };
+
+  const int qrow = qt * BM + wave * 32 + l32;
+  u32x4 qf[8];
+  if (qrow < a.Sq) {
+    const uint16_t *p = Qb + (int64_t)qrow * a.qss + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const u32x4 *)(p + ks * 16);
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = u32x4{0, 0, 0, 0};
+  }
+  f32x16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
+  float m = kNegInf;  // running row max, in scale*log2(e) units
+  float lsum = 0.f;   // this lane's share of the running row sum
+  const int k_rd = k_read_base(l32, g);
+  const int v_rd = v_read_base(lane);
+
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  TileDma<NW, false> kdma;
+  TileDma<NW, true> vdma;
+  kdma.init(a.kss, wave_u, lane);
+  vdma.init(a.vss, wave_u, lane);
+
+  // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
+  kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
+  vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+  kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+  wait_vmem_all();
+  __syncthreads();
+  f32x16 s0, s1;
+  score_tile(kbuf[0], qf, k_rd, s0, s1);
+  u32x4 pf[4];
+  softmax_stage(s0, s1, key_base(0), a.Skv, g, a.sl2, m, lsum, o, pf);
+  __syncthreads();  // kbuf[0] is free for K(2)
+
+  auto dma = [&](auto par, int j) {
+    constexpr int P = decltype(par)::value;  // j & 1
+    kdma.issue(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
+    vdma.issue(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
+  };
+  // One basic block: 16 score MFMAs (the last stage multiplies the zero tile
+  // K(niter) and discards it) and 16 PV MFMAs, with the 48 LDS operand reads
+  // issued ahead of them: 6 up front, then 2 after each MFMA, so every read
+  // is in flight for at least 6 MFMAs (~200 cycles).
+  auto mfma = [&](auto par, int j) {
+    constexpr int P = decltype(par)::value;
+    (void)j;
+    __builtin_amdgcn_s_setprio(1);
+    score_tile(kbuf[P ^ 1], qf, k_rd, s0, s1);
+    pv_tile(vbuf[P], pf, v_rd, o);
+#if H3A_PP_READ_AHEAD
+    __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+#endif
+    __builtin_amdgcn_s_setprio(0);
+  };
+  auto soft = [&](int j) { softmax_stage(s0, s1, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf); };
+
+  if (wave_u < NW / 2) {
+    auto stage = [&](auto par, int j) {
+      dma(par, j);
+      mfma(par, j);
+      slot_barrier();
+      if (j + 1 < niter) soft(j);
+      wait_vmem_all();
+      slot_barrier();
+    };
+    for (int j = 0; j < niter; j += 2) {
+      stage(std::integral_constant<int, 0>{}, j);
+      if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
+    }
+  } else {
+    auto stage = [&](auto par, int j) {
+      dma(par, j);
+      if (j > 0) soft(j - 1);
+      slot_barrier();
+      mfma(par, j);
+      wait_vmem_all();
+      slot_barrier();
+    };
+    for (int j = 0; j < niter; j += 2) {
+      stage(std::integral_constant<int, 0>{}, j);
+      if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
+    }
   }
 
   const float ltot = half_swap_sum(lsum);
@@ -447,20 +657,28 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 
 // ---------------------------------------------------------------------------
 int launch_attn_dense(AttnArgs a, hipStream_t s) {
+#if H3A_DENSE_PINGPONG
+  constexpr int NW = 8;
+#else
   constexpr int NW = H3A_DENSE_WAVES;
+#endif
   a.nqt = (a.Sq + 32 * NW - 1) / (32 * NW);
   const int64_t total = (int64_t)a.B * a.H * a.nqt;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
   a.total = (int)total;
-  hipLaunchKernelGGL((attn_fwd_kernel<NW, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
+#if H3A_DENSE_PINGPONG
+  hipLaunchKernelGGL(attn_fwd_pingpong_kernel, dim3(a.total), dim3(64 * NW), 0, s, a);
+#else
+  hipLaunchKernelGGL((attn_fwd_kernel<NW, H3A_DENSE_STAGES, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
+#endif
   return check_launch("attn_fwd_kernel<dense>");
 }
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   if (blk_q == 128) {
-    hipLaunchKernelGGL((attn_fwd_kernel<4, true>), dim3(a.total), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<4, 2, true>), dim3(a.total), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((attn_fwd_kernel<2, true>), dim3(a.total), dim3(128), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<2, 2, true>), dim3(a.total), dim3(128), 0, s, a);
   }
   return check_launch("attn_fwd_kernel<sparse>");
 }
@@ -507,12 +725,16 @@ static int fill_attrs(const void *fn, int threads, double out[6]) {
 int attn_kernel_attrs(int which, double out[6]) {
   switch (which) {
     case H3A_KERNEL_ATTN_DENSE:
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<H3A_DENSE_WAVES, false>),
+#if H3A_DENSE_PINGPONG
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel), 512, out);
+#else
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<H3A_DENSE_WAVES, H3A_DENSE_STAGES, false>),
                         64 * H3A_DENSE_WAVES, out);
+#endif
     case H3A_KERNEL_ATTN_SPARSE_128:
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, true>), 256, out);
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, 2, true>), 256, out);
     case H3A_KERNEL_ATTN_SPARSE_64:
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<2, true>), 128, out);
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<2, 2, true>), 128, out);
     default:
       return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
   }

@@ -72,7 +72,8 @@ __device__ __forceinline__ u32x4 buffer_load_b128(__amdgpu_buffer_rsrc_t res, ui
 // Issued as inline asm on purpose: the compiler cannot tell which LDS bytes a
 // DMA writes, and with the builtin it waits for every DMA in flight before
 // any later LDS read, including reads of the other buffer.  The caller owns
-// completion: wait_vmem_all() and a barrier before the LDS bytes are read.
+// completion: a vmcnt wait (wait_vmem_le) and a barrier before the LDS
+// bytes are read.
 // The compiler's own vmcnt waits stay correct, since extra loads issued
 // after one of its loads only make a wait for that load more conservative.
 __device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t res, uint32_t byte_off,
@@ -81,9 +82,15 @@ __device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t res,
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(res), "{m0}"(m0) : "memory");
 }
 
-// s_waitcnt vmcnt(0): every vector-memory load of this wave (LDS DMA
-// included) has landed.  The other counters are left alone.
-__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N): at most the N most recent vector-memory loads of this
+// wave (LDS DMA included) are still in flight; loads complete in order.  The
+// other counters are left alone (expcnt 7, lgkmcnt 15).
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_vmem_all() { wait_vmem_le<0>(); }
 
 // ds_read_b64_tr_b16 (LDS transpose read).  Within each group of 16 lanes,
 // lane j receives element j%4 of the 4 consecutive 16-bit values addressed by
