@@ -56,14 +56,27 @@ namespace h3a {
 #ifndef H3A_DENSE_PINGPONG
 #define H3A_DENSE_PINGPONG 1
 #endif
+// Block-sparse path with 128-row query blocks: ping-pong kernel over pairs of
+// query blocks instead of attn_fwd_kernel<4, PadLayout, ...>.
+#ifndef H3A_SPARSE_PINGPONG
+#define H3A_SPARSE_PINGPONG 0
+#endif
+// LDS stage layout (0: SwzLayout, 1: PadLayout) of the dense kernels and of
+// the block-sparse ping-pong kernel.
+#ifndef H3A_DENSE_LAYOUT
+#define H3A_DENSE_LAYOUT 0
+#endif
+#ifndef H3A_SPARSE_LAYOUT
+#define H3A_SPARSE_LAYOUT 1
+#endif
+// Block-sparse attn_fwd_kernel: K/V staged through VGPRs (1) or by LDS DMA (0).
+#ifndef H3A_SPARSE_REGS
+#define H3A_SPARSE_REGS 1
+#endif
 // LDS operand reads issued ahead of the first MFMA of a ping-pong matrix
 // cluster (0: leave the order to the scheduler).
 #ifndef H3A_PP_READ_AHEAD
 #define H3A_PP_READ_AHEAD 6
-#endif
-// LDS stages per operand in the dense attn_fwd_kernel (2 or 3).
-#ifndef H3A_DENSE_STAGES
-#define H3A_DENSE_STAGES 2
 #endif
 // Row sum from the bf16-rounded P (v_dot2, 16 ops) instead of the unrounded
 // p (32 adds).  Off by default: the reference sums unrounded p.
@@ -74,29 +87,77 @@ namespace h3a {
 constexpr int kD = 128;
 constexpr int kBN = 64;               // keys per pipeline stage
 constexpr float kRescaleSlack = 8.f;  // log2 headroom before the running max is refreshed
-constexpr int kRowBytes = kD * 2;     // 256-byte LDS rows, no padding
-constexpr int kTile = kBN * kD;       // elements of one K or V stage in LDS (16 KiB)
 
-// LDS layout of a stage: 64 rows of 256 bytes; the 16-byte chunk c of row r
-// sits in slot c ^ swz(r) of that row.
+// ---------------------------------------------------------------------------
+// LDS layouts of a 64-key K or V stage.  A layout fixes the row pitch, which
+// 16-byte global chunk each 16-byte LDS slot holds, and how the MFMA operand
+// reads address the stage.  Both are bank-conflict free for the reads below
+// (SQ_LDS_BANK_CONFLICT = 0 measured for each).
+//
+// SwzLayout: 256-byte rows; chunk c of row r sits in slot c ^ swz(r).
 //   K: swz(r) = r & 15.  A 128-bit read of one chunk by 16 consecutive rows
 //      (the A operand of the score MFMA) hits 16 distinct bank groups.
 //   V: swz(r) = 4 * (r & 3).  A transpose read by 32 lanes covers 4 rows x
 //      4 chunks, which land on 16 distinct bank groups: all 64 banks once.
-__device__ __forceinline__ int k_swz(int r) { return r & 15; }
-__device__ __forceinline__ int v_swz(int r) { return 4 * (r & 3); }
+//   Read offsets are base ^ const, held per lane.
+// PadLayout: K rows of 272 bytes (17 slots), V rows of 320 bytes (20 slots),
+//   chunk c in slot c; the extra slots are padding that shifts consecutive
+//   rows across the banks.  Read offsets are base + immediate.
+struct SwzLayout {
+  static constexpr int kKRow = 256, kVRow = 256;  // bytes
+  static constexpr int kKSlots = 16, kVSlots = 16;
+  __device__ __forceinline__ static int k_chunk(int r, int slot) { return slot ^ (r & 15); }
+  __device__ __forceinline__ static int v_chunk(int r, int slot) { return slot ^ (4 * (r & 3)); }
+  // Lane's A-operand chunk of k-step 0 (row l32, chunk g); k-step ks reads
+  // chunk 2*ks + g, i.e. offset k_base ^ (32*ks).
+  __device__ __forceinline__ static int k_base(int l32, int g) {
+    return l32 * kKRow + 32 * ((l32 >> 1) & 7) + 16 * (g ^ (l32 & 1));
+  }
+  __device__ __forceinline__ static int k_off(int kb, int ks) { return kb ^ (32 * ks); }
+  // Column block dt of the transpose reads is chunk 4*dt + c of the row,
+  // stored in slot (4*dt + c) ^ 4*(row & 3): offset v_base ^ (64*dt).
+  __device__ __forceinline__ static int v_base(int lane) {
+    const int i = (lane & 15) >> 2;
+    const int row = 4 * (lane >> 5) + i;
+    const int c = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    return row * kVRow + 64 * i + 16 * c + 8 * (lane & 1);
+  }
+  __device__ __forceinline__ static int v_off(int vb, int dt) { return vb ^ (64 * dt); }
+};
 
-// Global -> LDS staging of one 64-key K or V stage by LDS DMA.  A stage is
-// 16 KiB = 16 DMA instructions of 64 lanes x 16 bytes; instruction t fills
-// slots 64t..64t+63 (rows 4t..4t+3), and each lane fetches the global chunk
-// that its slot holds under the swizzle.  The NW waves of the workgroup issue
-// 16/NW instructions each.  The buffer resource is rebased on the stage's
-// first key and covers exactly its valid rows, so rows >= Skv arrive as zeros
-// (masked keys never carry NaN/Inf) and the per-lane offsets are loop-invariant.
-template <int NW, bool kIsV>
+struct PadLayout {
+  static constexpr int kKRow = 272, kVRow = 320;  // bytes
+  static constexpr int kKSlots = 17, kVSlots = 20;
+  // Padding slots load a duplicate of an in-row chunk (never read back).
+  __device__ __forceinline__ static int k_chunk(int, int slot) { return slot & 15; }
+  __device__ __forceinline__ static int v_chunk(int, int slot) { return slot & 15; }
+  __device__ __forceinline__ static int k_base(int l32, int g) { return l32 * kKRow + 16 * g; }
+  __device__ __forceinline__ static int k_off(int kb, int ks) { return kb + 32 * ks; }
+  __device__ __forceinline__ static int v_base(int lane) {
+    const int row = 4 * (lane >> 5) + ((lane & 15) >> 2);
+    return row * kVRow + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
+  }
+  __device__ __forceinline__ static int v_off(int vb, int dt) { return vb + 64 * dt; }
+};
+
+template <class L>
+struct StageBytes {
+  static constexpr int kK = kBN * L::kKRow;
+  static constexpr int kV = kBN * L::kVRow;
+};
+
+// Global -> LDS staging of one 64-key K or V stage by LDS DMA.  Instruction t
+// fills the 64 consecutive 16-byte slots 64t..64t+63 of the stage (1 KiB);
+// each lane fetches the global chunk that its slot holds under the layout.
+// The NW waves of the stream issue instructions t = wave, wave+NW, ...  The
+// buffer resource is rebased on the stage's first key and covers exactly its
+// valid rows, so rows >= Skv arrive as zeros (masked keys never carry
+// NaN/Inf) and the per-lane offsets are loop-invariant.
+template <int NW, class L, bool kIsV>
 struct TileDma {
-  static constexpr int kInst = 16 / NW;
-  static_assert(kInst * NW == 16, "16 DMA instructions per stage must split evenly");
+  static constexpr int kSlots = kIsV ? L::kVSlots : L::kKSlots;  // per row
+  static constexpr int kInstTotal = kSlots;                       // 64 rows x kSlots / 64 lanes
+  static constexpr int kInst = (kInstTotal + NW - 1) / NW;        // per wave (the last may be idle)
   uint32_t off[kInst];
   int wave;  // wave-uniform
 
@@ -104,9 +165,10 @@ struct TileDma {
     wave = wave_uniform;
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
-      const int row = 4 * (wave + i * NW) + (lane >> 4);
-      const int chunk = (lane & 15) ^ (kIsV ? v_swz(row) : k_swz(row));
-      off[i] = (uint32_t)(((int64_t)row * ss + chunk * 8) * 2);
+      const int slot = 64 * (wave + i * NW) + lane;
+      const int row = slot / kSlots, sl = slot % kSlots;
+      const int chunk = kIsV ? L::v_chunk(row, sl) : L::k_chunk(row, sl);
+      off[i] = (uint32_t)(((int64_t)(row < kBN ? row : kBN - 1) * ss + chunk * 8) * 2);
     }
   }
   __device__ __forceinline__ void issue(const uint16_t *base, int64_t ss, int key0, int Skv,
@@ -114,17 +176,59 @@ struct TileDma {
     const int rows = Skv - key0 >= kBN ? kBN : (Skv > key0 ? Skv - key0 : 0);
     const __amdgpu_buffer_rsrc_t res = stage_rsrc(base + (int64_t)key0 * ss, ss, rows);
 #pragma unroll
-    for (int i = 0; i < kInst; ++i) buffer_load_lds_b128(res, off[i], tile + (wave + i * NW) * 512);
+    for (int i = 0; i < kInst; ++i) {
+      if (kInstTotal % NW == 0 || wave + i * NW < kInstTotal)
+        buffer_load_lds_b128(res, off[i], tile + (wave + i * NW) * 512);
+    }
+  }
+  // Common staging interface: start() at the top of a stage, finish() at its
+  // end; kAsync stagers need a vmcnt wait before the stage's barrier.
+  static constexpr bool kAsync = true;
+  __device__ __forceinline__ void start(const uint16_t *base, int64_t ss, int key0, int Skv,
+                                        uint16_t *tile) {
+    issue(base, ss, key0, Skv, tile);
+  }
+  __device__ __forceinline__ void finish(uint16_t *) const {}
+};
+
+// Staging through VGPRs into PadLayout: 128-bit buffer loads when the stage
+// starts, ds_write_b128 when it ends.  Thread t of the stream moves chunks
+// idx = t + i*NT (row idx/16, chunk idx%16), so its global offsets and LDS
+// addresses are one base plus compile-time steps.  The block-sparse kernels
+// use it: their key blocks arrive in LUT order, and with LDS DMA instead the
+// same kernel measured a lower L2 hit rate (32 % vs 62 %) and ran 6 % slower.
+template <int NW, bool kIsV>
+struct TileRegs {
+  static constexpr int NT = NW * 64;
+  static constexpr int kInst = (kBN * kD / 8) / NT;  // 16-byte chunks per thread
+  static_assert(kInst * NT == kBN * kD / 8, "stage must split evenly");
+  static constexpr int kRow = kIsV ? PadLayout::kVRow : PadLayout::kKRow;
+  static constexpr bool kAsync = false;
+  u32x4 r[kInst];
+  uint32_t goff;  // global byte offset of chunk 0 (row t/16, chunk t%16)
+  int loff;       // LDS byte offset of chunk 0
+  uint32_t gstep; // global bytes between consecutive chunks of this thread (NT/16 rows)
+
+  __device__ __forceinline__ void init(int64_t ss, int tid) {
+    goff = (uint32_t)(((int64_t)(tid >> 4) * ss + (tid & 15) * 8) * 2);
+    gstep = (uint32_t)((NT / 16) * ss * 2);
+    loff = (tid >> 4) * kRow + (tid & 15) * 16;
+  }
+  __device__ __forceinline__ void start(const uint16_t *base, int64_t ss, int key0, int Skv, uint16_t *) {
+    const int rows = Skv - key0 >= kBN ? kBN : (Skv > key0 ? Skv - key0 : 0);
+    const __amdgpu_buffer_rsrc_t res = stage_rsrc(base + (int64_t)key0 * ss, ss, rows);
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) r[i] = buffer_load_b128(res, goff + i * gstep);
+  }
+  __device__ __forceinline__ void finish(uint16_t *tile) const {
+    char *t = reinterpret_cast<char *>(tile) + loff;
+#pragma unroll
+    for (int i = 0; i < kInst; ++i) *(u32x4 *)(t + i * (NT / 16) * kRow) = r[i];
   }
 };
 
-// Byte offset, within a K stage, of this lane's A-operand chunk for k-step 0
-// (row l32, chunk g); k-step ks reads chunk 2*ks + g, i.e. offset k_rd ^ (32*ks).
-__device__ __forceinline__ int k_read_base(int l32, int g) {
-  return l32 * kRowBytes + 32 * ((l32 >> 1) & 7) + 16 * (g ^ (l32 & 1));
-}
-
 // S^T (64 keys x 32 queries of this wave) = K_stage Q^T.  s0: keys 0-31, s1: 32-63.
+template <class L>
 __device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&qf)[8], int k_rd,
                                            f32x16 &s0, f32x16 &s1) {
   s0 = f32x16{0.f};
@@ -132,9 +236,9 @@ __device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&q
   const char *kb = reinterpret_cast<const char *>(kbuf);
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    const char *p = kb + (k_rd ^ (32 * ks));
+    const char *p = kb + L::k_off(k_rd, ks);
     const u32x4 a0 = *(const u32x4 *)p;
-    const u32x4 a1 = *(const u32x4 *)(p + 32 * kRowBytes);
+    const u32x4 a1 = *(const u32x4 *)(p + 32 * L::kKRow);
     s0 = mfma_32x32x16(a0, qf[ks], s0);
     s1 = mfma_32x32x16(a1, qf[ks], s1);
   }
@@ -152,22 +256,14 @@ __device__ __forceinline__ void pack_p(const f32x16 &s0, const f32x16 &s1, u32x4
   }
 }
 
-// Per-lane byte offset of the V transpose reads.  Within each 16-lane group a
-// ds_read_b64_tr_b16 gives lane j element j%4 of the 4 consecutive bf16 that
-// lanes 4k + j/4 address (k = 0..3).  Lane i of group t points at row
-// 4*(t/2) + i/4 (+16*ks, +8 for k-slots 4..7) and columns 16*(t%2) + 4*(i%4)
-// (+32*dt), so lane l receives V[key][32*dt + l%32] for the 4 keys of its
-// k-slots, in the score accumulator's key order.  Column block dt is chunk
-// 4*dt + c of the row, stored in slot (4*dt + c) ^ 4*(row & 3): the offset for
-// dt is v_rd ^ (64*dt), and the row steps are multiples of 256 bytes.
-__device__ __forceinline__ int v_read_base(int lane) {
-  const int i = (lane & 15) >> 2;
-  const int row = 4 * (lane >> 5) + i;
-  const int c = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-  return row * kRowBytes + 64 * i + 16 * c + 8 * (lane & 1);
-}
-
+// V transpose reads.  Within each 16-lane group a ds_read_b64_tr_b16 gives
+// lane j element j%4 of the 4 consecutive bf16 that lanes 4k + j/4 address
+// (k = 0..3).  Lane i of group t points at row 4*(t/2) + i/4 (+16*ks, +8 for
+// k-slots 4..7) and columns 16*(t%2) + 4*(i%4) (+32*dt), so lane l receives
+// V[key][32*dt + l%32] for the 4 keys of its k-slots, in the score
+// accumulator's key order.  L::v_base / L::v_off place that in the layout.
 // O^T (128 dims x 32 queries) += V^T_stage P^T.
+template <class L>
 __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[4], int v_rd,
                                         f32x16 (&o)[4]) {
   const char *vb = reinterpret_cast<const char *>(vbuf);
@@ -175,9 +271,9 @@ __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[
   for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const char *p = vb + (v_rd ^ (64 * dt)) + 16 * ks * kRowBytes;
+      const char *p = vb + L::v_off(v_rd, dt) + 16 * ks * L::kVRow;
       const u32x2 lo = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p));
-      const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * kRowBytes));
+      const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * L::kVRow));
       o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[ks], o[dt]);
     }
   }
@@ -202,17 +298,14 @@ __device__ __forceinline__ void mask_tail(f32x16 &s0, f32x16 &s1, int key0, int 
   }
 }
 
-// NS = LDS stages per operand (2 or 3): with 3, the DMA runs two stages ahead
-// and a stage's barrier waits only for the loads issued one stage earlier.
-template <int NW, int NS, bool kSparse>
+// kRegs: stage K/V through VGPRs into PadLayout (TileRegs) instead of LDS DMA.
+template <int NW, class L, bool kRegs, bool kSparse>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_kernel(AttnArgs a) {
-  static_assert(NS == 2 || NS == 3, "2 or 3 LDS stages");
+  static_assert(!kRegs || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
   constexpr int BM = NW * 32;
-  // DMA instructions per wave still allowed in flight at a stage barrier.
-  constexpr int kInFlight = (NS - 2) * 2 * TileDma<NW, false>::kInst;
-  __shared__ __attribute__((aligned(1024))) uint16_t kbuf[NS][kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t vbuf[NS][kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][StageBytes<L>::kK / 2];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][StageBytes<L>::kV / 2];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -280,38 +373,47 @@ attn_fwd_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
-  const int k_rd = k_read_base(l32, g);
-  const int v_rd = v_read_base(lane);
+  const int k_rd = L::k_base(l32, g);
+  const int v_rd = L::v_base(lane);
 
   // Software pipeline: K runs one stage ahead of V.  Entering stage j, LDS
-  // holds V(j) in vbuf[j%NS] and K(j+1) in kbuf[(j+1)%NS], and the registers
-  // hold the masked scores S(j).  Stage j starts the DMA of K(j+NS) and
-  // V(j+NS-1) into the buffers stage j-1 finished with, computes
-  // S(j+1) = K(j+1) Q^T while the softmax of S(j) runs (independent work the
-  // scheduler interleaves), then O += V(j) P(j).  Its closing barrier needs
-  // only K(j+2) and V(j+1), issued NS-2 stages earlier.
+  // holds V(j) in vbuf[j&1] and K(j+1) in kbuf[(j+1)&1], and the registers
+  // hold the masked scores S(j).  Stage j starts fetching K(j+2) and V(j+1)
+  // for the buffers stage j-1 finished with, computes S(j+1) = K(j+1) Q^T
+  // while the softmax of S(j) runs (independent work the scheduler
+  // interleaves), then O += V(j) P(j); the fetch lands by the stage's barrier.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  TileDma<NW, false> kdma;
-  TileDma<NW, true> vdma;
-  kdma.init(a.kss, wave_u, lane);
-  vdma.init(a.vss, wave_u, lane);
-#pragma unroll
-  for (int t = 0; t < NS - 1; ++t) {
-    kdma.issue(Kb, a.kss, key_base(t), a.Skv, kbuf[t]);
-    vdma.issue(Vb, a.vss, key_base(t), a.Skv, vbuf[t]);
+  using KStager = std::conditional_t<kRegs, TileRegs<NW, false>, TileDma<NW, L, false>>;
+  using VStager = std::conditional_t<kRegs, TileRegs<NW, true>, TileDma<NW, L, true>>;
+  KStager kst;
+  VStager vst;
+  if constexpr (kRegs) {
+    kst.init(a.kss, tid);
+    vst.init(a.vss, tid);
+  } else {
+    kst.init(a.kss, wave_u, lane);
+    vst.init(a.vss, wave_u, lane);
   }
-  wait_vmem_le<kInFlight>();  // K(0), V(0) landed
-  __syncthreads();
-  kdma.issue(Kb, a.kss, key_base(NS - 1), a.Skv, kbuf[NS - 1]);
+  auto land = [&] {  // this wave's stage fetches are in LDS
+    if constexpr (KStager::kAsync) wait_vmem_all();
+  };
   f32x16 s0, s1;
-  score_tile(kbuf[0], qf, k_rd, s0, s1);
-  wait_vmem_le<kInFlight>();  // K(1) landed
+  kst.start(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
+  vst.start(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+  kst.finish(kbuf[0]);
+  vst.finish(vbuf[0]);
+  land();
+  __syncthreads();
+  kst.start(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+  score_tile<L>(kbuf[0], qf, k_rd, s0, s1);
+  kst.finish(kbuf[1]);
+  land();
   __syncthreads();
 
   auto stage = [&](auto phase, int j) {
-    constexpr int P = decltype(phase)::value;  // j % NS
-    kdma.issue(Kb, a.kss, key_base(j + NS), a.Skv, kbuf[P]);
-    vdma.issue(Vb, a.vss, key_base(j + NS - 1), a.Skv, vbuf[(P + NS - 1) % NS]);
+    constexpr int P = decltype(phase)::value;  // j & 1
+    kst.start(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
+    vst.start(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
 
     // The two rare branches (tail mask, rescale) come first, so everything
     // after them is one basic block the scheduler can interleave freely.
@@ -338,7 +440,7 @@ attn_fwd_kernel(AttnArgs a) {
 
     // S(j+1) on the MFMA pipe, softmax(j) on the VALU: no dependence between them.
     f32x16 n0, n1;
-    score_tile(kbuf[(P + 1) % NS], qf, k_rd, n0, n1);
+    score_tile<L>(kbuf[P ^ 1], qf, k_rd, n0, n1);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       s0[r] = fast_exp2(fmaf(s0[r], a.sl2, -muse));
@@ -357,7 +459,7 @@ attn_fwd_kernel(AttnArgs a) {
     for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
     lsum += rs;
 #endif
-    pv_tile(vbuf[P], pf, v_rd, o);
+    pv_tile<L>(vbuf[P], pf, v_rd, o);
     s0 = n0;
     s1 = n1;
 #if H3A_SCHED_HINTS
@@ -371,16 +473,15 @@ attn_fwd_kernel(AttnArgs a) {
     }
 #endif
 
-    wait_vmem_le<kInFlight>();
+    kst.finish(kbuf[P]);
+    vst.finish(vbuf[P ^ 1]);
+    land();
     __syncthreads();
   };
 
-  for (int j = 0; j < niter; j += NS) {
+  for (int j = 0; j < niter; j += 2) {
     stage(std::integral_constant<int, 0>{}, j);
     if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
-    if constexpr (NS == 3) {
-      if (j + 2 < niter) stage(std::integral_constant<int, 2>{}, j + 2);
-    }
   }
 
   const float ltot = half_swap_sum(lsum);
@@ -437,13 +538,13 @@ __device__ __forceinline__ void slot_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Dense kernel with ping-pong wave groups.  8 waves x 32 query rows; waves
-// 0-3 (group A) and 4-7 (group B) sit one of each per SIMD.  Every stage is
-// split into a matrix-core cluster, MFMA(j): S(j+1) = K(j+1) Q^T and
-// O += V(j) P(j), and a softmax cluster, SOFT(j): S(j+1) -> P(j+1), with a
-// workgroup barrier after each.  Group B runs one cluster behind group A, so
-// on every SIMD one wave issues MFMAs while the other issues the softmax's
-// VALU work and the two pipes overlap.
+// Ping-pong kernel: 8 waves x 32 query rows; waves 0-3 (group A) and 4-7
+// (group B) sit one of each per SIMD.  Every stage is split into a
+// matrix-core cluster, MFMA(j): S(j+1) = K(j+1) Q^T and O += V(j) P(j), and a
+// softmax cluster, SOFT(j): S(j+1) -> P(j+1), with a workgroup barrier after
+// each.  Group B runs one cluster behind group A, so on every SIMD one wave
+// issues MFMAs while the other issues the softmax's VALU work and the two
+// pipes overlap.
 //
 // Barrier slots after the prologue (both groups pass the same barriers):
 //   slot 2j+1:  A: DMA(j), MFMA(j)            B: DMA(j), SOFT(j-1)
@@ -452,31 +553,90 @@ __device__ __forceinline__ void slot_barrier() {
 // buffers were last read by MFMA(j-1), which both groups finished by the end
 // of slot 2j; the data is read by MFMA(j+1) from slot 2j+3 on, after every
 // wave waited for its share of the DMA at the end of slot 2j+2.
+//
+// Dense: the workgroup is one 256-row query tile; both groups share one K/V
+// stream (the 8 waves split each DMA).  Block-sparse (blk_q = 128): the
+// workgroup is two 128-row query blocks of one head, group A the even one and
+// group B the odd one, each with its own LUT row, K/V buffers and DMA.  Both
+// groups run max(stages of A, stages of B) stages so they pass the same
+// barriers; past its own count a group only takes part in the barriers.
+template <bool kSparse, class L>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   constexpr int NW = 8;
-  constexpr int BM = NW * 32;
-  __shared__ __attribute__((aligned(1024))) uint16_t kbuf[2][kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t vbuf[2][kTile];
+  constexpr int kStreams = kSparse ? 2 : 1;  // K/V streams per workgroup
+  constexpr int kDmaWaves = NW / kStreams;   // waves sharing one stream's DMA
+  constexpr int kKE = StageBytes<L>::kK / 2, kVE = StageBytes<L>::kV / 2;  // elements
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[kStreams][2][kKE];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[kStreams][2][kVE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const bool lead = wave_u < NW / 2;  // group A
 #if H3A_XCD_REMAP
   const int w = xcd_remap(blockIdx.x, a.total);
 #else
   const int w = blockIdx.x;
 #endif
-  const int qt = w % a.nqt, bh = w / a.nqt;
+  // Query tiles per (b,h) in units of this workgroup: 256-row tiles (dense) or
+  // pairs of 128-row blocks (sparse, a.nqt blocks).
+  const int wg_tiles = kSparse ? (a.nqt + 1) / 2 : a.nqt;
+  const int qt = w % wg_tiles, bh = w / wg_tiles;
   const int h = bh % a.H, b = bh / a.H;
   const uint16_t *Qb = a.q + b * a.qsb + h * a.qsh;
   const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
   const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
   uint16_t *Ob = a.o + b * a.osb + h * a.osh;
 
-  const int niter = (a.Skv + kBN - 1) / kBN;  // >= 1
-  auto key_base = [&](int j) -> int { return j < niter ? j * kBN : a.Skv; };
+  int niter;         // stages of this wave's group
+  int niter_wg;      // stages the workgroup runs (max over the groups)
+  int qrow;          // this lane's query row
+  const int32_t *lut_row = nullptr;
+  if constexpr (kSparse) {
+    const int grp = lead ? 0 : 1;
+    const int qb = 2 * qt + grp;
+    auto stages_of = [&](int blk) -> int {
+      if (blk >= a.nqt) return 0;
+      const int cnt = a.counts[(int64_t)bh * a.nqt + blk];
+      return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
+    };
+    niter = stages_of(qb);
+    const int other = stages_of(2 * qt + (1 - grp));
+    niter_wg = niter > other ? niter : other;
+    lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
+    qrow = qb * 128 + (wave & 3) * 32 + l32;
+  } else {
+    niter = (a.Skv + kBN - 1) / kBN;  // >= 1
+    niter_wg = niter;
+    qrow = qt * 256 + wave * 32 + l32;
+  }
+  // First key of stage j of this group; past the group's last stage (and for
+  // LUT entries outside the key range) it is Skv, which loads nothing (zeros).
+  auto key_base = [&](int j) -> int {
+    if (j >= niter) return a.Skv;
+    if constexpr (kSparse) {
+      const int kb = lut_row[j / a.sub];
+      const int key0 = kb * a.blk_k + (j % a.sub) * kBN;
+      return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
+    } else {
+      return j * kBN;
+    }
+  };
 
-  const int qrow = qt * BM + wave * 32 + l32;
+  if (niter_wg == 0) {
+    // Neither group has a key block (empty LUT rows): O = 0.  No barrier is
+    // reached by any wave of the workgroup.
+    if (qrow < a.Sq) {
+      uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
+    }
+    return;
+  }
+  uint16_t (*kbuf)[kKE] = kbuf_all[kSparse && !lead ? 1 : 0];
+  uint16_t (*vbuf)[kVE] = vbuf_all[kSparse && !lead ? 1 : 0];
+
   u32x4 qf[8];
   if (qrow < a.Sq) {
     const uint16_t *p = Qb + (int64_t)qrow * a.qss + 8 * g;
@@ -491,25 +651,30 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
-  const int k_rd = k_read_base(l32, g);
-  const int v_rd = v_read_base(lane);
+  const int k_rd = L::k_base(l32, g);
+  const int v_rd = L::v_base(lane);
 
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  TileDma<NW, false> kdma;
-  TileDma<NW, true> vdma;
-  kdma.init(a.kss, wave_u, lane);
-  vdma.init(a.vss, wave_u, lane);
+  TileDma<kDmaWaves, L, false> kdma;
+  TileDma<kDmaWaves, L, true> vdma;
+  const int dma_wave = kSparse ? (wave_u & 3) : wave_u;
+  kdma.init(a.kss, dma_wave, lane);
+  vdma.init(a.vss, dma_wave, lane);
+  const bool active = niter > 0;
 
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
-  kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
-  vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
-  kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+  if (active) {
+    kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
+    vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+    kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+  }
   wait_vmem_all();
   __syncthreads();
   f32x16 s0, s1;
-  score_tile(kbuf[0], qf, k_rd, s0, s1);
   u32x4 pf[4];
-  softmax_stage(s0, s1, key_base(0), a.Skv, g, a.sl2, m, lsum, o, pf);
+  if (active) {
+    score_tile<L>(kbuf[0], qf, k_rd, s0, s1);
+    softmax_stage(s0, s1, key_base(0), a.Skv, g, a.sl2, m, lsum, o, pf);
+  }
   __syncthreads();  // kbuf[0] is free for K(2)
 
   auto dma = [&](auto par, int j) {
@@ -517,16 +682,15 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     kdma.issue(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
     vdma.issue(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
   };
-  // One basic block: 16 score MFMAs (the last stage multiplies the zero tile
-  // K(niter) and discards it) and 16 PV MFMAs, with the 48 LDS operand reads
-  // issued ahead of them: 6 up front, then 2 after each MFMA, so every read
-  // is in flight for at least 6 MFMAs (~200 cycles).
-  auto mfma = [&](auto par, int j) {
+  // One basic block: 16 score MFMAs (the group's last stage multiplies the
+  // zero tile past its keys and discards it) and 16 PV MFMAs, with the 48 LDS
+  // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
+  // after each MFMA, so every read is in flight for several MFMAs.
+  auto mfma = [&](auto par) {
     constexpr int P = decltype(par)::value;
-    (void)j;
     __builtin_amdgcn_s_setprio(1);
-    score_tile(kbuf[P ^ 1], qf, k_rd, s0, s1);
-    pv_tile(vbuf[P], pf, v_rd, o);
+    score_tile<L>(kbuf[P ^ 1], qf, k_rd, s0, s1);
+    pv_tile<L>(vbuf[P], pf, v_rd, o);
 #if H3A_PP_READ_AHEAD
     __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
 #pragma unroll
@@ -539,31 +703,37 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   };
   auto soft = [&](int j) { softmax_stage(s0, s1, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf); };
 
-  if (wave_u < NW / 2) {
+  if (lead) {
     auto stage = [&](auto par, int j) {
-      dma(par, j);
-      mfma(par, j);
+      const bool run = j < niter;
+      if (run) {
+        dma(par, j);
+        mfma(par);
+      }
       slot_barrier();
       if (j + 1 < niter) soft(j);
       wait_vmem_all();
       slot_barrier();
     };
-    for (int j = 0; j < niter; j += 2) {
+    for (int j = 0; j < niter_wg; j += 2) {
       stage(std::integral_constant<int, 0>{}, j);
-      if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
+      if (j + 1 < niter_wg) stage(std::integral_constant<int, 1>{}, j + 1);
     }
   } else {
     auto stage = [&](auto par, int j) {
-      dma(par, j);
-      if (j > 0) soft(j - 1);
+      const bool run = j < niter;
+      if (run) {
+        dma(par, j);
+        if (j > 0) soft(j - 1);
+      }
       slot_barrier();
-      mfma(par, j);
+      if (run) mfma(par);
       wait_vmem_all();
       slot_barrier();
     };
-    for (int j = 0; j < niter; j += 2) {
+    for (int j = 0; j < niter_wg; j += 2) {
       stage(std::integral_constant<int, 0>{}, j);
-      if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
+      if (j + 1 < niter_wg) stage(std::integral_constant<int, 1>{}, j + 1);
     }
   }
 
@@ -586,9 +756,9 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Fragment tests: one wave, the same staging and fragment code as above.
 __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const uint16_t *K, float *S) {
-  __shared__ __attribute__((aligned(1024))) uint16_t kb[kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t kb[StageBytes<SwzLayout>::kK / 2];
   const int tid = threadIdx.x, g = tid >> 5, l32 = tid & 31;
-  TileDma<1, false> dma;
+  TileDma<1, SwzLayout, false> dma;
   dma.init(kD, 0, tid);
   dma.issue(K, kD, 0, kBN, kb);
   wait_vmem_all();
@@ -597,7 +767,7 @@ __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const ui
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const u32x4 *)(Q + l32 * kD + ks * 16 + 8 * g);
   f32x16 s0, s1;
-  score_tile(kb, qf, k_read_base(l32, g), s0, s1);
+  score_tile<SwzLayout>(kb, qf, SwzLayout::k_base(l32, g), s0, s1);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = 8 * (r >> 2) + 4 * g + (r & 3);
@@ -607,9 +777,9 @@ __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const ui
 }
 
 __global__ void __launch_bounds__(64) test_pv_kernel(const uint16_t *P, const uint16_t *V, float *O) {
-  __shared__ __attribute__((aligned(1024))) uint16_t vb[kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vb[StageBytes<SwzLayout>::kV / 2];
   const int tid = threadIdx.x, g = tid >> 5, l32 = tid & 31;
-  TileDma<1, true> dma;
+  TileDma<1, SwzLayout, true> dma;
   dma.init(kD, 0, tid);
   dma.issue(V, kD, 0, kBN, vb);
   wait_vmem_all();
@@ -627,7 +797,7 @@ __global__ void __launch_bounds__(64) test_pv_kernel(const uint16_t *P, const ui
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
-  pv_tile(vb, pf, v_read_base(tid), o);
+  pv_tile<SwzLayout>(vb, pf, SwzLayout::v_base(tid), o);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -656,6 +826,9 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 }
 
 // ---------------------------------------------------------------------------
+using DenseLayout = std::conditional_t<H3A_DENSE_LAYOUT == 1, PadLayout, SwzLayout>;
+using SparseLayout = std::conditional_t<H3A_SPARSE_LAYOUT == 1, PadLayout, SwzLayout>;
+
 int launch_attn_dense(AttnArgs a, hipStream_t s) {
 #if H3A_DENSE_PINGPONG
   constexpr int NW = 8;
@@ -667,18 +840,25 @@ int launch_attn_dense(AttnArgs a, hipStream_t s) {
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
   a.total = (int)total;
 #if H3A_DENSE_PINGPONG
-  hipLaunchKernelGGL(attn_fwd_pingpong_kernel, dim3(a.total), dim3(64 * NW), 0, s, a);
+  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<false, DenseLayout>), dim3(a.total), dim3(64 * NW), 0, s, a);
 #else
-  hipLaunchKernelGGL((attn_fwd_kernel<NW, H3A_DENSE_STAGES, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<NW, DenseLayout, false, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
 #endif
   return check_launch("attn_fwd_kernel<dense>");
 }
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   if (blk_q == 128) {
-    hipLaunchKernelGGL((attn_fwd_kernel<4, 2, true>), dim3(a.total), dim3(256), 0, s, a);
+#if H3A_SPARSE_PINGPONG
+    // Pairs of 128-row query blocks per workgroup.
+    AttnArgs p = a;
+    p.total = a.B * a.H * ((a.nqt + 1) / 2);
+    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<true, SparseLayout>), dim3(p.total), dim3(512), 0, s, p);
+#else
+    hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(256), 0, s, a);
+#endif
   } else {
-    hipLaunchKernelGGL((attn_fwd_kernel<2, 2, true>), dim3(a.total), dim3(128), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(128), 0, s, a);
   }
   return check_launch("attn_fwd_kernel<sparse>");
 }
@@ -726,15 +906,19 @@ int attn_kernel_attrs(int which, double out[6]) {
   switch (which) {
     case H3A_KERNEL_ATTN_DENSE:
 #if H3A_DENSE_PINGPONG
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel), 512, out);
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<false, DenseLayout>), 512, out);
 #else
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<H3A_DENSE_WAVES, H3A_DENSE_STAGES, false>),
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<H3A_DENSE_WAVES, DenseLayout, false, false>),
                         64 * H3A_DENSE_WAVES, out);
 #endif
     case H3A_KERNEL_ATTN_SPARSE_128:
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, 2, true>), 256, out);
+#if H3A_SPARSE_PINGPONG
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<true, SparseLayout>), 512, out);
+#else
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), 256, out);
+#endif
     case H3A_KERNEL_ATTN_SPARSE_64:
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<2, 2, true>), 128, out);
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), 128, out);
     default:
       return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
   }

@@ -79,7 +79,8 @@ __device__ __forceinline__ u32x4 buffer_load_b128(__amdgpu_buffer_rsrc_t res, ui
 __device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t res, uint32_t byte_off,
                                                      void *lds_dst) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_dst;
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(res), "{m0}"(m0) : "memory");
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(res), "{m0}"(m0)
+               : "memory");
 }
 
 // s_waitcnt vmcnt(N): at most the N most recent vector-memory loads of this
