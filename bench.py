@@ -307,7 +307,7 @@ def run_prologue(args, torch, h3attn, dev):
 
 def run_fused(args, torch, h3attn, dev):
     """One H3 block's attention on the fused QKV layout: prologue in place, then attention
-    reading strided views and writing [S, H*D], S=8192, H=56."""
+    reading strided views and writing [S, H*D], S=8192, H=56, rot 128."""
     s_len, rot = 8192, 128
     qkv, qw, kw = _prologue_inputs(torch, dev, s_len, H, 9)
     rope = h3attn.rope_freqs(s_len, rot, device=dev)
@@ -377,7 +377,7 @@ def main():
     args = _parse()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported "
-              "(the attention path is single-GPU; see DESIGN.md for how it shards)", file=sys.stderr)
+              "(the attention path runs on one GPU; it shards by heads across GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -57,6 +57,7 @@ const char *h3a_last_error(void);
  * rounded to bf16 before the PV product (as the reference kernel does,
  * attn_sm80/fa3_sm80_h3.cu:405-420).  Sq != Skv is allowed (pad path,
  * harness/sp_runtime.py:106-109).  scale > 0 (1/sqrt(128) for the DiT).
+ * The seq strides of k and v must be < 2^24 elements (H3A_ERR_UNSUPPORTED).
  * Replaces fa3_sm80_h3_launch (attn_sm80/fa3_sm80_h3.cu:460-470), which
  * ignored B, fixed the scale and launched on the legacy default stream.
  */

@@ -30,6 +30,8 @@ int check_launch(const char *what) {
 
 namespace {
 
+constexpr int64_t kMaxSeqStride = int64_t(1) << 24;
+
 bool strides_ok(const int64_t s[3]) {
   for (int i = 0; i < 3; ++i)
     if (s[i] < 0 || (s[i] & 7) != 0) return false;
@@ -52,6 +54,11 @@ int check_attn(const void *q, const void *k, const void *v, void *o, int B, int 
   if (!strides_ok(qs) || !strides_ok(ks) || !strides_ok(vs) || !strides_ok(os))
     return fail(H3A_ERR_ALIGNMENT, "strides must be non-negative multiples of 8 elements");
   if (Skv > INT_MAX - 256 || Sq > INT_MAX - 256) return fail(H3A_ERR_INVALID_ARG, "sequence too long");
+  // A 64-key stage of K or V is addressed with 32-bit byte offsets from the
+  // stage's first row (buffer range and per-lane offsets): 64 rows must span
+  // less than 2 GiB.
+  if (ks[2] >= kMaxSeqStride || vs[2] >= kMaxSeqStride)
+    return fail(H3A_ERR_UNSUPPORTED, "k/v sequence stride must be < %lld elements", (long long)kMaxSeqStride);
   return H3A_OK;
 }
 

@@ -95,7 +95,7 @@ def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int
     pooled score, no forced diagonal.  SLA centres k by its sequence mean
     first (smooth_k); that shifts every score of a query block by the same
     amount and cannot change which key blocks are kept, so the selection is
-    computed without it.  The BASELINE block-sparse workload uses
+    computed without it.  The H3 block-sparse workload (128x128 tiles, top 25 %) uses
     force_diag=True.  Pooling and selection run in libh3attn; ties are broken
     towards the lower key-block index.
     """

@@ -18,7 +18,7 @@ for p in (PKG, ORACLE):
     if p not in sys.path:
         sys.path.insert(0, p)
 
-# BASELINE tolerance for floating-point attention outputs, relative to the
+# Tolerance for floating-point attention outputs, relative to the
 # reference's absolute maximum: max |o - ref| <= 1e-2 * absmax(ref) and
 # mean |o - ref| <= 1e-3 * absmax(ref).
 MAX_REL = 1e-2
@@ -30,7 +30,7 @@ def pytest_configure(config):
 
 
 def assert_close_absmax(out, ref, max_rel=MAX_REL, mean_rel=MEAN_REL, what=""):
-    """BASELINE tolerance check on float arrays/tensors; returns (max_err, mean_err, absmax)."""
+    """Attention tolerance check on float arrays/tensors; returns (max_err, mean_err, absmax)."""
     o = np.asarray(out, dtype=np.float64)
     r = np.asarray(ref, dtype=np.float64)
     assert o.shape == r.shape, f"{what}: shape {o.shape} vs {r.shape}"

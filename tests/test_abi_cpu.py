@@ -55,6 +55,11 @@ def test_attn_argument_errors():
     assert _attn(L, q=24) == _lib.H3A_ERR_ALIGNMENT        # 8-byte aligned only
     assert _attn(L, qs=(0, 0, 12)) == _lib.H3A_ERR_ALIGNMENT  # row stride not a multiple of 8
     assert _attn(L, qs=(0, -8, 8)) == _lib.H3A_ERR_ALIGNMENT
+    z = S3(0, 0, 0)
+    big = S3(0, 0, 1 << 24)  # a 64-row K/V stage would not fit 32-bit byte offsets
+    assert L.h3a_attn_fwd(16, 16, 16, 16, 1, 1, 4, 4, 128, z, big, z, z, 0.1, None) == _lib.H3A_ERR_UNSUPPORTED
+    assert b"sequence stride" in L.h3a_last_error()
+    assert L.h3a_attn_fwd(16, 16, 16, 16, 1, 1, 4, 4, 128, z, z, big, z, 0.1, None) == _lib.H3A_ERR_UNSUPPORTED
 
 
 def test_blocksparse_argument_errors():

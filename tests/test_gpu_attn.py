@@ -68,15 +68,15 @@ def test_dense_vs_oracle(gpu, B, H, Sq, Skv):
     assert_close_absmax(o, oracle.attn_fwd(q, k, v, round_p=False), what="vs exact softmax")
 
 
-def test_dense_config1_vs_oracle_and_sdpa(gpu):
-    """B=1, H=4, S=2048, D=128, N(0,1) inputs, scale 1/sqrt(128)."""
+def test_dense_h4_s2048_vs_oracle_and_sdpa(gpu):
+    """B=1, H=4, S=2048, D=128, N(0,1) inputs, scale 1/sqrt(128) (the CPU-runnable case)."""
     rng = np.random.default_rng(2048)
     q, k, v = (randn_bf16(rng, (1, 4, 2048, 128)) for _ in range(3))
     o = _run(q, k, v, gpu)
-    assert_close_absmax(o, oracle.attn_fwd(q, k, v), what="config1 vs oracle")
+    assert_close_absmax(o, oracle.attn_fwd(q, k, v), what="H=4 S=2048 vs oracle")
     qt, kt, vt = (to_dev_bf16(x, gpu).float() for x in (q, k, v))
     sd = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt).cpu().numpy()
-    assert_close_absmax(o, sd, what="config1 vs fp32 SDPA")
+    assert_close_absmax(o, sd, what="H=4 S=2048 vs fp32 SDPA")
 
 
 @pytest.mark.parametrize("S", [1160, 4104])
@@ -173,7 +173,7 @@ def _ref_fp32_heads(q, k, v, heads, scale, chunk=4096):
 
 @pytest.mark.parametrize("H", [56, 14])
 def test_full_h3_shape(gpu, H):
-    """BASELINE configs 3/4: B=1, S=42120 (512+256+2048+39304), D=128, q,k ~ N(0,1), v ~ 4 N(0,1)."""
+    """H3 shape: B=1, S=42120 (512+256+2048+39304), D=128, H=56 and 14, q,k ~ N(0,1), v ~ 4 N(0,1)."""
     S = 42120
     g = torch.Generator(device=gpu).manual_seed(3)
     q = torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16)

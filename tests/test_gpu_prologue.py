@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 def _inputs(rng, S, H, spread=True):
     x = rng.standard_normal((2, S, H, 128)).astype(np.float32)
-    if spread:  # per-token dynamic range U(0.5, 4), as BASELINE config 2
+    if spread:  # per-token dynamic range U(0.5, 4), as in the S=8192 prologue workload
         x *= rng.uniform(0.5, 4.0, size=(2, S, 1, 1)).astype(np.float32)
     w = (1.0 + 0.05 * rng.standard_normal((2, 128))).astype(np.float32)
     return oracle.f32_to_bf16(x), oracle.f32_to_bf16(w)
@@ -83,8 +83,8 @@ def test_prologue_small(gpu, S, H, rot, fused):
     _compare(gk, rk[0], "k")
 
 
-def test_prologue_config2(gpu):
-    """S=8192, H=56 strided views of the fused QKV output, theta 10000."""
+def test_prologue_s8192_h56_fused_views(gpu):
+    """S=8192, H=56 strided views of the fused QKV output, theta 10000, rot 128."""
     S, H = 8192, 56
     rng = np.random.default_rng(8192)
     x, w = _inputs(rng, S, H)
