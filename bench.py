@@ -84,11 +84,13 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--workload", default="dense",
-                    choices=["dense", "h14", "sparse", "prologue", "fused"],
+                    choices=["dense", "h14", "sparse", "prologue", "fused", "graph"],
                     help="dense: the headline (H=56, S=42120, 50 layers); h14: one GPU's share of "
                          "4-way head parallelism (H=14); sparse: block-sparse top-25%%+diagonal at "
                          "128x128 tiles; prologue: qk-RMSNorm+RoPE at S=8192, H=56 (GB/s); fused: "
-                         "prologue + attention on the fused QKV layout at S=8192, H=56")
+                         "prologue + attention on the fused QKV layout at S=8192, H=56; graph: "
+                         "--layers layers of prologue + attention at S=2048, H=4, eager vs one "
+                         "HIP-graph replay (launch overhead)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run one device copy of this many MiB "
@@ -345,6 +347,47 @@ def run_fused(args, torch, h3attn, dev):
     return res
 
 
+def run_graph(args, torch, h3attn, dev):
+    """Launch overhead of a layer sequence: `--layers` layers of in-place prologue + dense
+    attention on the fused QKV layout at S=2048, H=4 (per-layer GPU work of tens of
+    microseconds), run eagerly from Python and as one HIP-graph replay (h3attn.graphs)."""
+    from h3attn import graphs
+
+    s_len, heads, rot = 2048, 4, 128
+    rope = h3attn.rope_freqs(s_len, rot, device=dev)
+    layers = []
+    for i in range(args.layers):
+        qkv, qw, kw = _prologue_inputs(torch, dev, s_len, heads, 100 + i)
+        layers.append({"qkv": qkv, "rope": rope, "qw": qw, "kw": kw})
+    # The prologue renormalises its inputs in place every pass; RMSNorm keeps them bounded,
+    # so repeated passes are valid timing input.
+    seq = graphs.LayerSequence(layers, heads=heads)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps
+
+    eager_s = timed(seq.run)
+    seq.capture(warmup=1)
+    graph_s = timed(seq.replay)
+    fl = flops_per_layer(h=heads, s=s_len) * args.layers
+    res = _base(args, f"HIP-graph replay of {args.layers} layers (prologue + attention) at S=2048,H=4: "
+                      "attention TFLOP/s", fl / graph_s / 1e12, "TFLOP/s", graph_s * 1e3,
+                {"workload": f"{args.layers} x (in-place prologue + dense attention) on fused [S,3HD] "
+                             "views, one HIP graph", "S": s_len, "H": heads, "D": D, "rot_dim": rot})
+    res.update({"ms_per_step_eager": round(eager_s * 1e3, 3), "ms_per_step_graph": round(graph_s * 1e3, 3),
+                "us_per_layer_eager": round(eager_s * 1e6 / args.layers, 1),
+                "us_per_layer_graph": round(graph_s * 1e6 / args.layers, 1),
+                "graph_speedup": round(eager_s / graph_s, 2)})
+    return res
+
+
 def cpu_prologue_baseline(torch, s_len, rot):
     """A torch fp32 CPU restatement of the prologue (the reference has no CPU path)."""
     threads = os.cpu_count() or 1
@@ -393,6 +436,8 @@ def main():
         res = run_sparse(args, torch, h3attn, dev)
     elif args.workload == "prologue":
         res = run_prologue(args, torch, h3attn, dev)
+    elif args.workload == "graph":
+        res = run_graph(args, torch, h3attn, dev)
     else:
         res = run_fused(args, torch, h3attn, dev)
     print(json.dumps(res), flush=True)

@@ -1,7 +1,8 @@
 """h3attn - MI355X (gfx950) exact attention path of the MiniMax-H3 video DiT.
 
 Python side of libh3attn: tensor entry points (ops), the block-sparse h3_sla
-path (sla), the ComfyUI drop-in hooks (hooks) and RoPE tables (rope).  All
+path (sla), the ComfyUI drop-in hooks (hooks), RoPE tables (rope), HIP-graph
+capture of layer sequences (graphs) and per-component timing (profiling).  All
 arithmetic happens in the HIP kernels of libh3attn.so; nothing here computes
 attention on the CPU.
 """

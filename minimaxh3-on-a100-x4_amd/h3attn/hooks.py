@@ -29,7 +29,7 @@ from typing import Callable
 
 import torch
 
-from . import ops, sla
+from . import ops, profiling, sla
 
 _state = threading.local()
 
@@ -174,50 +174,59 @@ def _weight(p, device):
 
 
 def make_attention_forward(orig_forward, prologue: Callable = ops.rms_rope_split_half_,
-                           attention: Callable = hip_optimized_attention):
-    """Build a replacement Attention.forward; `orig_forward` handles rope_freqs=None."""
+                           attention: Callable = hip_optimized_attention, timer=None):
+    """Build a replacement Attention.forward; `orig_forward` handles rope_freqs=None.
+
+    With a `timer` (h3attn.profiling.OpTimer) the four sub-operations are
+    timed under the reference profiler's component names
+    (custom_nodes/h3_profiler/__init__.py:98-115) whenever the timer is armed.
+    """
+    mark = timer.mark if timer is not None else profiling.passthrough
 
     def forward(self, x, rope_freqs=None, transformer_options={}):
         if rope_freqs is None:
             return orig_forward(self, x, rope_freqs=rope_freqs, transformer_options=transformer_options)
         s = x.shape[0]
         H, D = self.heads, self.head_dim
-        qkv = self.qkv_proj(x)
+        qkv = mark("attn.qkv", self.qkv_proj, x)
         q, k, v = qkv.split(H * D, dim=-1)
         q = q.view(1, s, H, D)
         k = k.view(1, s, H, D)
         rot = rope_freqs.shape[-3] * 2
-        prologue(q, k, rope_freqs, _weight(self.q_norm.weight, x.device),
-                 _weight(self.k_norm.weight, x.device), epsilon=self.q_norm.eps, rot_dim=rot)
+        mark("attn.qknorm_rope", prologue, q, k, rope_freqs, _weight(self.q_norm.weight, x.device),
+             _weight(self.k_norm.weight, x.device), epsilon=self.q_norm.eps, rot_dim=rot)
         qh = q.transpose(1, 2)
         kh = k.transpose(1, 2)
         vh = v.view(1, s, H, D).transpose(1, 2)
         override = (transformer_options or {}).get("optimized_attention_override")
         if override is not None:
-            out = override(attention, qh, kh, vh, H, mask=None, skip_reshape=True,
-                           transformer_options=transformer_options)
+            out = mark("attn.softmax", override, attention, qh, kh, vh, H, mask=None, skip_reshape=True,
+                       transformer_options=transformer_options)
         else:
-            out = attention(qh, kh, vh, H, mask=None, skip_reshape=True,
-                            transformer_options=transformer_options)
-        return self.out_proj(out.reshape(s, H * D))
+            out = mark("attn.softmax", attention, qh, kh, vh, H, mask=None, skip_reshape=True,
+                       transformer_options=transformer_options)
+        return mark("attn.out", self.out_proj, out.reshape(s, H * D))
 
     forward._h3attn_patched = True
     forward._h3attn_orig = orig_forward
+    forward._h3attn_timer = timer
     return forward
 
 
 def install(attention_cls=None, prologue: Callable = ops.rms_rope_split_half_,
-            attention: Callable = hip_optimized_attention) -> bool:
+            attention: Callable = hip_optimized_attention, timer=None) -> bool:
     """Patch Attention.forward (comfy.ldm.minimax.model.Attention by default); idempotent.
 
-    Returns True when a patch was installed, False when it already was.
+    `timer`: optional h3attn.profiling.OpTimer that times the sub-operations
+    while armed.  Returns True when a patch was installed, False when it
+    already was.
     """
     if attention_cls is None:
         import comfy.ldm.minimax.model as mm  # ComfyUI is optional: imported only here
         attention_cls = mm.Attention
     if getattr(attention_cls.forward, "_h3attn_patched", False):
         return False
-    attention_cls.forward = make_attention_forward(attention_cls.forward, prologue, attention)
+    attention_cls.forward = make_attention_forward(attention_cls.forward, prologue, attention, timer)
     return True
 
 

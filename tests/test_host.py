@@ -193,3 +193,64 @@ def test_sla_override_scope_schedule_and_fallback():
         m(x, transformer_options=opts)
     assert logs == [] and seen["in_scope"] is False
     assert sched.keep_for(None) == sched.default_keep and sched.keep_for(99) == sched.default_keep
+
+
+# ----------------------------------------------------------------------------- per-component timing
+class _FakeEvent:
+    """record() stamps a shared tick counter; elapsed_time is the tick difference."""
+    clock = [0]
+
+    def record(self):
+        _FakeEvent.clock[0] += 1
+        self.t = _FakeEvent.clock[0]
+
+    def elapsed_time(self, other):
+        return float(other.t - self.t)
+
+
+def test_op_timer_bookkeeping():
+    from h3attn import profiling
+    syncs = []
+    t = profiling.OpTimer(event_factory=_FakeEvent, synchronize=lambda: syncs.append(1))
+    assert t.mark("x", lambda a: a + 1, 1) == 2  # disarmed: plain call, nothing recorded
+    assert t.report()["components_ms"] == {}
+    t.arm()
+    t.mark("attn.qkv", lambda: None)
+    t.mark("attn.softmax", lambda: [e.record() for e in (_FakeEvent(), _FakeEvent())])  # 2 inner ticks
+    t.mark("attn.qkv", lambda: None)
+    t.disarm()
+    t.mark("attn.qkv", lambda: None)  # not counted
+    rep = t.report(total_ms=10.0)
+    assert rep["calls"] == {"attn.qkv": 2, "attn.softmax": 1}
+    assert rep["components_ms"] == {"attn.qkv": 2.0, "attn.softmax": 3.0}
+    assert rep["sum_components_ms"] == 5.0 and rep["other_ms"] == 5.0
+    assert rep["components_pct"] == {"attn.qkv": 20.0, "attn.softmax": 30.0}
+    assert syncs
+    t.arm()  # a new measurement starts empty
+    assert t.report()["components_ms"] == {}
+
+
+def test_patched_forward_marks_reference_components():
+    from h3attn import profiling
+
+    class A(standin_dit.Attention):
+        pass
+
+    m = _model(3)
+    m.__class__ = A
+    x = torch.randn(12, 256)
+    rope = h3attn.rope_freqs(12, 128)
+    timer = profiling.OpTimer(event_factory=_FakeEvent, synchronize=lambda: None)
+    with torch.no_grad():
+        want = m(x, rope_freqs=rope)
+        assert hooks.install(A, prologue=standin_dit.rms_rope_split_half_, attention=_cpu_attention,
+                             timer=timer)
+        got_idle = m(x, rope_freqs=rope)
+        timer.arm()
+        got = m(x, rope_freqs=rope)
+        m(x, rope_freqs=rope)
+        timer.disarm()
+        hooks.uninstall(A)
+    assert torch.equal(got, want) and torch.equal(got_idle, want)
+    rep = timer.report()
+    assert rep["calls"] == {c: 2 for c in profiling.COMPONENTS}
