@@ -56,6 +56,14 @@ namespace h3a {
 #ifndef H3A_DENSE_PINGPONG
 #define H3A_DENSE_PINGPONG 1
 #endif
+// Row max / row sum of a stage as trees instead of dependent chains.
+#ifndef H3A_TREE_REDUCE
+#define H3A_TREE_REDUCE 1
+#endif
+// Keep each softmax cluster's results inside its own slot (see pin()).
+#ifndef H3A_PP_PIN_SOFTMAX
+#define H3A_PP_PIN_SOFTMAX 1
+#endif
 // Block-sparse path with 128-row query blocks: ping-pong kernel over pairs of
 // query blocks instead of attn_fwd_kernel<4, PadLayout, ...>.
 #ifndef H3A_SPARSE_PINGPONG
@@ -281,11 +289,48 @@ __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[
 
 // Row max of a masked score tile (both 32-key halves, both lane halves), in
 // scale*log2(e) units.
+// Both reductions are trees (depth 4-5) rather than 16-long dependent chains:
+// the softmax cluster is latency-bound, not issue-bound.
 __device__ __forceinline__ float tile_max(const f32x16 &s0, const f32x16 &s1, float sl2) {
+#if H3A_TREE_REDUCE
+  float a[11];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {  // 30 of the 32 values, three at a time
+    const int u = 3 * i;
+    const float x = u < 16 ? s0[u] : s1[u - 16];
+    const float y = u + 1 < 16 ? s0[u + 1] : s1[u + 1 - 16];
+    const float z = u + 2 < 16 ? s0[u + 2] : s1[u + 2 - 16];
+    a[i] = fmaxf(fmaxf(x, y), z);
+  }
+  a[10] = fmaxf(s1[14], s1[15]);
+  const float b0 = fmaxf(fmaxf(a[0], a[1]), a[2]), b1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
+  const float b2 = fmaxf(fmaxf(a[6], a[7]), a[8]), b3 = fmaxf(a[9], a[10]);
+  const float mx = fmaxf(fmaxf(b0, b1), fmaxf(b2, b3));
+#else
   float mx = kNegInf;
 #pragma unroll
   for (int r = 0; r < 16; ++r) mx = fmaxf(fmaxf(mx, s0[r]), s1[r]);
+#endif
   return half_swap_max(mx) * sl2;
+}
+
+// This lane's share of the row sum of a stage's p values.
+__device__ __forceinline__ float tile_sum(const f32x16 &s0, const f32x16 &s1) {
+#if H3A_TREE_REDUCE
+  float a[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) a[r] = s0[r] + s1[r];
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int r = 0; r < w; ++r) a[r] += a[r + w];
+  return a[0];
+#else
+  float rs = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
+  return rs;
+#endif
 }
 
 // Keys >= Skv of the stage starting at key0 -> -inf (tail stage only).
@@ -454,10 +499,7 @@ attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) lsum = dot2_bf16_ones(pf[ks][c], lsum);
 #else
-    float rs = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
-    lsum += rs;
+    lsum += tile_sum(s0, s1);
 #endif
     pv_tile<L>(vbuf[P], pf, v_rd, o);
     s0 = n0;
@@ -525,11 +567,16 @@ __device__ __forceinline__ void softmax_stage(f32x16 &s0, f32x16 &s1, int key0, 
     s1[r] = fast_exp2(fmaf(s1[r], sl2, -muse));
   }
   pack_p(s0, s1, pf);
-  float rs = 0.f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
-  lsum += rs;
+  lsum += tile_sum(s0, s1);
 }
+
+// Pin values to this point of the program: an empty volatile asm that reads
+// and rewrites them.  Everything they depend on must be computed before it,
+// and volatile asm keeps its place relative to the workgroup barriers.  Without
+// it the compiler sinks softmax arithmetic (exp2, packing, the row sum) past a
+// barrier toward the MFMAs that consume it, into the other cluster's slot.
+__device__ __forceinline__ void pin(float &x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(u32x4 &x) { asm volatile("" : "+v"(x)); }
 
 // Workgroup barrier that the instruction scheduler does not move work across.
 __device__ __forceinline__ void slot_barrier() {
@@ -701,7 +748,14 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 #endif
     __builtin_amdgcn_s_setprio(0);
   };
-  auto soft = [&](int j) { softmax_stage(s0, s1, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf); };
+  auto soft = [&](int j) {
+    softmax_stage(s0, s1, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
+#if H3A_PP_PIN_SOFTMAX
+    for (int i = 0; i < 4; ++i) pin(pf[i]);
+    pin(lsum);
+    pin(m);
+#endif
+  };
 
   if (lead) {
     auto stage = [&](auto par, int j) {
