@@ -92,6 +92,9 @@ def _parse():
                          "--layers layers of prologue + attention at S=2048, H=4, eager vs one "
                          "HIP-graph replay (launch overhead)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-split-tail", action="store_true",
+                    help="dense: run h3a_attn_fwd (never splits the last round of tiles) instead of "
+                         "h3a_attn_fwd_ws")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run one device copy of this many MiB "
                          "(reference kernel for scaling FETCH_SIZE/WRITE_SIZE counters)")
@@ -149,7 +152,7 @@ def run_dense(args, torch, h3attn, dev, heads=H):
         for layer in range(L):
             if events is not None:
                 events[layer][0].record(stream)
-            h3attn.attn_fwd(qs[layer], ks[layer], vs[layer], out=out)
+            h3attn.attn_fwd(qs[layer], ks[layer], vs[layer], out=out, split_tail=not args.no_split_tail)
             if events is not None:
                 events[layer][1].record(stream)
 
@@ -174,7 +177,7 @@ def run_dense(args, torch, h3attn, dev, heads=H):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES if heads == H else None,
-                     "kernel": "attn_fwd_pingpong_kernel", "flop_per_launch": fpl,
+                     "kernel": "attn_fwd_pingpong_kernel (+ split_combine_kernel for the split tail)", "flop_per_launch": fpl,
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     })
     if not args.no_cpu_baseline:

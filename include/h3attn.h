@@ -28,6 +28,7 @@
 #ifndef H3ATTN_H
 #define H3ATTN_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -66,6 +67,27 @@ int h3a_attn_fwd(const void *q, const void *k, const void *v, void *o,
                  const int64_t q_strides[3], const int64_t k_strides[3],
                  const int64_t v_strides[3], const int64_t o_strides[3],
                  float scale, h3a_stream_t stream);
+
+/*
+ * h3a_attn_fwd with a caller-supplied device workspace (no allocation in the
+ * library).  With it, the query tiles of the last, partly filled round of
+ * workgroups are split into key ranges that run side by side and are merged
+ * by a second kernel on the same stream; results equal h3a_attn_fwd's within
+ * floating-point rounding.  h3a_attn_fwd_workspace_size gives the bytes
+ * needed for a problem on the current device (0: nothing is split, and
+ * workspace may be NULL).  The workspace must stay untouched until the call's
+ * work on `stream` has completed, and two calls in flight at once need two
+ * workspaces.  Same arguments and errors as h3a_attn_fwd, plus
+ * H3A_ERR_INVALID_ARG for a missing or short workspace.  This entry point has
+ * no counterpart in the reference; h3a_attn_fwd is the drop-in for
+ * fa3_sm80_h3_launch.
+ */
+int h3a_attn_fwd_workspace_size(int B, int H, int Sq, int Skv, int D, size_t *bytes);
+int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o,
+                    int B, int H, int Sq, int Skv, int D,
+                    const int64_t q_strides[3], const int64_t k_strides[3],
+                    const int64_t v_strides[3], const int64_t o_strides[3],
+                    float scale, void *workspace, size_t workspace_bytes, h3a_stream_t stream);
 
 /*
  * Block-sparse attention forward (h3_sla path, custom_nodes/h3_sla/__init__.py:226-235).

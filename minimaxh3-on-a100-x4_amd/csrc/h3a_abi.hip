@@ -76,6 +76,7 @@ void fill_attn_args(AttnArgs &a, const void *q, const void *k, const void *v, vo
   a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv;
   a.sl2 = scale * 1.4426950408889634f;
   a.lut = nullptr; a.counts = nullptr; a.lut_stride = 0; a.sub = 1; a.blk_k = 64;
+  a.split_first = INT_MAX; a.split_pieces = 1; a.ws = nullptr;
 }
 
 }  // namespace
@@ -99,6 +100,40 @@ int h3a_attn_fwd(const void *q, const void *k, const void *v, void *o, int B, in
   AttnArgs a;
   fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
   return launch_attn_dense(a, as_stream(stream));
+}
+
+int h3a_attn_fwd_workspace_size(int B, int H, int Sq, int Skv, int D, size_t *bytes) {
+  clear_error();
+  if (!bytes) return fail(H3A_ERR_INVALID_ARG, "null output pointer");
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
+  if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
+  SplitPlan plan;
+  const int rc = plan_attn_split(B, H, Sq, Skv, &plan);
+  if (rc) return rc;
+  *bytes = plan.bytes;
+  return H3A_OK;
+}
+
+int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o, int B, int H, int Sq, int Skv,
+                    int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                    const int64_t v_strides[3], const int64_t o_strides[3], float scale,
+                    void *workspace, size_t workspace_bytes, h3a_stream_t stream) {
+  clear_error();
+  int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
+  if (rc) return rc;
+  SplitPlan plan;
+  rc = plan_attn_split(B, H, Sq, Skv, &plan);
+  if (rc) return rc;
+  if (plan.pieces > 1) {
+    if (!workspace || workspace_bytes < plan.bytes)
+      return fail(H3A_ERR_INVALID_ARG, "workspace of %zu bytes needed, %zu given", plan.bytes,
+                  workspace ? workspace_bytes : (size_t)0);
+    if (!aligned16(workspace)) return fail(H3A_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+  }
+  AttnArgs a;
+  fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
+  return launch_attn_dense_split(a, plan, workspace, as_stream(stream));
 }
 
 int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o, int B, int H,

@@ -29,6 +29,7 @@
 //  * exp2-based softmax with scale*log2(e) folded into one FMA; the running
 //    max is refreshed only when a row outgrows it by 2^8 (lazy rescale).
 //  * Workgroup ids are remapped XCD-aware (xcd_remap).
+#include <atomic>
 #include <climits>
 #include <type_traits>
 
@@ -621,11 +622,25 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const bool lead = wave_u < NW / 2;  // group A
+  // Work item of this workgroup.  Dense with a split tail: the first
+  // a.split_first items are whole query tiles; each later tile is cut into
+  // a.split_pieces contiguous key ranges, one per workgroup, whose partial
+  // results are merged by split_combine_kernel.
+  int w, piece = -1, j0 = 0, j_end = 0;
+  if (kSparse || (int)blockIdx.x < a.split_first) {
+    const int whole = kSparse ? a.total : (a.split_first < a.total ? a.split_first : a.total);
 #if H3A_XCD_REMAP
-  const int w = xcd_remap(blockIdx.x, a.total);
+    w = xcd_remap(blockIdx.x, whole);
 #else
-  const int w = blockIdx.x;
+    w = blockIdx.x;
 #endif
+  } else {
+    piece = blockIdx.x - a.split_first;
+    w = a.split_first + piece / a.split_pieces;
+    const int p = piece % a.split_pieces, n = (a.Skv + kBN - 1) / kBN;
+    j0 = (int)((int64_t)n * p / a.split_pieces);
+    j_end = (int)((int64_t)n * (p + 1) / a.split_pieces);
+  }
   // Query tiles per (b,h) in units of this workgroup: 256-row tiles (dense) or
   // pairs of 128-row blocks (sparse, a.nqt blocks).
   const int wg_tiles = kSparse ? (a.nqt + 1) / 2 : a.nqt;
@@ -654,7 +669,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
     qrow = qb * 128 + (wave & 3) * 32 + l32;
   } else {
-    niter = (a.Skv + kBN - 1) / kBN;  // >= 1
+    niter = piece < 0 ? (a.Skv + kBN - 1) / kBN : j_end - j0;  // >= 1
     niter_wg = niter;
     qrow = qt * 256 + wave * 32 + l32;
   }
@@ -667,7 +682,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       const int key0 = kb * a.blk_k + (j % a.sub) * kBN;
       return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
     } else {
-      return j * kBN;
+      return (j0 + j) * kBN;
     }
   };
 
@@ -792,6 +807,24 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   }
 
   const float ltot = half_swap_sum(lsum);
+  if (!kSparse && piece >= 0) {
+    // Partial result of one key range: unnormalised O, the reference max m
+    // it is relative to (scale*log2(e) units) and the row sum, for all 256
+    // rows of the tile (rows past Sq included; the combine skips them).
+    const int row = wave * 32 + l32;
+    float *po = a.ws + ((int64_t)piece * 256 + row) * kD + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        *(float4 *)(po + dt * 32 + 8 * rr) =
+            float4{o[dt][4 * rr + 0], o[dt][4 * rr + 1], o[dt][4 * rr + 2], o[dt][4 * rr + 3]};
+    if (g == 0) {
+      float *pml = a.ws + (int64_t)(a.total - a.split_first) * 256 * kD + ((int64_t)piece * 256 + row) * 2;
+      *(float2 *)pml = float2{m, ltot};
+    }
+    return;
+  }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
   if (qrow < a.Sq) {
     uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
@@ -805,6 +838,41 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       }
     }
   }
+}
+
+// Merge the key-range pieces of the split tiles:
+//   O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p,  M = max_p m_p.
+// One thread per (split tile, row, 4 dims); 8 rows per 256-thread block.
+__global__ void __launch_bounds__(256) split_combine_kernel(AttnArgs a) {
+  const int ntiles = (a.total - a.split_first) / a.split_pieces;
+  const int64_t item = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);  // (split tile, row)
+  if (item >= (int64_t)ntiles * 256) return;
+  const int t = (int)(item / 256), row = (int)(item % 256), d = 4 * (threadIdx.x & 31);
+  const int tile = a.split_first + t;
+  const int qt = tile % a.nqt, bh = tile / a.nqt;
+  const int h = bh % a.H, b = bh / a.H;
+  const int qrow = qt * 256 + row;
+  if (qrow >= a.Sq) return;
+  const int P = a.split_pieces;
+  const float *ml = a.ws + (int64_t)(a.total - a.split_first) * 256 * kD;
+  float M = kNegInf;
+  for (int p = 0; p < P; ++p) M = fmaxf(M, ml[((int64_t)(t * P + p) * 256 + row) * 2]);
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+  for (int p = 0; p < P; ++p) {
+    const int64_t pr = (int64_t)(t * P + p) * 256 + row;
+    const float mp = ml[pr * 2], lp = ml[pr * 2 + 1];
+    const float wgt = (mp == kNegInf) ? 0.f : fast_exp2(mp - M);
+    const float4 op = *(const float4 *)(a.ws + pr * kD + d);
+    acc.x = fmaf(wgt, op.x, acc.x);
+    acc.y = fmaf(wgt, op.y, acc.y);
+    acc.z = fmaf(wgt, op.z, acc.z);
+    acc.w = fmaf(wgt, op.w, acc.w);
+    L = fmaf(wgt, lp, L);
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  uint16_t *po = a.o + b * a.osb + h * a.osh + (int64_t)qrow * a.oss + d;
+  *(u32x2 *)po = u32x2{pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv)};
 }
 
 // ---------------------------------------------------------------------------
@@ -899,6 +967,58 @@ int launch_attn_dense(AttnArgs a, hipStream_t s) {
   hipLaunchKernelGGL((attn_fwd_kernel<NW, DenseLayout, false, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
 #endif
   return check_launch("attn_fwd_kernel<dense>");
+}
+
+// Split-tail plan.  With one workgroup per CU, N whole 256-row tiles run in
+// ceil(N / CUs) rounds and the last round keeps only N % CUs CUs busy (all of
+// the chip idles but N for N < CUs).  Those r tiles are cut into P key
+// ranges each, P = CUs / r (at least kMinSplitStages 64-key stages per
+// range), so the last round is ~1/P as long.
+int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
+  constexpr int kMinSplitStages = 4;
+  static std::atomic<int> cu_cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(H3A_ERR_HIP, "hipGetDevice failed");
+  int cus = (dev >= 0 && dev < 64) ? cu_cache[dev].load(std::memory_order_relaxed) : 0;
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      return fail(H3A_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
+    if (dev >= 0 && dev < 64) cu_cache[dev].store(cus, std::memory_order_relaxed);
+  }
+  const int64_t tiles = (int64_t)B * H * ((Sq + 255) / 256);
+  const int stages = (Skv + kBN - 1) / kBN;
+  const int64_t r = tiles >= cus ? tiles % cus : tiles;
+  int pieces = 1;
+  if (H3A_DENSE_PINGPONG && r > 0) {
+    const int64_t by_cus = cus / r, by_len = stages / kMinSplitStages;
+    pieces = (int)(by_cus < by_len ? by_cus : by_len);
+  }
+  if (tiles > INT_MAX || pieces < 2) {
+    *plan = SplitPlan{(int)(tiles > INT_MAX ? INT_MAX : tiles), (int)(tiles > INT_MAX ? INT_MAX : tiles), 1, 0};
+    return H3A_OK;
+  }
+  plan->tiles = (int)tiles;
+  plan->first = (int)(tiles - r);
+  plan->pieces = pieces;
+  plan->bytes = (size_t)r * pieces * 256 * (kD + 2) * sizeof(float);
+  return H3A_OK;
+}
+
+int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s) {
+  if (plan.pieces < 2) return launch_attn_dense(a, s);
+  a.nqt = (a.Sq + 255) / 256;
+  a.split_first = plan.first;
+  a.split_pieces = plan.pieces;
+  a.ws = static_cast<float *>(ws);
+  const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
+  if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
+  a.total = (int)total;
+  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<false, DenseLayout>), dim3(a.total), dim3(512), 0, s, a);
+  int rc = check_launch("attn_fwd_pingpong_kernel<split>");
+  if (rc) return rc;
+  const int64_t rows = (int64_t)(plan.tiles - plan.first) * 256;
+  hipLaunchKernelGGL(split_combine_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, a);
+  return check_launch("split_combine_kernel");
 }
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {

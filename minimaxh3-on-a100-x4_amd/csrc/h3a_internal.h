@@ -37,10 +37,25 @@ struct AttnArgs {
   int lut_stride;  // max_k_blocks
   int sub;         // 64-key stages per key block (blk_k / 64)
   int blk_k;
+  // dense split tail (see launch_attn_dense): work items >= split_first are
+  // cut into split_pieces key ranges whose partial results go to ws
+  int split_first;
+  int split_pieces;
+  float *ws;
+};
+
+// Dense split-tail plan for a problem on the current device.
+struct SplitPlan {
+  int tiles;    // B*H*query tiles
+  int first;    // tiles run whole (the rest are split)
+  int pieces;   // key ranges per split tile (1: no split)
+  size_t bytes; // workspace bytes
 };
 
 // Launchers implemented in h3a_attn.hip / h3a_prologue.hip.
 int launch_attn_dense(AttnArgs a, hipStream_t s);  // sets nqt/total from its tile height
+int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan);
+int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s);
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s);
 int launch_block_map_to_lut(const uint8_t *map, int B, int H, int nq, int nk, int32_t *lut,
                             int32_t *counts, int max_k_blocks, hipStream_t s);

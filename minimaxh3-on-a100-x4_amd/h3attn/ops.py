@@ -76,19 +76,39 @@ def _prepare_attn(q, k, v, out):
     return q, k, v, out, (B, H, Sq, Skv, D)
 
 
+def attn_workspace_bytes(B: int, H: int, Sq: int, Skv: int, D: int = HEAD_DIM) -> int:
+    """Workspace bytes h3a_attn_fwd_ws needs on the current device (0: no split)."""
+    n = ctypes.c_size_t(0)
+    check("h3a_attn_fwd_workspace_size", lib().h3a_attn_fwd_workspace_size(B, H, Sq, Skv, D, ctypes.byref(n)))
+    return int(n.value)
+
+
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None, split_tail: bool = True) -> torch.Tensor:
     """Dense non-causal attention, q [B,H,Sq,128], k/v [B,H,Skv,128] bf16 -> [B,H,Sq,128].
 
     Any strides with a unit last dimension are read in place (e.g. the
     [1,H,S,D] transposed views of a fused QKV projection); `out` may also be a
     strided view (e.g. [1,S,H,D] memory seen as [1,H,S,D]).
+
+    split_tail: run through h3a_attn_fwd_ws with a workspace from torch's
+    allocator on q's stream, so the last partly filled round of workgroups is
+    split along the keys (equal results up to rounding); False runs
+    h3a_attn_fwd, which never splits.
     """
     q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
     sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    rc = lib().h3a_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                            B, H, Sq, Skv, D, _bhs(q), _bhs(k), _bhs(v), _bhs(out), sc, _stream(q))
-    check("h3a_attn_fwd", rc)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            B, H, Sq, Skv, D, _bhs(q), _bhs(k), _bhs(v), _bhs(out), sc)
+    with torch.cuda.device(q.device):
+        nbytes = attn_workspace_bytes(B, H, Sq, Skv, D) if split_tail else 0
+        if nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+            rc = lib().h3a_attn_fwd_ws(*args, ws.data_ptr(), nbytes, _stream(q))
+            check("h3a_attn_fwd_ws", rc)
+        else:
+            rc = lib().h3a_attn_fwd(*args, _stream(q))
+            check("h3a_attn_fwd", rc)
     return out
 
 

@@ -137,3 +137,18 @@ def test_python_check_raises_typed_errors():
         _lib.check("h3a_attn_fwd", rc)
     with pytest.raises(_lib.H3AError):
         _lib.check("h3a_attn_fwd", _lib.H3A_ERR_HIP)
+
+
+def test_workspace_entry_points_argument_errors():
+    """h3a_attn_fwd_ws / h3a_attn_fwd_workspace_size reject bad arguments before any HIP call."""
+    L = _lib.lib()
+    n = ctypes.c_size_t(123)
+    assert L.h3a_attn_fwd_workspace_size(1, 1, 4, 4, 128, None) == _lib.H3A_ERR_INVALID_ARG
+    assert L.h3a_attn_fwd_workspace_size(1, 0, 4, 4, 128, ctypes.byref(n)) == _lib.H3A_ERR_INVALID_ARG
+    assert L.h3a_attn_fwd_workspace_size(1, 1, 4, 4, 64, ctypes.byref(n)) == _lib.H3A_ERR_UNSUPPORTED
+    assert n.value == 123  # untouched on error
+    z = S3(0, 0, 0)
+    ws = L.h3a_attn_fwd_ws
+    assert ws(None, 16, 16, 16, 1, 1, 4, 4, 128, z, z, z, z, 0.1, None, 0, None) == _lib.H3A_ERR_INVALID_ARG
+    assert ws(16, 16, 16, 16, 1, 1, 4, 4, 64, z, z, z, z, 0.1, None, 0, None) == _lib.H3A_ERR_UNSUPPORTED
+    assert ws(16, 16, 16, 16, 1, 1, 4, 4, 128, S3(0, 0, 12), z, z, z, 0.1, None, 0, None) == _lib.H3A_ERR_ALIGNMENT

@@ -58,14 +58,15 @@ def test_sparse_vs_masked_oracle(gpu, blk, S, H):
 
 @pytest.mark.parametrize("blk_k", [64, 128])
 def test_all_blocks_kept_equals_dense(gpu, blk_k):
-    """A full block map visits the key stages in the dense order: bit-identical output."""
+    """A full block map visits the key stages in the dense order: bit-identical output
+    to the unsplit dense kernel (h3a_attn_fwd)."""
     rng = np.random.default_rng(21)
     S = 1000
     q, k, v = (to_dev_bf16(randn_bf16(rng, (1, 2, S, 128)), gpu) for _ in range(3))
     nq, nk = -(-S // 128), -(-S // blk_k)
     lut, cnt = h3attn.block_map_to_lut(torch.ones(1, 2, nq, nk, dtype=torch.uint8, device=gpu))
     o_s = h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, 128, blk_k)
-    o_d = h3attn.attn_fwd(q, k, v)
+    o_d = h3attn.attn_fwd(q, k, v, split_tail=False)
     torch.cuda.synchronize()
     assert torch.equal(o_s, o_d)
 
