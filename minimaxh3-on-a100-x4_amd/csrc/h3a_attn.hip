@@ -57,26 +57,22 @@ namespace h3a {
 #ifndef H3A_DENSE_PINGPONG
 #define H3A_DENSE_PINGPONG 1
 #endif
-// Row max / row sum of a stage as trees instead of dependent chains.
-#ifndef H3A_TREE_REDUCE
-#define H3A_TREE_REDUCE 1
-#endif
 // Keep each softmax cluster's results inside its own slot (see pin()).
 #ifndef H3A_PP_PIN_SOFTMAX
 #define H3A_PP_PIN_SOFTMAX 1
 #endif
-// Block-sparse path with 128-row query blocks: ping-pong kernel over pairs of
-// query blocks instead of attn_fwd_kernel<4, PadLayout, ...>.
-#ifndef H3A_SPARSE_PINGPONG
-#define H3A_SPARSE_PINGPONG 0
-#endif
-// LDS stage layout (0: SwzLayout, 1: PadLayout) of the dense kernels and of
-// the block-sparse ping-pong kernel.
+// LDS stage layout of the dense kernels (0: SwzLayout, 1: PadLayout).
 #ifndef H3A_DENSE_LAYOUT
 #define H3A_DENSE_LAYOUT 0
 #endif
-#ifndef H3A_SPARSE_LAYOUT
-#define H3A_SPARSE_LAYOUT 1
+// Keys per stage of the dense ping-pong kernel (64 or 128).
+#ifndef H3A_DENSE_BN
+#define H3A_DENSE_BN 64
+#endif
+// Ping-pong matrix cluster: PV of the current stage before the next stage's
+// scores (P's registers die before the new scores are written).
+#ifndef H3A_PP_PV_FIRST
+#define H3A_PP_PV_FIRST 0
 #endif
 // Block-sparse attn_fwd_kernel: K/V staged through VGPRs (1) or by LDS DMA (0).
 #ifndef H3A_SPARSE_REGS
@@ -149,24 +145,25 @@ struct PadLayout {
   __device__ __forceinline__ static int v_off(int vb, int dt) { return vb + 64 * dt; }
 };
 
-template <class L>
+template <class L, int ROWS = kBN>
 struct StageBytes {
-  static constexpr int kK = kBN * L::kKRow;
-  static constexpr int kV = kBN * L::kVRow;
+  static constexpr int kK = ROWS * L::kKRow;
+  static constexpr int kV = ROWS * L::kVRow;
 };
 
-// Global -> LDS staging of one 64-key K or V stage by LDS DMA.  Instruction t
-// fills the 64 consecutive 16-byte slots 64t..64t+63 of the stage (1 KiB);
+// Global -> LDS staging of one ROWS-key K or V stage by LDS DMA.  Instruction
+// t fills the 64 consecutive 16-byte slots 64t..64t+63 of the stage (1 KiB);
 // each lane fetches the global chunk that its slot holds under the layout.
 // The NW waves of the stream issue instructions t = wave, wave+NW, ...  The
 // buffer resource is rebased on the stage's first key and covers exactly its
 // valid rows, so rows >= Skv arrive as zeros (masked keys never carry
 // NaN/Inf) and the per-lane offsets are loop-invariant.
-template <int NW, class L, bool kIsV>
+template <int NW, class L, bool kIsV, int ROWS = kBN>
 struct TileDma {
   static constexpr int kSlots = kIsV ? L::kVSlots : L::kKSlots;  // per row
-  static constexpr int kInstTotal = kSlots;                       // 64 rows x kSlots / 64 lanes
+  static constexpr int kInstTotal = ROWS * kSlots / 64;           // 64 lanes per instruction
   static constexpr int kInst = (kInstTotal + NW - 1) / NW;        // per wave (the last may be idle)
+  static_assert(ROWS * kSlots % 64 == 0, "a stage is a whole number of DMA instructions");
   uint32_t off[kInst];
   int wave;  // wave-uniform
 
@@ -177,17 +174,17 @@ struct TileDma {
       const int slot = 64 * (wave + i * NW) + lane;
       const int row = slot / kSlots, sl = slot % kSlots;
       const int chunk = kIsV ? L::v_chunk(row, sl) : L::k_chunk(row, sl);
-      off[i] = (uint32_t)(((int64_t)(row < kBN ? row : kBN - 1) * ss + chunk * 8) * 2);
+      off[i] = (uint32_t)(((int64_t)(row < ROWS ? row : ROWS - 1) * ss + chunk * 8) * 2);
     }
   }
   __device__ __forceinline__ void issue(const uint16_t *base, int64_t ss, int key0, int Skv,
                                         uint16_t *tile) const {
-    const int rows = Skv - key0 >= kBN ? kBN : (Skv > key0 ? Skv - key0 : 0);
-    const __amdgpu_buffer_rsrc_t res = stage_rsrc(base + (int64_t)key0 * ss, ss, rows);
+    const int rows = Skv - key0 >= ROWS ? ROWS : (Skv > key0 ? Skv - key0 : 0);
+    const u32x4 desc = stage_desc(base + (int64_t)key0 * ss, ss, rows);
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
       if (kInstTotal % NW == 0 || wave + i * NW < kInstTotal)
-        buffer_load_lds_b128(res, off[i], tile + (wave + i * NW) * 512);
+        buffer_load_lds_b128(desc, off[i], tile + (wave + i * NW) * 512);
     }
   }
   // Common staging interface: start() at the top of a stage, finish() at its
@@ -236,33 +233,41 @@ struct TileRegs {
   }
 };
 
-// S^T (64 keys x 32 queries of this wave) = K_stage Q^T.  s0: keys 0-31, s1: 32-63.
-template <class L>
+// A stage's scores live in NSUB accumulators of 32 keys: s[u] holds keys
+// 32u..32u+31 of the stage.  In the S^T accumulator layout lane l owns query
+// l%32; register r of s[u] holds key 32u + 8*(r/4) + 4*(l/32) + r%4.
+
+// S^T (32*NSUB keys x 32 queries of this wave) = K_stage Q^T.
+template <class L, int NSUB>
 __device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&qf)[8], int k_rd,
-                                           f32x16 &s0, f32x16 &s1) {
-  s0 = f32x16{0.f};
-  s1 = f32x16{0.f};
+                                           f32x16 (&s)[NSUB]) {
+#pragma unroll
+  for (int u = 0; u < NSUB; ++u) s[u] = f32x16{0.f};
   const char *kb = reinterpret_cast<const char *>(kbuf);
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     const char *p = kb + L::k_off(k_rd, ks);
-    const u32x4 a0 = *(const u32x4 *)p;
-    const u32x4 a1 = *(const u32x4 *)(p + 32 * L::kKRow);
-    s0 = mfma_32x32x16(a0, qf[ks], s0);
-    s1 = mfma_32x32x16(a1, qf[ks], s1);
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u) {
+      const u32x4 a = *(const u32x4 *)(p + 32 * u * L::kKRow);
+      s[u] = mfma_32x32x16(a, qf[ks], s[u]);
+    }
   }
 }
 
-// P^T fragments for the 4 sixteen-key steps, straight from the S^T registers.
-// Step ks, k-slot (g = lane/32, e) carries key 16*ks + 8*(e/4) + 4*g + e%4.
-__device__ __forceinline__ void pack_p(const f32x16 &s0, const f32x16 &s1, u32x4 (&pf)[4]) {
+// P^T fragments for the 2*NSUB sixteen-key steps, straight from the S^T
+// registers.  Step ks, k-slot (g = lane/32, e) carries key
+// 16*ks + 8*(e/4) + 4*g + e%4.
+template <int NSUB>
+__device__ __forceinline__ void pack_p(const f32x16 (&s)[NSUB], u32x4 (&pf)[2 * NSUB]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    pf[h] = u32x4{pack_bf16x2(s0[8 * h + 0], s0[8 * h + 1]), pack_bf16x2(s0[8 * h + 2], s0[8 * h + 3]),
-                  pack_bf16x2(s0[8 * h + 4], s0[8 * h + 5]), pack_bf16x2(s0[8 * h + 6], s0[8 * h + 7])};
-    pf[2 + h] = u32x4{pack_bf16x2(s1[8 * h + 0], s1[8 * h + 1]), pack_bf16x2(s1[8 * h + 2], s1[8 * h + 3]),
-                      pack_bf16x2(s1[8 * h + 4], s1[8 * h + 5]), pack_bf16x2(s1[8 * h + 6], s1[8 * h + 7])};
-  }
+  for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      pf[2 * u + h] = u32x4{pack_bf16x2(s[u][8 * h + 0], s[u][8 * h + 1]),
+                            pack_bf16x2(s[u][8 * h + 2], s[u][8 * h + 3]),
+                            pack_bf16x2(s[u][8 * h + 4], s[u][8 * h + 5]),
+                            pack_bf16x2(s[u][8 * h + 6], s[u][8 * h + 7])};
 }
 
 // V transpose reads.  Within each 16-lane group a ds_read_b64_tr_b16 gives
@@ -271,13 +276,13 @@ __device__ __forceinline__ void pack_p(const f32x16 &s0, const f32x16 &s1, u32x4
 // k-slots 4..7) and columns 16*(t%2) + 4*(i%4) (+32*dt), so lane l receives
 // V[key][32*dt + l%32] for the 4 keys of its k-slots, in the score
 // accumulator's key order.  L::v_base / L::v_off place that in the layout.
-// O^T (128 dims x 32 queries) += V^T_stage P^T.
-template <class L>
-__device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[4], int v_rd,
+// O^T (128 dims x 32 queries) += V^T_stage P^T over NKS sixteen-key steps.
+template <class L, int NKS>
+__device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[NKS], int v_rd,
                                         f32x16 (&o)[4]) {
   const char *vb = reinterpret_cast<const char *>(vbuf);
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < NKS; ++ks) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const char *p = vb + L::v_off(v_rd, dt) + 16 * ks * L::kVRow;
@@ -288,59 +293,67 @@ __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[
   }
 }
 
-// Row max of a masked score tile (both 32-key halves, both lane halves), in
-// scale*log2(e) units.
-// Both reductions are trees (depth 4-5) rather than 16-long dependent chains:
-// the softmax cluster is latency-bound, not issue-bound.
-__device__ __forceinline__ float tile_max(const f32x16 &s0, const f32x16 &s1, float sl2) {
-#if H3A_TREE_REDUCE
-  float a[11];
+// Max of N values as a tree of v_max3 (depth log3 N), not a dependent chain:
+// the softmax cluster is latency-bound.
+template <int N>
+__device__ __forceinline__ float max_tree(const float (&v)[N]) {
+  if constexpr (N == 1) {
+    return v[0];
+  } else if constexpr (N == 2) {
+    return fmaxf(v[0], v[1]);
+  } else {
+    constexpr int M = (N + 2) / 3;
+    float t[M];
 #pragma unroll
-  for (int i = 0; i < 10; ++i) {  // 30 of the 32 values, three at a time
-    const int u = 3 * i;
-    const float x = u < 16 ? s0[u] : s1[u - 16];
-    const float y = u + 1 < 16 ? s0[u + 1] : s1[u + 1 - 16];
-    const float z = u + 2 < 16 ? s0[u + 2] : s1[u + 2 - 16];
-    a[i] = fmaxf(fmaxf(x, y), z);
+    for (int i = 0; i < M; ++i) {
+      if (3 * i + 2 < N)
+        t[i] = fmaxf(fmaxf(v[3 * i], v[3 * i + 1]), v[3 * i + 2]);
+      else if (3 * i + 1 < N)
+        t[i] = fmaxf(v[3 * i], v[3 * i + 1]);
+      else
+        t[i] = v[3 * i];
+    }
+    return max_tree<M>(t);
   }
-  a[10] = fmaxf(s1[14], s1[15]);
-  const float b0 = fmaxf(fmaxf(a[0], a[1]), a[2]), b1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
-  const float b2 = fmaxf(fmaxf(a[6], a[7]), a[8]), b3 = fmaxf(a[9], a[10]);
-  const float mx = fmaxf(fmaxf(b0, b1), fmaxf(b2, b3));
-#else
-  float mx = kNegInf;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) mx = fmaxf(fmaxf(mx, s0[r]), s1[r]);
-#endif
-  return half_swap_max(mx) * sl2;
 }
 
-// This lane's share of the row sum of a stage's p values.
-__device__ __forceinline__ float tile_sum(const f32x16 &s0, const f32x16 &s1) {
-#if H3A_TREE_REDUCE
+// Row max of a masked score stage (all sub-tiles, both lane halves), in
+// scale*log2(e) units.
+template <int NSUB>
+__device__ __forceinline__ float tile_max(const f32x16 (&s)[NSUB], float sl2) {
+  float v[16 * NSUB];
+#pragma unroll
+  for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[16 * u + r] = s[u][r];
+  return half_swap_max(max_tree<16 * NSUB>(v)) * sl2;
+}
+
+// This lane's share of the row sum of a stage's p values (a tree of adds).
+template <int NSUB>
+__device__ __forceinline__ float tile_sum(const f32x16 (&s)[NSUB]) {
   float a[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) a[r] = s0[r] + s1[r];
+  for (int r = 0; r < 16; ++r) {
+    a[r] = s[0][r] + s[1][r];
+    if constexpr (NSUB == 4) a[r] += s[2][r] + s[3][r];
+  }
 #pragma unroll
   for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
     for (int r = 0; r < w; ++r) a[r] += a[r + w];
   return a[0];
-#else
-  float rs = 0.f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) rs += s0[r] + s1[r];
-  return rs;
-#endif
 }
 
 // Keys >= Skv of the stage starting at key0 -> -inf (tail stage only).
-__device__ __forceinline__ void mask_tail(f32x16 &s0, f32x16 &s1, int key0, int Skv, int g) {
+template <int NSUB>
+__device__ __forceinline__ void mask_tail(f32x16 (&s)[NSUB], int key0, int Skv, int g) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int kk = key0 + 8 * (r >> 2) + 4 * g + (r & 3);
-    if (kk >= Skv) s0[r] = kNegInf;
-    if (kk + 32 >= Skv) s1[r] = kNegInf;
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u)
+      if (kk + 32 * u >= Skv) s[u][r] = kNegInf;
   }
 }
 
@@ -381,7 +394,7 @@ attn_fwd_kernel(AttnArgs a) {
   }
   // First key of stage j.  Prefetches past the last stage and LUT entries
   // outside the key range map to Skv: such a stage loads nothing (zeros).
-  auto key_base = [&](int j) -> int {
+  auto key_base = [&](int j) __attribute__((always_inline)) -> int {
     if (j >= niter) return a.Skv;
     if constexpr (kSparse) {
       const int kb = lut_row[j / a.sub];
@@ -440,10 +453,10 @@ attn_fwd_kernel(AttnArgs a) {
     kst.init(a.kss, wave_u, lane);
     vst.init(a.vss, wave_u, lane);
   }
-  auto land = [&] {  // this wave's stage fetches are in LDS
+  auto land = [&]() __attribute__((always_inline)) {  // this wave's stage fetches are in LDS
     if constexpr (KStager::kAsync) wait_vmem_all();
   };
-  f32x16 s0, s1;
+  f32x16 s[2];
   kst.start(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
   vst.start(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
   kst.finish(kbuf[0]);
@@ -451,12 +464,12 @@ attn_fwd_kernel(AttnArgs a) {
   land();
   __syncthreads();
   kst.start(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
-  score_tile<L>(kbuf[0], qf, k_rd, s0, s1);
+  score_tile<L, 2>(kbuf[0], qf, k_rd, s);
   kst.finish(kbuf[1]);
   land();
   __syncthreads();
 
-  auto stage = [&](auto phase, int j) {
+  auto stage = [&](auto phase, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(phase)::value;  // j & 1
     kst.start(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
     vst.start(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
@@ -464,8 +477,8 @@ attn_fwd_kernel(AttnArgs a) {
     // The two rare branches (tail mask, rescale) come first, so everything
     // after them is one basic block the scheduler can interleave freely.
     const int key0 = key_base(j);
-    if (key0 + kBN > a.Skv) mask_tail(s0, s1, key0, a.Skv, g);
-    const float mx = tile_max(s0, s1, a.sl2);
+    if (key0 + kBN > a.Skv) mask_tail<2>(s, key0, a.Skv, g);
+    const float mx = tile_max<2>(s, a.sl2);
 #if H3A_LAZY_RESCALE
     // The reference max only has to bound the exponents: keep the stale max
     // while this stage's row max exceeds it by at most kRescaleSlack (p stays
@@ -485,26 +498,26 @@ attn_fwd_kernel(AttnArgs a) {
     const float muse = (m == kNegInf) ? 0.f : m;
 
     // S(j+1) on the MFMA pipe, softmax(j) on the VALU: no dependence between them.
-    f32x16 n0, n1;
-    score_tile<L>(kbuf[P ^ 1], qf, k_rd, n0, n1);
+    f32x16 n[2];
+    score_tile<L, 2>(kbuf[P ^ 1], qf, k_rd, n);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      s0[r] = fast_exp2(fmaf(s0[r], a.sl2, -muse));
-      s1[r] = fast_exp2(fmaf(s1[r], a.sl2, -muse));
+      s[0][r] = fast_exp2(fmaf(s[0][r], a.sl2, -muse));
+      s[1][r] = fast_exp2(fmaf(s[1][r], a.sl2, -muse));
     }
     u32x4 pf[4];
-    pack_p(s0, s1, pf);
+    pack_p<2>(s, pf);
 #if H3A_ROWSUM_BF16
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int c = 0; c < 4; ++c) lsum = dot2_bf16_ones(pf[ks][c], lsum);
 #else
-    lsum += tile_sum(s0, s1);
+    lsum += tile_sum<2>(s);
 #endif
-    pv_tile<L>(vbuf[P], pf, v_rd, o);
-    s0 = n0;
-    s1 = n1;
+    pv_tile<L, 4>(vbuf[P], pf, v_rd, o);
+    s[0] = n[0];
+    s[1] = n[1];
 #if H3A_SCHED_HINTS
     // Interleave the block: each MFMA followed by LDS reads and VALU work
     // that can issue in its 32-cycle shadow.
@@ -544,15 +557,16 @@ attn_fwd_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Softmax of one 64-key score stage, in place: S -> P (bf16 pairs in pf), the
-// running max m (refreshed lazily, as in attn_fwd_kernel) and this lane's
-// share of the row sum of the unrounded p; O and l are rescaled when the max
-// moves.  VALU work only.
-__device__ __forceinline__ void softmax_stage(f32x16 &s0, f32x16 &s1, int key0, int Skv, int g,
-                                              float sl2, float &m, float &lsum, f32x16 (&o)[4],
-                                              u32x4 (&pf)[4]) {
-  if (key0 + kBN > Skv) mask_tail(s0, s1, key0, Skv, g);
-  const float mx = tile_max(s0, s1, sl2);
+// Softmax of one score stage (32*NSUB keys), in place: S -> P (bf16 pairs in
+// pf), the running max m (refreshed lazily, as in attn_fwd_kernel) and this
+// lane's share of the row sum of the unrounded p; O and l are rescaled when
+// the max moves.  VALU work only.
+template <int NSUB>
+__device__ __forceinline__ void softmax_stage(f32x16 (&s)[NSUB], int key0, int Skv, int g, float sl2,
+                                              float &m, float &lsum, f32x16 (&o)[4],
+                                              u32x4 (&pf)[2 * NSUB]) {
+  if (key0 + 32 * NSUB > Skv) mask_tail<NSUB>(s, key0, Skv, g);
+  const float mx = tile_max<NSUB>(s, sl2);
   if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0) {
     const float mnew = fmaxf(m, mx);
     const float alpha = fast_exp2(m - ((mnew == kNegInf) ? 0.f : mnew));
@@ -563,12 +577,11 @@ __device__ __forceinline__ void softmax_stage(f32x16 &s0, f32x16 &s1, int key0, 
   }
   const float muse = (m == kNegInf) ? 0.f : m;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    s0[r] = fast_exp2(fmaf(s0[r], sl2, -muse));
-    s1[r] = fast_exp2(fmaf(s1[r], sl2, -muse));
-  }
-  pack_p(s0, s1, pf);
-  lsum += tile_sum(s0, s1);
+  for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[u][r] = fast_exp2(fmaf(s[u][r], sl2, -muse));
+  pack_p<NSUB>(s, pf);
+  lsum += tile_sum<NSUB>(s);
 }
 
 // Pin values to this point of the program: an empty volatile asm that reads
@@ -586,49 +599,43 @@ __device__ __forceinline__ void slot_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Ping-pong kernel: 8 waves x 32 query rows; waves 0-3 (group A) and 4-7
-// (group B) sit one of each per SIMD.  Every stage is split into a
-// matrix-core cluster, MFMA(j): S(j+1) = K(j+1) Q^T and O += V(j) P(j), and a
-// softmax cluster, SOFT(j): S(j+1) -> P(j+1), with a workgroup barrier after
-// each.  Group B runs one cluster behind group A, so on every SIMD one wave
-// issues MFMAs while the other issues the softmax's VALU work and the two
-// pipes overlap.
+// Dense ping-pong kernel: 8 waves x 32 query rows (one 256-row query tile per
+// workgroup); waves 0-3 (group A) and 4-7 (group B) sit one of each per SIMD.
+// Every stage of BN = 32*NSUB keys is split into a matrix-core cluster,
+// MFMA(j): S(j+1) = K(j+1) Q^T and O += V(j) P(j), and a softmax cluster,
+// SOFT(j): S(j+1) -> P(j+1), with a workgroup barrier after each.  Group B
+// runs one cluster behind group A, so on every SIMD one wave issues MFMAs
+// while the other issues the softmax's VALU work and the two pipes overlap.
 //
 // Barrier slots after the prologue (both groups pass the same barriers):
 //   slot 2j+1:  A: DMA(j), MFMA(j)            B: DMA(j), SOFT(j-1)
 //   slot 2j+2:  A: SOFT(j), wait for DMA      B: MFMA(j), wait for DMA
-// DMA(j) fetches K(j+2) into kbuf[j&1] and V(j+1) into vbuf[(j+1)&1].  Those
-// buffers were last read by MFMA(j-1), which both groups finished by the end
-// of slot 2j; the data is read by MFMA(j+1) from slot 2j+3 on, after every
-// wave waited for its share of the DMA at the end of slot 2j+2.
-//
-// Dense: the workgroup is one 256-row query tile; both groups share one K/V
-// stream (the 8 waves split each DMA).  Block-sparse (blk_q = 128): the
-// workgroup is two 128-row query blocks of one head, group A the even one and
-// group B the odd one, each with its own LUT row, K/V buffers and DMA.  Both
-// groups run max(stages of A, stages of B) stages so they pass the same
-// barriers; past its own count a group only takes part in the barriers.
-template <bool kSparse, class L>
+// DMA(j) fetches K(j+2) into kbuf[j&1] and V(j+1) into vbuf[(j+1)&1] (the 8
+// waves split each tile).  Those buffers were last read by MFMA(j-1), which
+// both groups finished by the end of slot 2j; the data is read by MFMA(j+1)
+// from slot 2j+3 on, after every wave waited for its share of the DMA at the
+// end of slot 2j+2.
+template <class L, int NSUB>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   constexpr int NW = 8;
-  constexpr int kStreams = kSparse ? 2 : 1;  // K/V streams per workgroup
-  constexpr int kDmaWaves = NW / kStreams;   // waves sharing one stream's DMA
-  constexpr int kKE = StageBytes<L>::kK / 2, kVE = StageBytes<L>::kV / 2;  // elements
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[kStreams][2][kKE];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[kStreams][2][kVE];
+  constexpr int BN = 32 * NSUB;  // keys per stage
+  constexpr int kKE = StageBytes<L, BN>::kK / 2, kVE = StageBytes<L, BN>::kV / 2;  // elements
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kKE];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kVE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const bool lead = wave_u < NW / 2;  // group A
-  // Work item of this workgroup.  Dense with a split tail: the first
+  const int nstages = (a.Skv + BN - 1) / BN;
+  // Work item of this workgroup.  With a split tail, the first
   // a.split_first items are whole query tiles; each later tile is cut into
-  // a.split_pieces contiguous key ranges, one per workgroup, whose partial
-  // results are merged by split_combine_kernel.
-  int w, piece = -1, j0 = 0, j_end = 0;
-  if (kSparse || (int)blockIdx.x < a.split_first) {
-    const int whole = kSparse ? a.total : (a.split_first < a.total ? a.split_first : a.total);
+  // a.split_pieces contiguous ranges of stages, one per workgroup, whose
+  // partial results are merged by split_combine_kernel.
+  int w, piece = -1, j0 = 0, niter = nstages;
+  if ((int)blockIdx.x < a.split_first) {
+    const int whole = a.split_first < a.total ? a.split_first : a.total;
 #if H3A_XCD_REMAP
     w = xcd_remap(blockIdx.x, whole);
 #else
@@ -637,67 +644,20 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   } else {
     piece = blockIdx.x - a.split_first;
     w = a.split_first + piece / a.split_pieces;
-    const int p = piece % a.split_pieces, n = (a.Skv + kBN - 1) / kBN;
-    j0 = (int)((int64_t)n * p / a.split_pieces);
-    j_end = (int)((int64_t)n * (p + 1) / a.split_pieces);
+    const int p = piece % a.split_pieces;
+    j0 = (int)((int64_t)nstages * p / a.split_pieces);
+    niter = (int)((int64_t)nstages * (p + 1) / a.split_pieces) - j0;  // >= 1
   }
-  // Query tiles per (b,h) in units of this workgroup: 256-row tiles (dense) or
-  // pairs of 128-row blocks (sparse, a.nqt blocks).
-  const int wg_tiles = kSparse ? (a.nqt + 1) / 2 : a.nqt;
-  const int qt = w % wg_tiles, bh = w / wg_tiles;
+  const int qt = w % a.nqt, bh = w / a.nqt;
   const int h = bh % a.H, b = bh / a.H;
   const uint16_t *Qb = a.q + b * a.qsb + h * a.qsh;
   const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
   const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
   uint16_t *Ob = a.o + b * a.osb + h * a.osh;
-
-  int niter;         // stages of this wave's group
-  int niter_wg;      // stages the workgroup runs (max over the groups)
-  int qrow;          // this lane's query row
-  const int32_t *lut_row = nullptr;
-  if constexpr (kSparse) {
-    const int grp = lead ? 0 : 1;
-    const int qb = 2 * qt + grp;
-    auto stages_of = [&](int blk) -> int {
-      if (blk >= a.nqt) return 0;
-      const int cnt = a.counts[(int64_t)bh * a.nqt + blk];
-      return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
-    };
-    niter = stages_of(qb);
-    const int other = stages_of(2 * qt + (1 - grp));
-    niter_wg = niter > other ? niter : other;
-    lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
-    qrow = qb * 128 + (wave & 3) * 32 + l32;
-  } else {
-    niter = piece < 0 ? (a.Skv + kBN - 1) / kBN : j_end - j0;  // >= 1
-    niter_wg = niter;
-    qrow = qt * 256 + wave * 32 + l32;
-  }
-  // First key of stage j of this group; past the group's last stage (and for
-  // LUT entries outside the key range) it is Skv, which loads nothing (zeros).
-  auto key_base = [&](int j) -> int {
-    if (j >= niter) return a.Skv;
-    if constexpr (kSparse) {
-      const int kb = lut_row[j / a.sub];
-      const int key0 = kb * a.blk_k + (j % a.sub) * kBN;
-      return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
-    } else {
-      return (j0 + j) * kBN;
-    }
-  };
-
-  if (niter_wg == 0) {
-    // Neither group has a key block (empty LUT rows): O = 0.  No barrier is
-    // reached by any wave of the workgroup.
-    if (qrow < a.Sq) {
-      uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
-#pragma unroll
-      for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
-    }
-    return;
-  }
-  uint16_t (*kbuf)[kKE] = kbuf_all[kSparse && !lead ? 1 : 0];
-  uint16_t (*vbuf)[kVE] = vbuf_all[kSparse && !lead ? 1 : 0];
+  const int qrow = qt * 256 + wave * 32 + l32;
+  // First key of local stage j; past the last stage it is Skv, which loads
+  // nothing (zeros).
+  auto key_base = [&](int j) __attribute__((always_inline)) -> int { return j < niter ? (j0 + j) * BN : a.Skv; };
 
   u32x4 qf[8];
   if (qrow < a.Sq) {
@@ -716,98 +676,92 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   const int k_rd = L::k_base(l32, g);
   const int v_rd = L::v_base(lane);
 
-  TileDma<kDmaWaves, L, false> kdma;
-  TileDma<kDmaWaves, L, true> vdma;
-  const int dma_wave = kSparse ? (wave_u & 3) : wave_u;
-  kdma.init(a.kss, dma_wave, lane);
-  vdma.init(a.vss, dma_wave, lane);
-  const bool active = niter > 0;
+  TileDma<NW, L, false, BN> kdma;
+  TileDma<NW, L, true, BN> vdma;
+  kdma.init(a.kss, wave_u, lane);
+  vdma.init(a.vss, wave_u, lane);
 
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
-  if (active) {
-    kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
-    vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
-    kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
-  }
+  kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
+  vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+  kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
   wait_vmem_all();
   __syncthreads();
-  f32x16 s0, s1;
-  u32x4 pf[4];
-  if (active) {
-    score_tile<L>(kbuf[0], qf, k_rd, s0, s1);
-    softmax_stage(s0, s1, key_base(0), a.Skv, g, a.sl2, m, lsum, o, pf);
-  }
+  f32x16 s[NSUB];
+  u32x4 pf[2 * NSUB];
+  score_tile<L, NSUB>(kbuf[0], qf, k_rd, s);
+  softmax_stage<NSUB>(s, key_base(0), a.Skv, g, a.sl2, m, lsum, o, pf);
   __syncthreads();  // kbuf[0] is free for K(2)
 
-  auto dma = [&](auto par, int j) {
+  auto dma = [&](auto par, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;  // j & 1
     kdma.issue(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
     vdma.issue(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
   };
-  // One basic block: 16 score MFMAs (the group's last stage multiplies the
-  // zero tile past its keys and discards it) and 16 PV MFMAs, with the 48 LDS
+  // One basic block: 32*NSUB MFMAs (the last stage's scores are of
+  // the zero tile past the keys and are discarded), with the 24*NSUB LDS
   // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
   // after each MFMA, so every read is in flight for several MFMAs.
-  auto mfma = [&](auto par) {
+  auto mfma = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
     __builtin_amdgcn_s_setprio(1);
-    score_tile<L>(kbuf[P ^ 1], qf, k_rd, s0, s1);
-    pv_tile<L>(vbuf[P], pf, v_rd, o);
+#if H3A_PP_PV_FIRST
+    pv_tile<L, 2 * NSUB>(vbuf[P], pf, v_rd, o);
+    score_tile<L, NSUB>(kbuf[P ^ 1], qf, k_rd, s);
+#else
+    score_tile<L, NSUB>(kbuf[P ^ 1], qf, k_rd, s);
+    pv_tile<L, 2 * NSUB>(vbuf[P], pf, v_rd, o);
+#endif
 #if H3A_PP_READ_AHEAD
     __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 32 * NSUB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
 #endif
     __builtin_amdgcn_s_setprio(0);
   };
-  auto soft = [&](int j) {
-    softmax_stage(s0, s1, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
+  auto soft = [&](int j) __attribute__((always_inline)) {
+    softmax_stage<NSUB>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
 #if H3A_PP_PIN_SOFTMAX
-    for (int i = 0; i < 4; ++i) pin(pf[i]);
+#pragma unroll
+    for (int i = 0; i < 2 * NSUB; ++i) pin(pf[i]);
     pin(lsum);
     pin(m);
 #endif
   };
 
   if (lead) {
-    auto stage = [&](auto par, int j) {
-      const bool run = j < niter;
-      if (run) {
-        dma(par, j);
-        mfma(par);
-      }
+    auto stage = [&](auto par, int j) __attribute__((always_inline)) {
+      dma(par, j);
+      mfma(par);
       slot_barrier();
       if (j + 1 < niter) soft(j);
       wait_vmem_all();
       slot_barrier();
     };
-    for (int j = 0; j < niter_wg; j += 2) {
+    for (int j = 0; j < niter; j += 2) {
       stage(std::integral_constant<int, 0>{}, j);
-      if (j + 1 < niter_wg) stage(std::integral_constant<int, 1>{}, j + 1);
+      if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
     }
   } else {
-    auto stage = [&](auto par, int j) {
-      const bool run = j < niter;
-      if (run) {
-        dma(par, j);
-        if (j > 0) soft(j - 1);
-      }
+    auto stage = [&](auto par, int j) __attribute__((always_inline)) {
+      dma(par, j);
+      if (j > 0) soft(j - 1);
       slot_barrier();
-      if (run) mfma(par);
+      mfma(par);
       wait_vmem_all();
       slot_barrier();
     };
-    for (int j = 0; j < niter_wg; j += 2) {
+    for (int j = 0; j < niter; j += 2) {
       stage(std::integral_constant<int, 0>{}, j);
-      if (j + 1 < niter_wg) stage(std::integral_constant<int, 1>{}, j + 1);
+      if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
     }
   }
 
   const float ltot = half_swap_sum(lsum);
-  if (!kSparse && piece >= 0) {
+  if (piece >= 0) {
     // Partial result of one key range: unnormalised O, the reference max m
     // it is relative to (scale*log2(e) units) and the row sum, for all 256
     // rows of the tile (rows past Sq included; the combine skips them).
@@ -888,13 +842,13 @@ __global__ void __launch_bounds__(64) test_qk_kernel(const uint16_t *Q, const ui
   u32x4 qf[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const u32x4 *)(Q + l32 * kD + ks * 16 + 8 * g);
-  f32x16 s0, s1;
-  score_tile<SwzLayout>(kb, qf, SwzLayout::k_base(l32, g), s0, s1);
+  f32x16 s[2];
+  score_tile<SwzLayout, 2>(kb, qf, SwzLayout::k_base(l32, g), s);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = 8 * (r >> 2) + 4 * g + (r & 3);
-    S[l32 * kBN + key] = s0[r];
-    S[l32 * kBN + key + 32] = s1[r];
+    S[l32 * kBN + key] = s[0][r];
+    S[l32 * kBN + key + 32] = s[1][r];
   }
 }
 
@@ -907,19 +861,19 @@ __global__ void __launch_bounds__(64) test_pv_kernel(const uint16_t *P, const ui
   wait_vmem_all();
   __syncthreads();
   // Place P[q][key] where the score accumulators would hold it.
-  f32x16 s0, s1;
+  f32x16 s[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = 8 * (r >> 2) + 4 * g + (r & 3);
-    s0[r] = __uint_as_float((uint32_t)P[l32 * kBN + key] << 16);
-    s1[r] = __uint_as_float((uint32_t)P[l32 * kBN + key + 32] << 16);
+    s[0][r] = __uint_as_float((uint32_t)P[l32 * kBN + key] << 16);
+    s[1][r] = __uint_as_float((uint32_t)P[l32 * kBN + key + 32] << 16);
   }
   u32x4 pf[4];
-  pack_p(s0, s1, pf);
+  pack_p<2>(s, pf);
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
-  pv_tile<SwzLayout>(vb, pf, SwzLayout::v_base(tid), o);
+  pv_tile<SwzLayout, 4>(vb, pf, SwzLayout::v_base(tid), o);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -949,7 +903,8 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 
 // ---------------------------------------------------------------------------
 using DenseLayout = std::conditional_t<H3A_DENSE_LAYOUT == 1, PadLayout, SwzLayout>;
-using SparseLayout = std::conditional_t<H3A_SPARSE_LAYOUT == 1, PadLayout, SwzLayout>;
+constexpr int kDenseSub = H3A_DENSE_BN / 32;
+static_assert(kDenseSub == 2 || kDenseSub == 4, "dense stages of 64 or 128 keys");
 
 int launch_attn_dense(AttnArgs a, hipStream_t s) {
 #if H3A_DENSE_PINGPONG
@@ -962,7 +917,7 @@ int launch_attn_dense(AttnArgs a, hipStream_t s) {
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
   a.total = (int)total;
 #if H3A_DENSE_PINGPONG
-  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<false, DenseLayout>), dim3(a.total), dim3(64 * NW), 0, s, a);
+  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>), dim3(a.total), dim3(64 * NW), 0, s, a);
 #else
   hipLaunchKernelGGL((attn_fwd_kernel<NW, DenseLayout, false, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
 #endif
@@ -986,7 +941,7 @@ int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
     if (dev >= 0 && dev < 64) cu_cache[dev].store(cus, std::memory_order_relaxed);
   }
   const int64_t tiles = (int64_t)B * H * ((Sq + 255) / 256);
-  const int stages = (Skv + kBN - 1) / kBN;
+  const int stages = (Skv + H3A_DENSE_BN - 1) / H3A_DENSE_BN;
   const int64_t r = tiles >= cus ? tiles % cus : tiles;
   int pieces = 1;
   if (H3A_DENSE_PINGPONG && r > 0) {
@@ -1013,7 +968,7 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
   const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
   a.total = (int)total;
-  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<false, DenseLayout>), dim3(a.total), dim3(512), 0, s, a);
+  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>), dim3(a.total), dim3(512), 0, s, a);
   int rc = check_launch("attn_fwd_pingpong_kernel<split>");
   if (rc) return rc;
   const int64_t rows = (int64_t)(plan.tiles - plan.first) * 256;
@@ -1023,14 +978,7 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   if (blk_q == 128) {
-#if H3A_SPARSE_PINGPONG
-    // Pairs of 128-row query blocks per workgroup.
-    AttnArgs p = a;
-    p.total = a.B * a.H * ((a.nqt + 1) / 2);
-    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<true, SparseLayout>), dim3(p.total), dim3(512), 0, s, p);
-#else
     hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(256), 0, s, a);
-#endif
   } else {
     hipLaunchKernelGGL((attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(128), 0, s, a);
   }
@@ -1080,17 +1028,13 @@ int attn_kernel_attrs(int which, double out[6]) {
   switch (which) {
     case H3A_KERNEL_ATTN_DENSE:
 #if H3A_DENSE_PINGPONG
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<false, DenseLayout>), 512, out);
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>), 512, out);
 #else
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<H3A_DENSE_WAVES, DenseLayout, false, false>),
                         64 * H3A_DENSE_WAVES, out);
 #endif
     case H3A_KERNEL_ATTN_SPARSE_128:
-#if H3A_SPARSE_PINGPONG
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<true, SparseLayout>), 512, out);
-#else
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), 256, out);
-#endif
     case H3A_KERNEL_ATTN_SPARSE_64:
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), 128, out);
     default:

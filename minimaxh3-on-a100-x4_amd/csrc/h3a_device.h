@@ -76,11 +76,23 @@ __device__ __forceinline__ u32x4 buffer_load_b128(__amdgpu_buffer_rsrc_t res, ui
 // bytes are read.
 // The compiler's own vmcnt waits stay correct, since extra loads issued
 // after one of its loads only make a wait for that load more conservative.
-__device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t res, uint32_t byte_off,
-                                                     void *lds_dst) {
+// `desc` is the V# as four scalar words (stage_desc).
+__device__ __forceinline__ void buffer_load_lds_b128(u32x4 desc, uint32_t byte_off, void *lds_dst) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_dst;
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(res), "{m0}"(m0)
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(desc), "{m0}"(m0)
                : "memory");
+}
+
+// stage_rsrc's V# as four words for inline asm: base address (48 bits, stride
+// 0), num_records, config.  Each word goes through readfirstlane, so the
+// operand is provably wave-uniform and lives in SGPRs whatever the register
+// pressure around the call.
+__device__ __forceinline__ u32x4 stage_desc(const uint16_t *base, int64_t stride, int rows) {
+  const uint32_t bytes = rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + 128) * 2) : 0u;
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(addr >> 32) & 0xffffu)),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), (uint32_t)kBufferConfig};
 }
 
 // s_waitcnt vmcnt(N): at most the N most recent vector-memory loads of this
