@@ -74,6 +74,11 @@ namespace h3a {
 #ifndef H3A_PP_PV_FIRST
 #define H3A_PP_PV_FIRST 0
 #endif
+// Ping-pong softmax against a stale reference max: no per-stage row max, only
+// a check of the stage's p sum (1), or the per-stage max with lazy refresh (0).
+#ifndef H3A_PP_STALE_MAX
+#define H3A_PP_STALE_MAX 1
+#endif
 // Block-sparse attn_fwd_kernel: K/V staged through VGPRs (1) or by LDS DMA (0).
 #ifndef H3A_SPARSE_REGS
 #define H3A_SPARSE_REGS 1
@@ -92,6 +97,7 @@ namespace h3a {
 constexpr int kD = 128;
 constexpr int kBN = 64;               // keys per pipeline stage
 constexpr float kRescaleSlack = 8.f;  // log2 headroom before the running max is refreshed
+constexpr float kStaleSumLimit = 0x1p64f;  // largest stage p sum accepted without a refresh
 
 // ---------------------------------------------------------------------------
 // LDS layouts of a 64-key K or V stage.  A layout fixes the row pitch, which
@@ -164,27 +170,59 @@ struct TileDma {
   static constexpr int kInstTotal = ROWS * kSlots / 64;           // 64 lanes per instruction
   static constexpr int kInst = (kInstTotal + NW - 1) / NW;        // per wave (the last may be idle)
   static_assert(ROWS * kSlots % 64 == 0, "a stage is a whole number of DMA instructions");
-  uint32_t off[kInst];
-  int wave;  // wave-uniform
+  // With 16-slot rows and NW a multiple of 4, instruction i covers rows
+  // 4*(wave + i*NW) + lane/16: the swizzle (row & 15 or row & 3) does not
+  // depend on i, so the offsets are off[0] + i * 4*NW rows and one register
+  // holds them all.
+  static constexpr bool kAffine = kSlots == 16 && NW % 4 == 0;
+  uint32_t off[kAffine ? 1 : kInst];
+  uint32_t step;  // bytes between instructions when kAffine (wave-uniform)
+  int wave;       // wave-uniform
 
   __device__ __forceinline__ void init(int64_t ss, int wave_uniform, int lane) {
     wave = wave_uniform;
+    step = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(4 * NW * ss * 2));
 #pragma unroll
-    for (int i = 0; i < kInst; ++i) {
+    for (int i = 0; i < (kAffine ? 1 : kInst); ++i) {
       const int slot = 64 * (wave + i * NW) + lane;
       const int row = slot / kSlots, sl = slot % kSlots;
       const int chunk = kIsV ? L::v_chunk(row, sl) : L::k_chunk(row, sl);
       off[i] = (uint32_t)(((int64_t)(row < ROWS ? row : ROWS - 1) * ss + chunk * 8) * 2);
     }
   }
+  // Offsets of instructions 0, 1, ... in issue order: `cur` starts at
+  // first() and next() moves it on.  The add is opaque to the compiler, which
+  // would otherwise hoist all kInst offsets out of the stage loop and keep
+  // them in registers.  Without kAffine the cursor is the instruction index.
+  __device__ __forceinline__ uint32_t first() const { return kAffine ? off[0] : 0u; }
+  __device__ __forceinline__ uint32_t next(uint32_t cur) const {
+    if constexpr (kAffine) {
+      uint32_t r;
+      asm volatile("v_add_u32 %0, %1, %2" : "=v"(r) : "v"(cur), "s"(step));
+      return r;
+    } else {
+      return cur + 1;
+    }
+  }
+  // Buffer descriptor of the stage that starts at key0 (valid rows only).
+  __device__ __forceinline__ u32x4 desc(const uint16_t *base, int64_t ss, int key0, int Skv) const {
+    const int rows = Skv - key0 >= ROWS ? ROWS : (Skv > key0 ? Skv - key0 : 0);
+    return stage_desc(base + (int64_t)key0 * ss, ss, rows);
+  }
+  // Instruction i (0 <= i < kInst, a compile-time index) of this wave's
+  // share; `cur` is its cursor (first(), then next() once per instruction).
+  __device__ __forceinline__ void issue_one(u32x4 d, int i, uint32_t cur, uint16_t *tile) const {
+    if (kInstTotal % NW == 0 || wave + i * NW < kInstTotal)
+      buffer_load_lds_b128(d, kAffine ? cur : off[i], tile + (wave + i * NW) * 512);
+  }
   __device__ __forceinline__ void issue(const uint16_t *base, int64_t ss, int key0, int Skv,
                                         uint16_t *tile) const {
-    const int rows = Skv - key0 >= ROWS ? ROWS : (Skv > key0 ? Skv - key0 : 0);
-    const u32x4 desc = stage_desc(base + (int64_t)key0 * ss, ss, rows);
+    const u32x4 d = desc(base, ss, key0, Skv);
+    uint32_t cur = first();
 #pragma unroll
     for (int i = 0; i < kInst; ++i) {
-      if (kInstTotal % NW == 0 || wave + i * NW < kInstTotal)
-        buffer_load_lds_b128(desc, off[i], tile + (wave + i * NW) * 512);
+      issue_one(d, i, cur, tile);
+      if (i + 1 < kInst) cur = next(cur);
     }
   }
   // Common staging interface: start() at the top of a stage, finish() at its
@@ -584,6 +622,66 @@ __device__ __forceinline__ void softmax_stage(f32x16 (&s)[NSUB], int key0, int S
   lsum += tile_sum<NSUB>(s);
 }
 
+// Softmax of one score stage against the running reference m without
+// computing the stage's row max.  p = 2^(s*sl2 - m) is formed, packed and
+// summed straight away; only if some lane's stage sum exceeds kStaleSumLimit
+// (or is not finite: a score ran 128 or more above m) does the wave take the
+// row max, refresh m, rescale O and l and redo the stage.  m must be finite
+// on entry (the first stage of a key range uses softmax_stage, which sets m
+// to that stage's row max, so every later row sum is >= 1).  p may then reach
+// 2^64 instead of 1: bf16 rounding of P and the fp32 sums are relative, so the
+// normalised O is unchanged, and 2^64 * 2^16 keys * |v| stays far from the
+// fp32 range limit.
+template <int NSUB>
+__device__ __forceinline__ void exp_pack_sum(const f32x16 (&s)[NSUB], float sl2, float m,
+                                             u32x4 (&pf)[2 * NSUB], float &ps) {
+  float a[16];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int r = 8 * h + 2 * w;
+      float p0[NSUB], p1[NSUB];
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        p0[u] = fast_exp2(fmaf(s[u][r], sl2, -m));
+        p1[u] = fast_exp2(fmaf(s[u][r + 1], sl2, -m));
+        pf[2 * u + h][w] = pack_bf16x2(p0[u], p1[u]);
+      }
+      a[r] = p0[0] + p0[1];
+      a[r + 1] = p1[0] + p1[1];
+      if constexpr (NSUB == 4) {
+        a[r] += p0[2] + p0[3];
+        a[r + 1] += p1[2] + p1[3];
+      }
+    }
+  }
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int r = 0; r < w; ++r) a[r] += a[r + w];
+  ps = a[0];
+}
+
+template <int NSUB>
+__device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0, int Skv, int g, float sl2,
+                                                    float &m, float &lsum, f32x16 (&o)[4],
+                                                    u32x4 (&pf)[2 * NSUB]) {
+  if (key0 + 32 * NSUB > Skv) mask_tail<NSUB>(s, key0, Skv, g);
+  float ps;
+  exp_pack_sum<NSUB>(s, sl2, m, pf, ps);
+  if (__builtin_amdgcn_ballot_w64(!(ps <= kStaleSumLimit)) != 0) {
+    const float mnew = fmaxf(m, tile_max<NSUB>(s, sl2));
+    const float alpha = fast_exp2(m - mnew);
+    m = mnew;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    exp_pack_sum<NSUB>(s, sl2, m, pf, ps);
+  }
+  lsum += ps;
+}
+
 // Pin values to this point of the program: an empty volatile asm that reads
 // and rewrites them.  Everything they depend on must be computed before it,
 // and volatile asm keeps its place relative to the workgroup barriers.  Without
@@ -698,7 +796,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     kdma.issue(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
     vdma.issue(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
   };
-  // One basic block: 32*NSUB MFMAs (the last stage's scores are of
+  // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
   // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
   // after each MFMA, so every read is in flight for several MFMAs.
@@ -715,7 +813,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 #if H3A_PP_READ_AHEAD
     __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
 #pragma unroll
-    for (int i = 0; i < 32 * NSUB; ++i) {
+    for (int i = 0; i < 16 * NSUB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
@@ -723,7 +821,11 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     __builtin_amdgcn_s_setprio(0);
   };
   auto soft = [&](int j) __attribute__((always_inline)) {
+#if H3A_PP_STALE_MAX
+    softmax_stage_stale<NSUB>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
+#else
     softmax_stage<NSUB>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
+#endif
 #if H3A_PP_PIN_SOFTMAX
 #pragma unroll
     for (int i = 0; i < 2 * NSUB; ++i) pin(pf[i]);
@@ -746,17 +848,22 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
     }
   } else {
-    auto stage = [&](auto par, int j) __attribute__((always_inline)) {
+    // kFirst: stage 0, which has no softmax before its matrix cluster (P(0)
+    // came from the prologue); peeled off so that the loop body has no branch.
+    auto stage = [&](auto par, int j, auto first) __attribute__((always_inline)) {
       dma(par, j);
-      if (j > 0) soft(j - 1);
+      if constexpr (!decltype(first)::value) soft(j - 1);
       slot_barrier();
       mfma(par);
       wait_vmem_all();
       slot_barrier();
     };
-    for (int j = 0; j < niter; j += 2) {
-      stage(std::integral_constant<int, 0>{}, j);
-      if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    stage(C0{}, 0, std::true_type{});
+    for (int j = 1; j < niter; j += 2) {
+      stage(C1{}, j, std::false_type{});
+      if (j + 1 < niter) stage(C0{}, j + 1, std::false_type{});
     }
   }
 

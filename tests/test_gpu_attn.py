@@ -126,6 +126,47 @@ def test_constant_value_rows(gpu):
     assert np.abs(o - 1.5).max() <= 1.5 * 2.0 ** -7
 
 
+def _ramp_case(rng, S, slope, q0):
+    """Scores that move steadily along the keys: dim 0 of key j is slope*j and
+    dim 0 of the queries is +-q0, the other dims small noise."""
+    q = rng.standard_normal((1, 2, S, 128)).astype(np.float32) * 0.1
+    k = rng.standard_normal((1, 2, S, 128)).astype(np.float32) * 0.1
+    v = rng.standard_normal((1, 2, S, 128)).astype(np.float32)
+    q[..., 0] = np.where(np.arange(S) % 2 == 0, q0, -q0)  # even rows rise, odd rows fall
+    k[..., 0] = slope * np.arange(S)
+    return tuple(oracle.f32_to_bf16(x) for x in (q, k, v))
+
+
+@pytest.mark.parametrize("S", [300, 1000])
+def test_running_max_rises_by_hundreds(gpu, S):
+    """Even query rows see scores that rise by ~26 (log2 units) every 64 keys, ~400 in
+    all: exp2 against the first stage's max would overflow many times over, so the
+    running max must be refreshed.  Odd rows fall and underflow towards zero."""
+    rng = np.random.default_rng(30)
+    q, k, v = _ramp_case(rng, S, slope=0.4 * 1000 / S, q0=64.0)
+    o = _run(q, k, v, gpu)
+    assert np.isfinite(o).all()
+    assert_close_absmax(o, oracle.attn_fwd(q, k, v, round_p=True), what="rising max")
+
+
+def test_lone_dominant_key(gpu):
+    """One key mid-sequence out-scores the rest by ~160 (log2 units): every row's output
+    is that key's value row to bf16 rounding."""
+    rng = np.random.default_rng(31)
+    S = 777
+    q = rng.standard_normal((1, 2, S, 128)).astype(np.float32) * 0.1
+    k = rng.standard_normal((1, 2, S, 128)).astype(np.float32) * 0.1
+    v = rng.standard_normal((1, 2, S, 128)).astype(np.float32)
+    q[..., 0] = 64.0
+    k[:, :, 500, 0] = 20.0
+    q, k, v = (oracle.f32_to_bf16(x) for x in (q, k, v))
+    o = _run(q, k, v, gpu)
+    ref = oracle.attn_fwd(q, k, v, round_p=True)
+    assert_close_absmax(o, ref, what="lone dominant key")
+    vrow = oracle.bf16_to_f32(v).reshape(v.shape)[:, :, 500:501, :]
+    assert np.abs(o - vrow).max() <= 2.0 ** -8 * np.abs(vrow).max()
+
+
 def test_key_value_permutation_invariance(gpu):
     rng = np.random.default_rng(9)
     q, k, v = (randn_bf16(rng, (1, 2, 333, 128)) for _ in range(3))
