@@ -54,6 +54,18 @@ def randn_bf16(rng: np.random.Generator, shape, scale=1.0) -> np.ndarray:
     return bf16_bits((rng.standard_normal(shape) * scale).astype(np.float32))
 
 
+def ramp_case(rng: np.random.Generator, S: int, slope: float, q0: float, H: int = 2):
+    """Scores that move steadily along the keys: dim 0 of key j is slope*j and dim 0
+    of the queries is +q0 (even rows: scores rise along the keys) or -q0 (odd rows:
+    they fall), the other dims small noise.  Returns q, k, v as bf16 bits."""
+    q = rng.standard_normal((1, H, S, 128)).astype(np.float32) * 0.1
+    k = rng.standard_normal((1, H, S, 128)).astype(np.float32) * 0.1
+    v = rng.standard_normal((1, H, S, 128)).astype(np.float32)
+    q[..., 0] = np.where(np.arange(S) % 2 == 0, q0, -q0)
+    k[..., 0] = slope * np.arange(S)
+    return tuple(bf16_bits(x) for x in (q, k, v))
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """The MI355X device; fails loudly when absent (GPU tests must not silently skip)."""

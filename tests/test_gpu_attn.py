@@ -14,7 +14,7 @@ import torch
 
 import h3attn
 import oracle
-from conftest import assert_close_absmax, from_dev_bf16, randn_bf16, to_dev_bf16
+from conftest import assert_close_absmax, from_dev_bf16, ramp_case, randn_bf16, to_dev_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -126,24 +126,15 @@ def test_constant_value_rows(gpu):
     assert np.abs(o - 1.5).max() <= 1.5 * 2.0 ** -7
 
 
-def _ramp_case(rng, S, slope, q0):
-    """Scores that move steadily along the keys: dim 0 of key j is slope*j and
-    dim 0 of the queries is +-q0, the other dims small noise."""
-    q = rng.standard_normal((1, 2, S, 128)).astype(np.float32) * 0.1
-    k = rng.standard_normal((1, 2, S, 128)).astype(np.float32) * 0.1
-    v = rng.standard_normal((1, 2, S, 128)).astype(np.float32)
-    q[..., 0] = np.where(np.arange(S) % 2 == 0, q0, -q0)  # even rows rise, odd rows fall
-    k[..., 0] = slope * np.arange(S)
-    return tuple(oracle.f32_to_bf16(x) for x in (q, k, v))
-
-
-@pytest.mark.parametrize("S", [300, 1000])
-def test_running_max_rises_by_hundreds(gpu, S):
-    """Even query rows see scores that rise by ~26 (log2 units) every 64 keys, ~400 in
-    all: exp2 against the first stage's max would overflow many times over, so the
-    running max must be refreshed.  Odd rows fall and underflow towards zero."""
+@pytest.mark.parametrize("S,slope", [(300, 4 / 3), (1000, 0.4), (1000, 0.0383)])
+def test_running_max_rises(gpu, S, slope):
+    """Even query rows see scores rising steadily along the keys: 64*slope/sqrt(128)
+    per key, i.e. ~700, ~210 and ~20 (log2 units) per 64-key stage for the three cases,
+    ~3300 / ~3300 / ~310 in all.  exp2 against the first stage's max would overflow, so
+    the running max is refreshed at every stage (first two) or every few stages, with
+    p up to 2^64 accepted in between (third).  Odd rows fall and underflow to zero."""
     rng = np.random.default_rng(30)
-    q, k, v = _ramp_case(rng, S, slope=0.4 * 1000 / S, q0=64.0)
+    q, k, v = ramp_case(rng, S, slope=slope, q0=64.0)
     o = _run(q, k, v, gpu)
     assert np.isfinite(o).all()
     assert_close_absmax(o, oracle.attn_fwd(q, k, v, round_p=True), what="rising max")

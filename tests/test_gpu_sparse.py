@@ -15,7 +15,7 @@ import torch
 
 import h3attn
 import oracle
-from conftest import assert_close_absmax, from_dev_bf16, randn_bf16, to_dev_bf16
+from conftest import assert_close_absmax, from_dev_bf16, ramp_case, randn_bf16, to_dev_bf16
 from h3attn import ops, sla
 
 pytestmark = pytest.mark.gpu
@@ -70,6 +70,69 @@ def test_all_blocks_kept_equals_dense(gpu, blk_k):
     o_d = h3attn.attn_fwd(q, k, v, split_tail=False)
     torch.cuda.synchronize()
     assert torch.equal(o_s, o_d)
+
+
+@pytest.mark.parametrize("blk,slope", [(64, 0.4), (128, 0.4), (128, 0.0383)])
+def test_sparse_running_max_rises(gpu, blk, slope):
+    """Even rows see scores rising along the keys (~210 or ~20 log2 units per 64 keys),
+    odd rows falling, over a random half of the key blocks plus the diagonal: the
+    running max is refreshed along the LUT order at every stage or every few stages."""
+    rng = np.random.default_rng(40 + blk)
+    S = 1000
+    q, k, v = ramp_case(rng, S, slope=slope, q0=64.0)
+    nk = -(-S // blk)
+    bmap = (rng.random((1, 2, nk, nk)) < 0.5).astype(np.uint8)
+    for i in range(nk):
+        bmap[:, :, i, i] = 1  # the diagonal block
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, blk, blk)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    assert np.isfinite(got).all()
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
+    assert_close_absmax(got, ref, what=f"sparse rising max blk={blk}")
+
+
+def test_sparse_lone_dominant_key(gpu):
+    """One kept key out-scores the rest by ~160 (log2 units): rows whose blocks include
+    it return its value row."""
+    rng = np.random.default_rng(42)
+    S, blk = 777, 128
+    q = rng.standard_normal((1, 1, S, 128)).astype(np.float32) * 0.1
+    k = rng.standard_normal((1, 1, S, 128)).astype(np.float32) * 0.1
+    v = rng.standard_normal((1, 1, S, 128)).astype(np.float32)
+    q[..., 0] = 64.0
+    k[:, :, 500, 0] = 20.0
+    q, k, v = (oracle.f32_to_bf16(x) for x in (q, k, v))
+    nk = -(-S // blk)
+    bmap = np.ones((1, 1, nk, nk), np.uint8)
+    bmap[0, 0, 0, 500 // blk] = 0  # the first query block does not see the key
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, blk, blk)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
+    assert_close_absmax(got, ref, what="sparse lone dominant key")
+    vrow = oracle.bf16_to_f32(v).reshape(v.shape)[0, 0, 500]
+    assert np.abs(got[0, 0, blk:] - vrow).max() <= 2.0 ** -8 * np.abs(vrow).max()
+
+
+@pytest.mark.parametrize("bad", [-1, 10**6])
+def test_lut_leading_invalid_entry_changes_nothing(gpu, bad):
+    """A LUT row whose first entries name no key block (-1, or a block past the keys)
+    starts with fully masked stages.  The result equals the row without them, bit for
+    bit: the first valid stage sets the reference max exactly either way."""
+    rng = np.random.default_rng(43)
+    S, blk = 1000, 128
+    q, k, v = (to_dev_bf16(randn_bf16(rng, (1, 2, S, 128)), gpu) for _ in range(3))
+    nq = nk = -(-S // blk)
+    kept = [sorted(rng.choice(nk, size=3, replace=False).tolist()) for _ in range(2 * nq)]
+    lut_a = torch.tensor([row + [-1, -1] for row in kept], dtype=torch.int32).view(1, 2, nq, 5)
+    cnt_a = torch.full((1, 2, nq), 3, dtype=torch.int32)
+    lut_b = torch.tensor([[bad, bad] + row for row in kept], dtype=torch.int32).view(1, 2, nq, 5)
+    cnt_b = torch.full((1, 2, nq), 5, dtype=torch.int32)
+    o_a = h3attn.attn_fwd_blocksparse(q, k, v, lut_a.to(gpu), cnt_a.to(gpu), blk, blk)
+    o_b = h3attn.attn_fwd_blocksparse(q, k, v, lut_b.to(gpu), cnt_b.to(gpu), blk, blk)
+    torch.cuda.synchronize()
+    assert torch.equal(o_a, o_b)
 
 
 def test_empty_rows_give_zero(gpu):
