@@ -88,6 +88,10 @@ namespace h3a {
 #ifndef H3A_PP_READ_AHEAD
 #define H3A_PP_READ_AHEAD 6
 #endif
+// LDS operand reads issued after each MFMA of a ping-pong matrix cluster.
+#ifndef H3A_PP_READS_PER_MFMA
+#define H3A_PP_READS_PER_MFMA 2
+#endif
 // Row sum from the bf16-rounded P (v_dot2, 16 ops) instead of the unrounded
 // p (32 adds).  Off by default: the reference sums unrounded p.
 #ifndef H3A_ROWSUM_BF16
@@ -815,7 +819,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16 * NSUB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
     }
 #endif
     __builtin_amdgcn_s_setprio(0);
