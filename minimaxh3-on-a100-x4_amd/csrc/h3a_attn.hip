@@ -88,6 +88,11 @@ namespace h3a {
 #ifndef H3A_PP_READ_AHEAD
 #define H3A_PP_READ_AHEAD 6
 #endif
+// Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
+// during the softmax cluster (2), or never (0).
+#ifndef H3A_PP_PRIO
+#define H3A_PP_PRIO 1
+#endif
 // LDS operand reads issued after each MFMA of a ping-pong matrix cluster.
 #ifndef H3A_PP_READS_PER_MFMA
 #define H3A_PP_READS_PER_MFMA 2
@@ -806,7 +811,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   // after each MFMA, so every read is in flight for several MFMAs.
   auto mfma = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
-    __builtin_amdgcn_s_setprio(1);
+    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(1);
 #if H3A_PP_PV_FIRST
     pv_tile<L, 2 * NSUB>(vbuf[P], pf, v_rd, o);
     score_tile<L, NSUB>(kbuf[P ^ 1], qf, k_rd, s);
@@ -822,9 +827,10 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
     }
 #endif
-    __builtin_amdgcn_s_setprio(0);
+    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(0);
   };
   auto soft = [&](int j) __attribute__((always_inline)) {
+    if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(1);
 #if H3A_PP_STALE_MAX
     softmax_stage_stale<NSUB>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
 #else
@@ -836,6 +842,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     pin(lsum);
     pin(m);
 #endif
+    if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(0);
   };
 
   if (lead) {
