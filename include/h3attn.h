@@ -95,8 +95,9 @@ int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o,
  *   lut[((b*H + h)*nqb + qb)*max_k_blocks + 0 .. counts[(b*H+h)*nqb + qb]-1]
  * (key-block indices in units of blk_k keys; nqb = ceil(Sq/blk_q)).
  * Skipped blocks contribute nothing; a query block with no kept key block
- * gets O = 0.  blk_q in {64,128}; blk_k in {64,128}.  Other arguments as
- * h3a_attn_fwd.
+ * gets O = 0.  LUT entries that name no key block (negative, or at or past
+ * ceil(Skv/blk_k)) are skipped as well.  blk_q in {64,128}; blk_k in
+ * {64,128}.  Other arguments as h3a_attn_fwd.
  */
 int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o,
                              int B, int H, int Sq, int Skv, int D,
