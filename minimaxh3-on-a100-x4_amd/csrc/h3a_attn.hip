@@ -93,6 +93,11 @@ namespace h3a {
 #ifndef H3A_PP_PRIO
 #define H3A_PP_PRIO 1
 #endif
+// Workgroup barrier between the two clusters of a ping-pong stage (1), or
+// only the one at the end of the stage (0), which the LDS buffers need.
+#ifndef H3A_PP_MID_BARRIER
+#define H3A_PP_MID_BARRIER 1
+#endif
 // LDS operand reads issued after each MFMA of a ping-pong matrix cluster.
 #ifndef H3A_PP_READS_PER_MFMA
 #define H3A_PP_READS_PER_MFMA 2
@@ -706,6 +711,15 @@ __device__ __forceinline__ void slot_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// The boundary between the two clusters of a ping-pong stage.
+__device__ __forceinline__ void mid_barrier() {
+#if H3A_PP_MID_BARRIER
+  slot_barrier();
+#else
+  __builtin_amdgcn_sched_barrier(0);
+#endif
+}
+
 // Dense ping-pong kernel: 8 waves x 32 query rows (one 256-row query tile per
 // workgroup); waves 0-3 (group A) and 4-7 (group B) sit one of each per SIMD.
 // Every stage of BN = 32*NSUB keys is split into a matrix-core cluster,
@@ -849,7 +863,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
       dma(par, j);
       mfma(par);
-      slot_barrier();
+      mid_barrier();
       if (j + 1 < niter) soft(j);
       wait_vmem_all();
       slot_barrier();
@@ -864,7 +878,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     auto stage = [&](auto par, int j, auto first) __attribute__((always_inline)) {
       dma(par, j);
       if constexpr (!decltype(first)::value) soft(j - 1);
-      slot_barrier();
+      mid_barrier();
       mfma(par);
       wait_vmem_all();
       slot_barrier();
