@@ -79,6 +79,11 @@ namespace h3a {
 #ifndef H3A_PP_STALE_MAX
 #define H3A_PP_STALE_MAX 1
 #endif
+// Block-sparse attention with 128-row query blocks: ping-pong kernel over
+// pairs of query blocks (1), or the single-group attn_fwd_kernel (0).
+#ifndef H3A_SPARSE_PINGPONG
+#define H3A_SPARSE_PINGPONG 0
+#endif
 // Block-sparse attn_fwd_kernel: K/V staged through VGPRs (1) or by LDS DMA (0).
 #ifndef H3A_SPARSE_REGS
 #define H3A_SPARSE_REGS 1
@@ -677,21 +682,24 @@ __device__ __forceinline__ void exp_pack_sum(const f32x16 (&s)[NSUB], float sl2,
   ps = a[0];
 }
 
-template <int NSUB>
+// kMaybeEmpty: m may still be -inf on entry (every earlier stage of the row
+// was fully masked, as block-sparse rows can be).  p is then formed against 0
+// and the stage always refreshes.
+template <int NSUB, bool kMaybeEmpty = false>
 __device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0, int Skv, int g, float sl2,
                                                     float &m, float &lsum, f32x16 (&o)[4],
                                                     u32x4 (&pf)[2 * NSUB]) {
   if (key0 + 32 * NSUB > Skv) mask_tail<NSUB>(s, key0, Skv, g);
   float ps;
-  exp_pack_sum<NSUB>(s, sl2, m, pf, ps);
-  if (__builtin_amdgcn_ballot_w64(!(ps <= kStaleSumLimit)) != 0) {
+  exp_pack_sum<NSUB>(s, sl2, kMaybeEmpty && m == kNegInf ? 0.f : m, pf, ps);
+  if (__builtin_amdgcn_ballot_w64(!(ps <= kStaleSumLimit) || (kMaybeEmpty && m == kNegInf)) != 0) {
     const float mnew = fmaxf(m, tile_max<NSUB>(s, sl2));
-    const float alpha = fast_exp2(m - mnew);
+    const float alpha = fast_exp2(m - (kMaybeEmpty && mnew == kNegInf ? 0.f : mnew));
     m = mnew;
     lsum *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-    exp_pack_sum<NSUB>(s, sl2, m, pf, ps);
+    exp_pack_sum<NSUB>(s, sl2, kMaybeEmpty && m == kNegInf ? 0.f : m, pf, ps);
   }
   lsum += ps;
 }
@@ -736,26 +744,44 @@ __device__ __forceinline__ void mid_barrier() {
 // both groups finished by the end of slot 2j; the data is read by MFMA(j+1)
 // from slot 2j+3 on, after every wave waited for its share of the DMA at the
 // end of slot 2j+2.
-template <class L, int NSUB>
+//
+// kSparse: block-sparse attention over pairs of 128-row query blocks.  Group A
+// takes query block 2p and group B block 2p+1 of pair p, each with its own LUT
+// row, its own double-buffered K/V stages in LDS and its own DMA (its 4 waves
+// split each tile); the barrier slots are as above.  Both groups step through
+// the longer of their two stage lists; the shorter one's extra stages load
+// nothing and are fully masked.
+template <class L, int NSUB, bool kSparse = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   constexpr int NW = 8;
   constexpr int BN = 32 * NSUB;  // keys per stage
   constexpr int kKE = StageBytes<L, BN>::kK / 2, kVE = StageBytes<L, BN>::kV / 2;  // elements
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kKE];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kVE];
+  constexpr int NG = kSparse ? 2 : 1;  // K/V streams
+  static_assert(!kSparse || BN == kBN, "block-sparse stages are 64 keys");
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[NG][2][kKE];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[NG][2][kVE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const bool lead = wave_u < NW / 2;  // group A
+  const int grp = kSparse ? (lead ? 0 : 1) : 0;
+  uint16_t(*kbuf)[kKE] = kbuf_all[grp];
+  uint16_t(*vbuf)[kVE] = vbuf_all[grp];
   const int nstages = (a.Skv + BN - 1) / BN;
   // Work item of this workgroup.  With a split tail, the first
   // a.split_first items are whole query tiles; each later tile is cut into
   // a.split_pieces contiguous ranges of stages, one per workgroup, whose
   // partial results are merged by split_combine_kernel.
   int w, piece = -1, j0 = 0, niter = nstages;
-  if ((int)blockIdx.x < a.split_first) {
+  if (kSparse) {
+#if H3A_XCD_REMAP
+    w = xcd_remap(blockIdx.x, a.total);
+#else
+    w = blockIdx.x;
+#endif
+  } else if ((int)blockIdx.x < a.split_first) {
     const int whole = a.split_first < a.total ? a.split_first : a.total;
 #if H3A_XCD_REMAP
     w = xcd_remap(blockIdx.x, whole);
@@ -769,16 +795,51 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     j0 = (int)((int64_t)nstages * p / a.split_pieces);
     niter = (int)((int64_t)nstages * (p + 1) / a.split_pieces) - j0;  // >= 1
   }
-  const int qt = w % a.nqt, bh = w / a.nqt;
+  // Sparse: a.nqt counts 128-row query blocks and w runs over (b, h, pair).
+  const int nw_bh = kSparse ? (a.nqt + 1) / 2 : a.nqt;
+  const int qt = w % nw_bh, bh = w / nw_bh;
   const int h = bh % a.H, b = bh / a.H;
   const uint16_t *Qb = a.q + b * a.qsb + h * a.qsh;
   const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
   const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
   uint16_t *Ob = a.o + b * a.osb + h * a.osh;
-  const int qrow = qt * 256 + wave * 32 + l32;
-  // First key of local stage j; past the last stage it is Skv, which loads
-  // nothing (zeros).
-  auto key_base = [&](int j) __attribute__((always_inline)) -> int { return j < niter ? (j0 + j) * BN : a.Skv; };
+  const int qrow = kSparse ? (2 * qt + grp) * 128 + (wave_u & 3) * 32 + l32 : qt * 256 + wave * 32 + l32;
+  // This group's stage count and LUT row (sparse).
+  int ngrp = niter;
+  const int32_t *lut_row = nullptr;
+  if constexpr (kSparse) {
+    auto stages_of = [&](int qb) __attribute__((always_inline)) -> int {
+      if (qb >= a.nqt) return 0;
+      const int cnt = a.counts[(int64_t)bh * a.nqt + qb];
+      return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
+    };
+    const int qb = 2 * qt + grp;
+    ngrp = stages_of(qb);
+    const int nother = stages_of(2 * qt + 1 - grp);
+    niter = ngrp > nother ? ngrp : nother;
+    lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
+  }
+  // First key of local stage j; past this group's last stage, and for LUT
+  // entries that name no key block, it is Skv, which loads nothing (zeros).
+  auto key_base = [&](int j) __attribute__((always_inline)) -> int {
+    if constexpr (kSparse) {
+      if (j >= ngrp) return a.Skv;
+      const int kb = lut_row[j / a.sub];
+      const int key0 = kb * a.blk_k + (j % a.sub) * BN;
+      return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
+    } else {
+      return j < niter ? (j0 + j) * BN : a.Skv;
+    }
+  };
+  if (kSparse && niter == 0) {
+    // Neither query block of the pair keeps a key block: O = 0.
+    if (qrow < a.Sq) {
+      uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
+    }
+    return;
+  }
 
   u32x4 qf[8];
   if (qrow < a.Sq) {
@@ -797,10 +858,13 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   const int k_rd = L::k_base(l32, g);
   const int v_rd = L::v_base(lane);
 
-  TileDma<NW, L, false, BN> kdma;
-  TileDma<NW, L, true, BN> vdma;
-  kdma.init(a.kss, wave_u, lane);
-  vdma.init(a.vss, wave_u, lane);
+  // Each K/V stream is fetched by the waves that read it: all 8 (dense) or
+  // the 4 of the group (sparse).
+  constexpr int NWD = NW / NG;
+  TileDma<NWD, L, false, BN> kdma;
+  TileDma<NWD, L, true, BN> vdma;
+  kdma.init(a.kss, kSparse ? (wave_u & 3) : wave_u, lane);
+  vdma.init(a.vss, kSparse ? (wave_u & 3) : wave_u, lane);
 
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
   kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
@@ -846,7 +910,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   auto soft = [&](int j) __attribute__((always_inline)) {
     if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(1);
 #if H3A_PP_STALE_MAX
-    softmax_stage_stale<NSUB>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
+    softmax_stage_stale<NSUB, kSparse>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
 #else
     softmax_stage<NSUB>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
 #endif
@@ -1109,6 +1173,14 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
 }
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
+  if (H3A_SPARSE_PINGPONG && blk_q == 128) {
+    AttnArgs p = a;
+    const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
+    if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
+    p.total = (int)pairs;
+    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SwzLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
+    return check_launch("attn_fwd_pingpong_kernel<sparse>");
+  }
   if (blk_q == 128) {
     hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(256), 0, s, a);
   } else {
