@@ -7,12 +7,12 @@
 //   block_pool_kernel   : bf16 [B,H,S,128] (strided) -> fp32 block means
 //                         [B,H,ceil(S/blk),128], over the valid rows of each
 //                         block.  HBM-bound: reads the tensor once.
-//   block_select_kernel : one workgroup per (b,h,query block): scores against
-//                         all key blocks into LDS, rank by (score desc, index
-//                         asc), keep rank < keep plus the optional diagonal,
-//                         and write the kept indices in ascending order (the
-//                         LUT h3a_attn_fwd_blocksparse consumes), the count,
-//                         and optionally the 0/1 map.
+//   block_select_kernel : up to 8 query blocks of one (b,h) per workgroup:
+//                         scores against all key blocks into LDS, rank by
+//                         (score desc, index asc), keep rank < keep plus the
+//                         optional diagonal, and write the kept indices in
+//                         ascending order (the LUT h3a_attn_fwd_blocksparse
+//                         consumes), the count, and optionally the 0/1 map.
 // Centring k by its sequence mean (SLA's K smoothing) shifts every score of a
 // row by the same amount, so it never changes the selection and is not needed.
 #include "h3a_device.h"
@@ -59,61 +59,141 @@ __global__ void __launch_bounds__(256) block_pool_kernel(const uint16_t *x, int6
 }
 
 constexpr int kSelThreads = 256;
+#ifndef H3A_SEL_ROWS
+#define H3A_SEL_ROWS 8
+#endif
+constexpr int kSelRowsMax = H3A_SEL_ROWS;  // query blocks per workgroup (at most)
+constexpr int kSelKeyChunk = 32;        // pooled key vectors staged in LDS at a time
+constexpr int kSelKeyPitch = kPoolD + 4; // floats per staged key row (bank spread)
+// LDS for the score rows: 64 KiB minus the query rows and the key chunk.
+constexpr int kSelScoreBytes = 65536 - (H3A_SEL_ROWS * kPoolD + kSelKeyChunk * kSelKeyPitch) * 4;
 
+// R (<= kSelRowsMax) query blocks of one (b,h) per workgroup, so each pooled
+// key vector is read from memory once per R rows.  Scores of all R rows go to
+// LDS (same fp32 FMA order as a plain dot product over d = 0..127).  Then wave
+// w selects rows w, w+4, with lane l on key blocks j = 64c + l: a bitwise
+// search over order-preserving keys finds the row's keep-th largest score in
+// 32 counting rounds (ballot + popcount), which fixes the kept set under
+// (score desc, index asc) order without ranking every pair.  Kept indices are
+// written in ascending order with one ballot per 64-key chunk.
 __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
-    const float *pq, const float *pk, int nq, int nk, int keep, int force_diag, int blk_q,
-    int blk_k, int32_t *lut, int32_t *counts, int max_k, uint8_t *map) {
+    const float *pq, const float *pk, int nq, int nk, int rows_per_wg, int keep, int force_diag,
+    int blk_q, int blk_k, int32_t *lut, int32_t *counts, int max_k, uint8_t *map) {
   extern __shared__ float sel_lds[];
-  float *sc = sel_lds;                       // [nk] scores
-  float *q = sel_lds + nk;                   // [128] pooled query block
-  int *flag = (int *)(sel_lds + nk + kPoolD);  // [nk] kept flags
-  const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;            // (b*H + h)*nq + i
-  const int i = (int)(row % nq);
-  const int64_t bh = row / nq;
+  float *qs = sel_lds;                                   // [kSelRowsMax][128] pooled query blocks
+  float *ks = qs + kSelRowsMax * kPoolD;                 // [kSelKeyChunk][kSelKeyPitch] key chunk
+  float *sc = ks + kSelKeyChunk * kSelKeyPitch;          // [R][nk] scores
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int R = rows_per_wg;
+  const int ngroups = (nq + R - 1) / R;
+  const int64_t bh = blockIdx.x / ngroups;
+  const int i0 = (int)(blockIdx.x % ngroups) * R;
+  const int nrows = nq - i0 < R ? nq - i0 : R;
+  for (int t = tid; t < kSelRowsMax * kPoolD; t += kSelThreads) {
+    const int r = t / kPoolD;
+    qs[t] = r < nrows ? pq[((bh * nq) + i0 + r) * kPoolD + (t % kPoolD)] : 0.f;
+  }
+  // Scores, kSelKeyChunk key blocks at a time: the chunk is staged with
+  // coalesced 16-byte loads, then thread (r, kk) forms one dot product in
+  // the order d = 0..127.
   const float *pkh = pk + bh * (int64_t)nk * kPoolD;
-  if (tid < kPoolD) q[tid] = pq[row * kPoolD + tid];
-  __syncthreads();
-  for (int j = tid; j < nk; j += kSelThreads) {
-    const float *kr = pkh + (int64_t)j * kPoolD;
-    float acc = 0.f;
+  const int my_r = tid / kSelKeyChunk, my_k = tid % kSelKeyChunk;
+  static_assert(kSelRowsMax * kSelKeyChunk <= kSelThreads, "one dot product per thread per chunk");
+  for (int kc = 0; kc < nk; kc += kSelKeyChunk) {
+    __syncthreads();  // qs written / previous chunk consumed
+    for (int t = tid; t < kSelKeyChunk * (kPoolD / 4); t += kSelThreads) {
+      const int kk = t / (kPoolD / 4), f4 = t % (kPoolD / 4);
+      const float4 v = kc + kk < nk ? *(const float4 *)(pkh + (int64_t)(kc + kk) * kPoolD + 4 * f4)
+                                    : float4{0.f, 0.f, 0.f, 0.f};
+      *(float4 *)(ks + kk * kSelKeyPitch + 4 * f4) = v;
+    }
+    __syncthreads();
+    if (my_r < nrows && kc + my_k < nk) {
+      const float *qr = qs + my_r * kPoolD;
+      const float *kr = ks + my_k * kSelKeyPitch;
+      float acc = 0.f;
 #pragma unroll 8
-    for (int d = 0; d < kPoolD; d += 4) {
-      const float4 kv = *(const float4 *)(kr + d);
-      acc = fmaf(q[d], kv.x, acc);
-      acc = fmaf(q[d + 1], kv.y, acc);
-      acc = fmaf(q[d + 2], kv.z, acc);
-      acc = fmaf(q[d + 3], kv.w, acc);
+      for (int d = 0; d < kPoolD; d += 4) {
+        const float4 q4 = *(const float4 *)(qr + d);
+        const float4 k4 = *(const float4 *)(kr + d);
+        acc = fmaf(q4.x, k4.x, acc);
+        acc = fmaf(q4.y, k4.y, acc);
+        acc = fmaf(q4.z, k4.z, acc);
+        acc = fmaf(q4.w, k4.w, acc);
+      }
+      sc[my_r * nk + kc + my_k] = acc;
     }
-    sc[j] = acc;
   }
   __syncthreads();
-  const int diag = (int)(((int64_t)i * blk_q) / blk_k);
-  for (int j = tid; j < nk; j += kSelThreads) {
-    const float v = sc[j];
-    int rank = 0;
-    for (int t = 0; t < nk; ++t) {
-      const float u = sc[t];
-      rank += (u > v) || (u == v && t < j);
+
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));  // lanes < this one
+  // Order-preserving key of a score: larger score <=> larger key (-0 as +0).
+  auto key_of = [](float x) __attribute__((always_inline)) -> uint32_t {
+    const uint32_t u = __float_as_uint(x + 0.f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  };
+  const int nchunks = (nk + 63) / 64;
+  // Rows of up to kSelRegChunks*64 key blocks keep their keys in registers
+  // for the counting rounds; longer rows re-read them from LDS each round.
+  constexpr int kSelRegChunks = 8;
+  const bool in_regs = nchunks <= kSelRegChunks;
+  for (int r = wave; r < nrows; r += kSelThreads / 64) {
+    const float *row_sc = sc + r * nk;
+    const int64_t row = bh * nq + i0 + r;
+    const int diag = (int)(((int64_t)(i0 + r) * blk_q) / blk_k);
+    int32_t *out = lut + row * max_k;
+    uint32_t kr[kSelRegChunks];  // valid keys; 0 (never counted: t >= 1 below) past nk
+#pragma unroll
+    for (int c = 0; c < kSelRegChunks; ++c) {
+      const int j = c * 64 + lane;
+      kr[c] = (in_regs && j < nk) ? key_of(row_sc[j < nk ? j : 0]) : 0u;
     }
-    flag[j] = (rank < keep) || (force_diag && j == diag);
-  }
-  __syncthreads();
-  int32_t *out = lut + row * max_k;
-  for (int j = tid; j < nk; j += kSelThreads) {
-    if (map) map[row * nk + j] = (uint8_t)flag[j];
-    if (flag[j]) {
-      int pos = 0;
-      for (int t = 0; t < j; ++t) pos += flag[t];
-      if (pos < max_k) out[pos] = j;
+    // Number of the row's keys >= t.  Every t asked for is >= 1, every score
+    // that is not a NaN has a key > 0, and the padding key 0 is never counted.
+    auto count_ge = [&](uint32_t t) __attribute__((always_inline)) -> int {
+      int n = 0;
+      if (in_regs) {
+#pragma unroll
+        for (int c = 0; c < kSelRegChunks; ++c) n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(kr[c] >= t));
+      } else {
+        for (int c = 0; c < nchunks; ++c) {
+          const int j = c * 64 + lane;
+          n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < nk && key_of(row_sc[j < nk ? j : 0]) >= t));
+        }
+      }
+      return n;
+    };
+    // T = the keep-th largest key: the largest t with count_ge(t) >= keep,
+    // built from the top bit down.  Then exactly the keys > T and the first
+    // (keep - #keys > T) keys == T in index order have rank < keep under
+    // (score desc, index asc).
+    uint32_t T = 0;
+    int need = 0;  // keys == T to keep
+    if (keep > 0) {
+      for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = T | (1u << bit);
+        if (count_ge(cand) >= keep) T = cand;
+      }
+      need = keep - (T == 0xffffffffu ? 0 : count_ge(T + 1));
     }
-  }
-  if (tid == 0) {
-    int total = 0;
-    for (int t = 0; t < nk; ++t) total += flag[t];
-    const int kept = total < max_k ? total : max_k;
-    counts[row] = kept;
-    for (int t = kept; t < max_k; ++t) out[t] = -1;
+    int base = 0, eq_before = 0;
+    for (int c = 0; c < nchunks; ++c) {
+      const int j = c * 64 + lane;
+      const uint32_t kj = j < nk ? key_of(row_sc[j < nk ? j : 0]) : 0u;
+      const bool eq = keep > 0 && j < nk && kj == T;
+      const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
+      const bool by_rank = keep > 0 && j < nk && (kj > T || (eq && eq_before + __builtin_popcountll(eqm & below) < need));
+      const bool kept = by_rank || (force_diag && j == diag && j < nk);
+      eq_before += __builtin_popcountll(eqm);
+      const uint64_t m = __builtin_amdgcn_ballot_w64(kept);
+      const int pos = base + __builtin_popcountll(m & below);
+      if (kept && pos < max_k) out[pos] = j;
+      if (map && j < nk) map[row * nk + j] = (uint8_t)kept;
+      base += __builtin_popcountll(m);
+    }
+    const int kept_n = base < max_k ? base : max_k;
+    for (int t = kept_n + lane; t < max_k; t += 64) out[t] = -1;
+    if (lane == 0) counts[row] = kept_n;
   }
 }
 
@@ -129,9 +209,12 @@ int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int 
 int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, int nk, int keep,
                         int force_diag, int blk_q, int blk_k, int32_t *lut, int32_t *counts,
                         int max_k, uint8_t *map, hipStream_t s) {
-  const size_t lds = (size_t)(2 * nk + kPoolD) * sizeof(float);
-  hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)((int64_t)B * H * nq)), dim3(kSelThreads), lds,
-                     s, pq, pk, nq, nk, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);
+  int rows = kSelScoreBytes / (nk * (int)sizeof(float));
+  rows = rows < 1 ? 1 : (rows > kSelRowsMax ? kSelRowsMax : rows);
+  const size_t lds = (size_t)(kSelRowsMax * kPoolD + kSelKeyChunk * kSelKeyPitch + rows * nk) * sizeof(float);
+  const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
+  hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)groups), dim3(kSelThreads), lds, s, pq, pk, nq,
+                     nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);
   return check_launch("block_select_kernel");
 }
 

@@ -198,6 +198,45 @@ def test_block_select_matches_oracle(gpu, blk, keep, diag):
     assert np.array_equal(lut.cpu().numpy(), rl)
 
 
+def _select_ref(pq, pk, keep, blk_q, blk_k, diag, max_k):
+    """Selection from exact scores: rank by (score desc, index asc), keep the first
+    `keep` plus the diagonal, list them ascending, truncate to max_k."""
+    B, H, nq, _ = pq.shape
+    nk = pk.shape[2]
+    sc = np.einsum("bhid,bhjd->bhij", pq.astype(np.float64), pk.astype(np.float64))
+    bmap = np.zeros((B, H, nq, nk), np.uint8)
+    lut = np.full((B, H, nq, max_k), -1, np.int32)
+    cnt = np.zeros((B, H, nq), np.int32)
+    for b, h, i in np.ndindex(B, H, nq):
+        order = np.lexsort((np.arange(nk), -sc[b, h, i]))  # score desc, then index asc
+        kept = set(order[:keep].tolist())
+        if diag and i * blk_q // blk_k < nk:
+            kept.add(i * blk_q // blk_k)
+        kept = sorted(kept)
+        bmap[b, h, i, kept] = 1
+        cnt[b, h, i] = min(len(kept), max_k)
+        lut[b, h, i, :cnt[b, h, i]] = kept[:max_k]
+    return bmap, lut, cnt
+
+
+@pytest.mark.parametrize("nq,nk,keep,diag,max_k", [
+    (9, 700, 37, True, 38), (17, 65, 1, False, 1), (1, 64, 64, False, 64), (9, 1, 1, True, 1),
+    (17, 700, 100, True, 50), (16, 200, 20, False, 20)])
+def test_block_select_exact_ties(gpu, nq, nk, keep, diag, max_k):
+    """Integer pooled vectors make every score an exact fp32 integer, with many ties:
+    the kept set, its order and the truncation to max_k_blocks must match exactly
+    (row groups of up to 8 query blocks per workgroup, several 512-key ranking passes)."""
+    rng = np.random.default_rng(50 + nq + nk)
+    pq = rng.integers(-2, 3, (1, 2, nq, 128)).astype(np.float32)
+    pk = rng.integers(-2, 3, (1, 2, nk, 128)).astype(np.float32)
+    bmap, lut, cnt = ops.block_select(torch.from_numpy(pq).to(gpu), torch.from_numpy(pk).to(gpu), keep,
+                                      128, 128, force_diag=diag, max_k_blocks=max_k)
+    rmap, rlut, rcnt = _select_ref(pq, pk, keep, 128, 128, diag, max_k)
+    assert np.array_equal(bmap.cpu().numpy(), rmap)
+    assert np.array_equal(cnt.cpu().numpy(), rcnt)
+    assert np.array_equal(lut.cpu().numpy(), rlut)
+
+
 def test_sparse_h56_s42120_full_shape(gpu):
     """H=56, S=42120, 128x128 tiles, top 25% + diagonal (the H3 sparse workload); checked on 2 heads."""
     S, H, blk = 42120, 56, 128
