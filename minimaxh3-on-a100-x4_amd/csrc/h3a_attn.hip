@@ -93,6 +93,17 @@ namespace h3a {
 #ifndef H3A_PP_READ_AHEAD
 #define H3A_PP_READ_AHEAD 6
 #endif
+// Dense ping-pong fetch split: instructions of each K and V stage (4 per wave
+// column: waves w and w+4 of the two groups) that the group-A wave issues
+// (H3A_PP_A_KINST of K, H3A_PP_A_VINST of V); the group-B wave issues the
+// rest.  -1: every wave issues 2 + 2 over an 8-wave layout.  Default: group B
+// fetches everything, at the top of its softmax cluster.
+#ifndef H3A_PP_A_KINST
+#define H3A_PP_A_KINST 0
+#endif
+#ifndef H3A_PP_A_VINST
+#define H3A_PP_A_VINST 0
+#endif
 // Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
 // during the softmax cluster (2), or never (0).
 #ifndef H3A_PP_PRIO
@@ -236,12 +247,22 @@ struct TileDma {
   }
   __device__ __forceinline__ void issue(const uint16_t *base, int64_t ss, int key0, int Skv,
                                         uint16_t *tile) const {
-    const u32x4 d = desc(base, ss, key0, Skv);
-    uint32_t cur = first();
+    issue_range<0, kInst>(base, ss, key0, Skv, tile);
+  }
+  // Instructions I0 .. I1-1 of this wave's share.
+  template <int I0, int I1>
+  __device__ __forceinline__ void issue_range(const uint16_t *base, int64_t ss, int key0, int Skv,
+                                              uint16_t *tile) const {
+    if constexpr (I1 > I0) {
+      const u32x4 d = desc(base, ss, key0, Skv);
+      uint32_t cur = first();
 #pragma unroll
-    for (int i = 0; i < kInst; ++i) {
-      issue_one(d, i, cur, tile);
-      if (i + 1 < kInst) cur = next(cur);
+      for (int i = 0; i < I0; ++i) cur = next(cur);
+#pragma unroll
+      for (int i = I0; i < I1; ++i) {
+        issue_one(d, i, cur, tile);
+        if (i + 1 < I1) cur = next(cur);
+      }
     }
   }
   // Common staging interface: start() at the top of a stage, finish() at its
@@ -737,10 +758,11 @@ __device__ __forceinline__ void mid_barrier() {
 // while the other issues the softmax's VALU work and the two pipes overlap.
 //
 // Barrier slots after the prologue (both groups pass the same barriers):
-//   slot 2j+1:  A: DMA(j), MFMA(j)            B: DMA(j), SOFT(j-1)
-//   slot 2j+2:  A: SOFT(j), wait for DMA      B: MFMA(j), wait for DMA
-// DMA(j) fetches K(j+2) into kbuf[j&1] and V(j+1) into vbuf[(j+1)&1] (the 8
-// waves split each tile).  Those buffers were last read by MFMA(j-1), which
+//   slot 2j+1:  A: MFMA(j)                    B: DMA(j), SOFT(j-1)
+//   slot 2j+2:  A: SOFT(j)                    B: MFMA(j), wait for DMA(j)
+// DMA(j) fetches K(j+2) into kbuf[j&1] and V(j+1) into vbuf[(j+1)&1]; the 4
+// waves of group B split each tile (H3A_PP_A_KINST / H3A_PP_A_VINST give part
+// of it to group A instead).  Those buffers were last read by MFMA(j-1), which
 // both groups finished by the end of slot 2j; the data is read by MFMA(j+1)
 // from slot 2j+3 on, after every wave waited for its share of the DMA at the
 // end of slot 2j+2.
@@ -860,16 +882,37 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 
   // Each K/V stream is fetched by the waves that read it: all 8 (dense) or
   // the 4 of the group (sparse).
-  constexpr int NWD = NW / NG;
+  // Dense with H3A_PP_A_KINST >= 0: waves w and w+4 share one column of
+  // the 4-wave layout, split between them as the knobs say.
+  constexpr bool kSplitDma = !kSparse && H3A_PP_A_KINST >= 0;
+  constexpr int NWD = (kSparse || kSplitDma) ? NW / 2 : NW;
   TileDma<NWD, L, false, BN> kdma;
   TileDma<NWD, L, true, BN> vdma;
-  kdma.init(a.kss, kSparse ? (wave_u & 3) : wave_u, lane);
-  vdma.init(a.vss, kSparse ? (wave_u & 3) : wave_u, lane);
+  kdma.init(a.kss, NWD == NW ? wave_u : (wave_u & 3), lane);
+  vdma.init(a.vss, NWD == NW ? wave_u : (wave_u & 3), lane);
+  constexpr int kKA = kSplitDma ? H3A_PP_A_KINST : 0, kVA = kSplitDma ? H3A_PP_A_VINST : 0;
+  constexpr int kKI = decltype(kdma)::kInst, kVI = decltype(vdma)::kInst;
+  auto fetch_k = [&](const uint16_t *base, int key0, uint16_t *tile) __attribute__((always_inline)) {
+    if constexpr (kSplitDma) {
+      if (lead) kdma.template issue_range<0, kKA>(base, a.kss, key0, a.Skv, tile);
+      else kdma.template issue_range<kKA, kKI>(base, a.kss, key0, a.Skv, tile);
+    } else {
+      kdma.issue(base, a.kss, key0, a.Skv, tile);
+    }
+  };
+  auto fetch_v = [&](const uint16_t *base, int key0, uint16_t *tile) __attribute__((always_inline)) {
+    if constexpr (kSplitDma) {
+      if (lead) vdma.template issue_range<0, kVA>(base, a.vss, key0, a.Skv, tile);
+      else vdma.template issue_range<kVA, kVI>(base, a.vss, key0, a.Skv, tile);
+    } else {
+      vdma.issue(base, a.vss, key0, a.Skv, tile);
+    }
+  };
 
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
-  kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
-  vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
-  kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+  fetch_k(Kb, key_base(0), kbuf[0]);
+  fetch_v(Vb, key_base(0), vbuf[0]);
+  fetch_k(Kb, key_base(1), kbuf[1]);
   wait_vmem_all();
   __syncthreads();
   f32x16 s[NSUB];
@@ -880,8 +923,8 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 
   auto dma = [&](auto par, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;  // j & 1
-    kdma.issue(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
-    vdma.issue(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
+    fetch_k(Kb, key_base(j + 2), kbuf[P]);
+    fetch_v(Vb, key_base(j + 1), vbuf[P ^ 1]);
   };
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
