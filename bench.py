@@ -25,7 +25,7 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.
 # HBM bytes per launch of the dense kernel at this shape, from the rocprofv3
 # FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0) passes recorded in
 # profiles/attn_dense_h56_s42120_counters.txt (scales from a 2048 MiB copy).
-MEASURED_TRAFFIC_BYTES = 8.716e9
+MEASURED_TRAFFIC_BYTES = 9.06e9
 B, H, S, D, LAYERS = 1, 56, 42120, 128, 50
 
 
