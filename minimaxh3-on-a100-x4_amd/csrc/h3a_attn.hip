@@ -8,27 +8,33 @@
 // :405-420), O = acc / l with row-guarded stores (:443-457).  How it is
 // computed is CDNA4-specific:
 //
-//  * Workgroup = NW waves x 32 query rows (BM = 32*NW).  Each wave keeps its
-//    32 query rows as the B operand of v_mfma_f32_32x32x16_bf16 in VGPRs.
-//  * The score tile is produced transposed, S^T = K Q^T, so every lane owns a
-//    single query row (column l%32) and 32 of the 64 keys of a stage.  Row
-//    max is an in-register v_max3 chain plus one v_permlane32_swap with the
-//    partner lane; the row sum needs no cross-lane traffic until the end.
-//  * That layout is already the B operand of O^T += V^T P^T: P goes from the
-//    score accumulators straight into the PV MFMA (no LDS round trip).  V
-//    stays row-major in LDS and its A operand is read with ds_read_b64_tr_b16
-//    (LDS transpose reads), addressed so that the key order matches the
-//    score accumulator's.
-//  * K/V stages of 64 keys are double-buffered in LDS and fetched by LDS DMA
-//    (buffer_load_dwordx4 ... lds: HBM/L2 -> LDS with no VGPR staging and no
-//    ds_write) while the current stage is consumed (one barrier per stage).
-//    Rows are 256 B, XOR-swizzled at 16-byte granularity for conflict-free
-//    MFMA operand reads.  The buffer resource is rebased per stage so rows
-//    past Skv arrive as zeros and offsets are loop-invariant; the loop is
-//    unrolled by two so every LDS address is a base + immediate.
-//  * exp2-based softmax with scale*log2(e) folded into one FMA; the running
-//    max is refreshed only when a row outgrows it by 2^8 (lazy rescale).
-//  * Workgroup ids are remapped XCD-aware (xcd_remap).
+//  * Each wave keeps 32 query rows as the B operand of
+//    v_mfma_f32_32x32x16_bf16 in VGPRs and produces the score tile
+//    transposed, S^T = K Q^T, so every lane owns a single query row (column
+//    l%32) and 32 of the 64 keys of a stage.  That layout is already the B
+//    operand of O^T += V^T P^T: P goes from the score accumulators straight
+//    into the PV MFMA (no LDS round trip).  V stays row-major in LDS and its A
+//    operand is read with ds_read_b64_tr_b16 (LDS transpose reads), addressed
+//    so that the key order matches the score accumulator's.
+//  * Dense (attn_fwd_pingpong_kernel): 8 waves = 256 query rows per
+//    workgroup, in two groups with one wave of each per SIMD.  Every 64-key
+//    stage is a matrix-core cluster and a softmax cluster separated by
+//    workgroup barriers, group B one cluster behind group A, so one wave per
+//    SIMD issues MFMAs while the other issues the softmax's VALU work.  K/V
+//    stages are double-buffered in LDS (256-byte rows, XOR-swizzled at
+//    16-byte granularity for conflict-free operand reads) and fetched by LDS
+//    DMA (buffer_load_dwordx4 ... lds) from group B.  The softmax runs against
+//    a stale reference max and takes a row max only when a stage's p sum
+//    overflows its bound.  A split tail cuts the last, partly filled round of
+//    query tiles into key ranges merged by split_combine_kernel.
+//  * Block-sparse (attn_fwd_kernel with kSparse): the LUT row of a query block
+//    lists the key stages; 4 waves per workgroup, two workgroups per CU, K/V
+//    staged through VGPRs into padded LDS rows, lazy rescale (the running max
+//    is refreshed only when a row outgrows it by 2^8).
+//  * Every stage's buffer resource is rebased on its first key and covers only
+//    the valid rows, so rows past Skv arrive as zeros and offsets stay
+//    loop-invariant; exp2-based softmax with scale*log2(e) folded into one
+//    FMA; workgroup ids are remapped XCD-aware (xcd_remap).
 #include <atomic>
 #include <climits>
 #include <type_traits>
