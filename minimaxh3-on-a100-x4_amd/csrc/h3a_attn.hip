@@ -110,6 +110,11 @@ namespace h3a {
 #ifndef H3A_PP_A_VINST
 #define H3A_PP_A_VINST 0
 #endif
+// 1: group A issues its share of the fetch after its matrix cluster (while
+// the last MFMAs drain) instead of before it.
+#ifndef H3A_PP_A_LATE
+#define H3A_PP_A_LATE 0
+#endif
 // Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
 // during the softmax cluster (2), or never (0).
 #ifndef H3A_PP_PRIO
@@ -246,10 +251,14 @@ struct TileDma {
     return stage_desc(base + (int64_t)key0 * ss, ss, rows);
   }
   // Instruction i (0 <= i < kInst, a compile-time index) of this wave's
-  // share; `cur` is its cursor (first(), then next() once per instruction).
-  __device__ __forceinline__ void issue_one(u32x4 d, int i, uint32_t cur, uint16_t *tile) const {
+  // share; `cur` is its offset cursor (first(), then next() once per
+  // instruction) and m0 the LDS address of its 1 KiB: that of instruction
+  // 0, lds_address(tile) + 1024 * wave, plus 1024 * NW per instruction,
+  // advanced by opaque_sadd so that the compiler does not keep every
+  // instruction's address of both buffers live in SGPRs.
+  __device__ __forceinline__ void issue_one(u32x4 d, int i, uint32_t cur, uint32_t m0) const {
     if (kInstTotal % NW == 0 || wave + i * NW < kInstTotal)
-      buffer_load_lds_b128(d, kAffine ? cur : off[i], tile + (wave + i * NW) * 512);
+      buffer_load_lds_b128(d, kAffine ? cur : off[i], m0);
   }
   __device__ __forceinline__ void issue(const uint16_t *base, int64_t ss, int key0, int Skv,
                                         uint16_t *tile) const {
@@ -264,10 +273,14 @@ struct TileDma {
       uint32_t cur = first();
 #pragma unroll
       for (int i = 0; i < I0; ++i) cur = next(cur);
+      uint32_t m0 = lds_address(tile) + (uint32_t)(wave + I0 * NW) * 1024u;
 #pragma unroll
       for (int i = I0; i < I1; ++i) {
-        issue_one(d, i, cur, tile);
-        if (i + 1 < I1) cur = next(cur);
+        issue_one(d, i, cur, m0);
+        if (i + 1 < I1) {
+          cur = next(cur);
+          m0 = opaque_sadd<1024u * NW>(m0);
+        }
       }
     }
   }
@@ -932,6 +945,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     fetch_k(Kb, key_base(j + 2), kbuf[P]);
     fetch_v(Vb, key_base(j + 1), vbuf[P ^ 1]);
   };
+  constexpr bool kALate = kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
   // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
@@ -974,8 +988,12 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 
   if (lead) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
-      dma(par, j);
+      if constexpr (!kALate) dma(par, j);
       mfma(par);
+      if constexpr (kALate) {
+        __builtin_amdgcn_sched_barrier(0);
+        dma(par, j);
+      }
       mid_barrier();
       if (j + 1 < niter) soft(j);
       wait_vmem_all();

@@ -76,11 +76,26 @@ __device__ __forceinline__ u32x4 buffer_load_b128(__amdgpu_buffer_rsrc_t res, ui
 // bytes are read.
 // The compiler's own vmcnt waits stay correct, since extra loads issued
 // after one of its loads only make a wait for that load more conservative.
-// `desc` is the V# as four scalar words (stage_desc).
-__device__ __forceinline__ void buffer_load_lds_b128(u32x4 desc, uint32_t byte_off, void *lds_dst) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds_dst;
+// `desc` is the V# as four scalar words (stage_desc); `m0` is the LDS byte
+// address of the destination (lds_address).
+__device__ __forceinline__ void buffer_load_lds_b128(u32x4 desc, uint32_t byte_off, uint32_t m0) {
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(desc), "{m0}"(m0)
                : "memory");
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// x + IMM on the scalar unit, opaque to the compiler: a wave-uniform cursor
+// advanced in place cannot be folded into per-use constants that the
+// compiler would then keep live across a loop.
+template <uint32_t IMM>
+__device__ __forceinline__ uint32_t opaque_sadd(uint32_t x) {
+  uint32_t r;
+  asm volatile("s_add_u32 %0, %1, %2" : "=s"(r) : "s"(x), "i"(IMM) : "scc");
+  return r;
 }
 
 // stage_rsrc's V# as four words for inline asm: base address (48 bits, stride
