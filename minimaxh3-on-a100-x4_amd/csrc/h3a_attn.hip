@@ -268,8 +268,12 @@ struct TileDma {
   template <int I0, int I1>
   __device__ __forceinline__ void issue_range(const uint16_t *base, int64_t ss, int key0, int Skv,
                                               uint16_t *tile) const {
+    if constexpr (I1 > I0) issue_desc<I0, I1>(desc(base, ss, key0, Skv), tile);
+  }
+  // The same with the stage's descriptor given (StageCursor::desc).
+  template <int I0, int I1>
+  __device__ __forceinline__ void issue_desc(u32x4 d, uint16_t *tile) const {
     if constexpr (I1 > I0) {
-      const u32x4 d = desc(base, ss, key0, Skv);
       uint32_t cur = first();
 #pragma unroll
       for (int i = 0; i < I0; ++i) cur = next(cur);
@@ -292,6 +296,42 @@ struct TileDma {
     issue(base, ss, key0, Skv, tile);
   }
   __device__ __forceinline__ void finish(uint16_t *) const {}
+};
+
+// Wave-uniform position of a K or V stream in a contiguous range of key
+// stages: the byte address of the next stage's first row and the number of
+// valid rows from there on (it goes negative past the range's end, where the
+// descriptor covers nothing and the DMA writes zeros).  advance() moves on by
+// one stage with one opaque 64-bit scalar add; rebuilding the address as
+// base + key0 * stride every stage costs a 64-bit multiply chain on the
+// scalar unit in the middle of the issuing wave's DMA burst.
+template <int ROWS>
+struct StageCursor {
+  uint32_t lo, hi, step_lo, step_hi, ss2;
+  int rows_left;
+  __device__ __forceinline__ void init(const uint16_t *base, int64_t ss, int key0, int key_end) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base) + (uint64_t)((int64_t)key0 * ss * 2);
+    const uint64_t step = (uint64_t)((int64_t)ROWS * ss * 2);
+    lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+    hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));
+    step_lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)step);
+    step_hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(step >> 32));
+    ss2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(ss * 2));
+    rows_left = __builtin_amdgcn_readfirstlane(key_end - key0);
+  }
+  // The V# of the current stage, as stage_desc builds it: valid rows only.
+  __device__ __forceinline__ u32x4 desc() const {
+    const int rows = rows_left >= ROWS ? ROWS : (rows_left > 0 ? rows_left : 0);
+    const uint32_t bytes = rows > 0 ? (uint32_t)(rows - 1) * ss2 + 256u : 0u;
+    return u32x4{lo, hi & 0xffffu, bytes, (uint32_t)kBufferConfig};
+  }
+  __device__ __forceinline__ void advance() {
+    asm volatile("s_add_u32 %0, %0, %2\n\ts_addc_u32 %1, %1, %3"
+                 : "+s"(lo), "+s"(hi)
+                 : "s"(step_lo), "s"(step_hi)
+                 : "scc");
+    rows_left -= ROWS;
+  }
 };
 
 // Staging through VGPRs into PadLayout: 128-bit buffer loads when the stage
@@ -928,6 +968,48 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     }
   };
 
+  // Dense: cursors of the K stream at local stage 2 and the V stream at
+  // stage 1, where the loop's fetches start.  The range ends at key_end, so
+  // stages from niter on load nothing, as key_base(j >= niter) = Skv does.
+  StageCursor<BN> kcur, vcur;
+  if constexpr (!kSparse) {
+    const int key_end = a.Skv < (j0 + niter) * BN ? a.Skv : (j0 + niter) * BN;
+    kcur.init(Kb, a.kss, (j0 + 2) * BN, key_end);
+    vcur.init(Vb, a.vss, (j0 + 1) * BN, key_end);
+  }
+  auto fetch_k_cur = [&](uint16_t *tile) __attribute__((always_inline)) {
+    if constexpr (kSplitDma) {
+      if (lead) {
+        if constexpr (kKA > 0) {
+          kdma.template issue_desc<0, kKA>(kcur.desc(), tile);
+          kcur.advance();
+        }
+      } else if constexpr (kKI > kKA) {
+        kdma.template issue_desc<kKA, kKI>(kcur.desc(), tile);
+        kcur.advance();
+      }
+    } else {
+      kdma.template issue_desc<0, kKI>(kcur.desc(), tile);
+      kcur.advance();
+    }
+  };
+  auto fetch_v_cur = [&](uint16_t *tile) __attribute__((always_inline)) {
+    if constexpr (kSplitDma) {
+      if (lead) {
+        if constexpr (kVA > 0) {
+          vdma.template issue_desc<0, kVA>(vcur.desc(), tile);
+          vcur.advance();
+        }
+      } else if constexpr (kVI > kVA) {
+        vdma.template issue_desc<kVA, kVI>(vcur.desc(), tile);
+        vcur.advance();
+      }
+    } else {
+      vdma.template issue_desc<0, kVI>(vcur.desc(), tile);
+      vcur.advance();
+    }
+  };
+
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
   fetch_k(Kb, key_base(0), kbuf[0]);
   fetch_v(Vb, key_base(0), vbuf[0]);
@@ -942,8 +1024,13 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 
   auto dma = [&](auto par, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;  // j & 1
-    fetch_k(Kb, key_base(j + 2), kbuf[P]);
-    fetch_v(Vb, key_base(j + 1), vbuf[P ^ 1]);
+    if constexpr (kSparse) {
+      fetch_k(Kb, key_base(j + 2), kbuf[P]);
+      fetch_v(Vb, key_base(j + 1), vbuf[P ^ 1]);
+    } else {
+      fetch_k_cur(kbuf[P]);
+      fetch_v_cur(vbuf[P ^ 1]);
+    }
   };
   constexpr bool kALate = kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
