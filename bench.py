@@ -91,6 +91,9 @@ def _parse():
                          "prologue + attention on the fused QKV layout at S=8192, H=56; graph: "
                          "--layers layers of prologue + attention at S=2048, H=4, eager vs one "
                          "HIP-graph replay (launch overhead)")
+    ap.add_argument("--blk", type=int, default=128, choices=[64, 128],
+                    help="sparse: query and key tile size (128: the 128x128 workload; 64: the SLA "
+                         "block size default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-split-tail", action="store_true",
                     help="dense: run h3a_attn_fwd (never splits the last round of tiles) instead of "
@@ -186,10 +189,12 @@ def run_dense(args, torch, h3attn, dev, heads=H):
 
 
 def run_sparse(args, torch, h3attn, dev):
-    """Block-sparse (h3_sla path): 128x128 tiles, top floor(0.25*330)=82 key tiles per query
-    tile from mean-pooled scores plus the diagonal; FLOPs counted exactly from the map."""
+    """Block-sparse (h3_sla path): blk x blk tiles (128 by default: 330 per head at S=42120),
+    top floor(0.25*nk) key tiles per query tile from mean-pooled scores plus the diagonal
+    (82 of 330 at 128); FLOPs counted exactly from the map."""
     from h3attn import sla
-    L, blk = args.layers, 128
+    L, blk = args.layers, args.blk
+    nk = (S + blk - 1) // blk
     items = []
     map_ms = []
     for layer in range(L):
@@ -225,9 +230,10 @@ def run_sparse(args, torch, h3attn, dev):
     value = flops * L * args.steps / wall / 1e12
     achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
     res = _base(args, "block-sparse attn TFLOP/s (exact kept-tile FLOPs) at H=56,S=42120,D=128, "
-                      "128x128 tiles, top-25%+diagonal", value, "TFLOP/s", wall * 1e3 / args.steps,
+                      f"{blk}x{blk} tiles, top-25%+diagonal", value, "TFLOP/s", wall * 1e3 / args.steps,
                 {"workload": f"block-sparse attention, {L} layers per step", "B": B, "H": H, "S": S,
-                 "D": D, "blk_q": blk, "blk_k": blk, "keep": "82 of 330 key tiles + diagonal"})
+                 "D": D, "blk_q": blk, "blk_k": blk,
+                 "keep": f"{int(0.25 * nk)} of {nk} key tiles + diagonal"})
     res.update({
         "ms_per_layer": round(avg_kernel_ms, 3),
         "kept_fraction": round(flops / flops_per_layer(), 4),
@@ -235,7 +241,7 @@ def run_sparse(args, torch, h3attn, dev):
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "attn_fwd_kernel<4,PadLayout,regs,sparse>", "flop_per_launch": flops,
+                     "kernel": f"attn_fwd_kernel<{blk // 32},PadLayout,regs,sparse>", "flop_per_launch": flops,
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     })
     return res

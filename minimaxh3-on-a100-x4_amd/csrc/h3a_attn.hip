@@ -94,6 +94,10 @@ namespace h3a {
 #ifndef H3A_SPARSE_REGS
 #define H3A_SPARSE_REGS 1
 #endif
+// 64-row query blocks: 4-wave key-split workgroups (1) or 2-wave workgroups (0).
+#ifndef H3A_SPARSE64_KEYSPLIT
+#define H3A_SPARSE64_KEYSPLIT 1
+#endif
 // LDS operand reads issued ahead of the first MFMA of a ping-pong matrix
 // cluster (0: leave the order to the scheduler).
 #ifndef H3A_PP_READ_AHEAD
@@ -472,7 +476,8 @@ __device__ __forceinline__ float tile_sum(const f32x16 (&s)[NSUB]) {
   float a[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    a[r] = s[0][r] + s[1][r];
+    a[r] = s[0][r];
+    if constexpr (NSUB >= 2) a[r] += s[1][r];
     if constexpr (NSUB == 4) a[r] += s[2][r] + s[3][r];
   }
 #pragma unroll
@@ -495,11 +500,21 @@ __device__ __forceinline__ void mask_tail(f32x16 (&s)[NSUB], int key0, int Skv, 
 }
 
 // kRegs: stage K/V through VGPRs into PadLayout (TileRegs) instead of LDS DMA.
-template <int NW, class L, bool kRegs, bool kSparse>
+// kKeySplit: a 4-wave workgroup on one 64-row query block.  Wave w takes the
+// 32 query rows of slice w & 1 against key half w >> 1 (keys 32*(w>>1) ..
+// +31) of every 64-key stage, with its own running max, row sum and O; at
+// the end the key-half-1 wave hands (O, m, l) to its partner through LDS and
+// the partner merges them, O = 2^(m1-M) O1 + 2^(m2-M) O2 over the same for
+// l, as the split-tail combine does.  Compared with a 2-wave workgroup on
+// the same block, the K/V stage in LDS feeds twice the waves: 8 per CU
+// instead of 4 (LDS holds two workgroups' double-buffered stages either way).
+template <int NW, class L, bool kRegs, bool kSparse, bool kKeySplit = false>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_kernel(AttnArgs a) {
   static_assert(!kRegs || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
-  constexpr int BM = NW * 32;
+  static_assert(!kKeySplit || NW == 4, "key-split workgroups are 2 query slices x 2 key halves");
+  constexpr int BM = kKeySplit ? 64 : NW * 32;
+  constexpr int NS = kKeySplit ? 1 : 2;  // 32-key score sub-tiles per wave and stage
   __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][StageBytes<L>::kK / 2];
   __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][StageBytes<L>::kV / 2];
 
@@ -542,12 +557,14 @@ attn_fwd_kernel(AttnArgs a) {
     }
   };
 
-  const int qrow = qt * BM + wave * 32 + l32;
+  const int rq = kKeySplit ? (wave & 1) : wave;  // 32-row query slice
+  const int kh = kKeySplit ? (wave >> 1) : 0;    // key half of each stage
+  const int qrow = qt * BM + rq * 32 + l32;
   if (niter == 0) {
     // No key block to attend to (block-sparse row with an empty LUT): O = 0.
     // Leaving before any load also keeps every path into the stage loop free
     // of outstanding loads, so the loop needs no waits on the Q fragments.
-    if (qrow < a.Sq) {
+    if (qrow < a.Sq && kh == 0) {
       uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
 #pragma unroll
       for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
@@ -569,8 +586,10 @@ attn_fwd_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
-  const int k_rd = L::k_base(l32, g);
-  const int v_rd = L::v_base(lane);
+  // Key half kh starts 32 rows into the stage: an offset that neither
+  // layout's per-step offsets (XOR or add below 256 bytes) interact with.
+  const int k_rd = L::k_base(l32, g) + kh * 32 * L::kKRow;
+  const int v_rd = L::v_base(lane) + kh * 32 * L::kVRow;
 
   // Software pipeline: K runs one stage ahead of V.  Entering stage j, LDS
   // holds V(j) in vbuf[j&1] and K(j+1) in kbuf[(j+1)&1], and the registers
@@ -593,7 +612,7 @@ attn_fwd_kernel(AttnArgs a) {
   auto land = [&]() __attribute__((always_inline)) {  // this wave's stage fetches are in LDS
     if constexpr (KStager::kAsync) wait_vmem_all();
   };
-  f32x16 s[2];
+  f32x16 s[NS];
   kst.start(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
   vst.start(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
   kst.finish(kbuf[0]);
@@ -601,7 +620,7 @@ attn_fwd_kernel(AttnArgs a) {
   land();
   __syncthreads();
   kst.start(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
-  score_tile<L, 2>(kbuf[0], qf, k_rd, s);
+  score_tile<L, NS>(kbuf[0], qf, k_rd, s);
   kst.finish(kbuf[1]);
   land();
   __syncthreads();
@@ -614,8 +633,8 @@ attn_fwd_kernel(AttnArgs a) {
     // The two rare branches (tail mask, rescale) come first, so everything
     // after them is one basic block the scheduler can interleave freely.
     const int key0 = key_base(j);
-    if (key0 + kBN > a.Skv) mask_tail<2>(s, key0, a.Skv, g);
-    const float mx = tile_max<2>(s, a.sl2);
+    if (key0 + kBN > a.Skv) mask_tail<NS>(s, key0 + 32 * kh, a.Skv, g);
+    const float mx = tile_max<NS>(s, a.sl2);
 #if H3A_LAZY_RESCALE
     // The reference max only has to bound the exponents: keep the stale max
     // while this stage's row max exceeds it by at most kRescaleSlack (p stays
@@ -635,31 +654,33 @@ attn_fwd_kernel(AttnArgs a) {
     const float muse = (m == kNegInf) ? 0.f : m;
 
     // S(j+1) on the MFMA pipe, softmax(j) on the VALU: no dependence between them.
-    f32x16 n[2];
-    score_tile<L, 2>(kbuf[P ^ 1], qf, k_rd, n);
+    f32x16 n[NS];
+    score_tile<L, NS>(kbuf[P ^ 1], qf, k_rd, n);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       s[0][r] = fast_exp2(fmaf(s[0][r], a.sl2, -muse));
-      s[1][r] = fast_exp2(fmaf(s[1][r], a.sl2, -muse));
+      if constexpr (NS == 2) s[1][r] = fast_exp2(fmaf(s[1][r], a.sl2, -muse));
     }
-    u32x4 pf[4];
-    pack_p<2>(s, pf);
+    u32x4 pf[2 * NS];
+    pack_p<NS>(s, pf);
 #if H3A_ROWSUM_BF16
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < 2 * NS; ++ks)
 #pragma unroll
       for (int c = 0; c < 4; ++c) lsum = dot2_bf16_ones(pf[ks][c], lsum);
 #else
-    lsum += tile_sum<2>(s);
+    lsum += tile_sum<NS>(s);
 #endif
-    pv_tile<L, 4>(vbuf[P], pf, v_rd, o);
+    pv_tile<L, 2 * NS>(vbuf[P], pf, v_rd, o);
+    // Explicit copies: written as an unrolled loop, they changed the 2-sub-tile
+    // build's register allocation (237 -> 245 VGPRs) and cost it ~1 %.
     s[0] = n[0];
-    s[1] = n[1];
+    if constexpr (NS == 2) s[1] = n[1];
 #if H3A_SCHED_HINTS
     // Interleave the block: each MFMA followed by LDS reads and VALU work
     // that can issue in its 32-cycle shadow.
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 16 * NS; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
@@ -677,6 +698,35 @@ attn_fwd_kernel(AttnArgs a) {
     if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
   }
 
+  if constexpr (kKeySplit) {
+    // The loop ended on a barrier after every read of the K/V buffers, so
+    // they hold the exchange: O of the key-half-1 wave of each query slice
+    // in kbuf (lane-major: 64 consecutive floats per register), its m and
+    // l in vbuf.
+    static_assert(sizeof(kbuf) >= 2 * 64 * 64 * sizeof(float), "O exchange fits kbuf");
+    static_assert(sizeof(vbuf) >= 2 * 2 * 64 * sizeof(float), "m/l exchange fits vbuf");
+    float *xo = reinterpret_cast<float *>(&kbuf[0][0]) + rq * 64 * 64;
+    float *xm = reinterpret_cast<float *>(&vbuf[0][0]) + rq * 2 * 64;
+    if (kh == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(16 * dt + r) * 64 + lane] = o[dt][r];
+      xm[lane] = m;
+      xm[64 + lane] = lsum;
+    }
+    __syncthreads();
+    if (kh == 1) return;  // no barrier follows
+    const float m2 = xm[lane], l2 = xm[64 + lane];
+    const float mn = fmaxf(m, m2);
+    const float a1 = m == kNegInf ? 0.f : fast_exp2(m - mn);
+    const float a2 = m2 == kNegInf ? 0.f : fast_exp2(m2 - mn);
+    lsum = lsum * a1 + l2 * a2;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a1 + xo[(16 * dt + r) * 64 + lane] * a2;
+  }
   const float ltot = half_swap_sum(lsum);
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
   if (qrow < a.Sq) {
@@ -1337,6 +1387,9 @@ int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   }
   if (blk_q == 128) {
     hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(256), 0, s, a);
+  } else if (H3A_SPARSE64_KEYSPLIT) {
+    hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true, true>), dim3(a.total), dim3(256), 0,
+                       s, a);
   } else {
     hipLaunchKernelGGL((attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(128), 0, s, a);
   }
@@ -1394,7 +1447,12 @@ int attn_kernel_attrs(int which, double out[6]) {
     case H3A_KERNEL_ATTN_SPARSE_128:
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), 256, out);
     case H3A_KERNEL_ATTN_SPARSE_64:
+#if H3A_SPARSE64_KEYSPLIT
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true, true>),
+                        256, out);
+#else
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), 128, out);
+#endif
     default:
       return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
   }

@@ -72,6 +72,47 @@ def test_all_blocks_kept_equals_dense(gpu, blk_k):
     assert torch.equal(o_s, o_d)
 
 
+@pytest.mark.parametrize("blk_k", [64, 128])
+@pytest.mark.parametrize("S", [1, 20, 33, 64, 97, 300])
+def test_sparse64_key_halves_vs_oracle(gpu, S, blk_k):
+    """64-row query blocks run as 4-wave workgroups whose two key halves (keys 0-31
+    and 32-63 of every 64-key stage) keep separate softmax state and are merged at
+    the end.  Key counts that leave the second half empty (S <= 32), partly filled
+    (33, 97) or exact (64), and a full block map at both key-block sizes, against
+    the masked oracle."""
+    rng = np.random.default_rng(900 + S + blk_k)
+    q, k, v = (randn_bf16(rng, (1, 2, S, 128)) for _ in range(3))
+    nq, nk = -(-S // 64), -(-S // blk_k)
+    bmap = np.ones((1, 2, nq, nk), np.uint8)
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, 64, blk_k)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=64, blk_k=blk_k)
+    assert_close_absmax(got, ref, what=f"sparse64 S={S} blk_k={blk_k}")
+
+
+def test_sparse64_key_half_maxima_differ(gpu):
+    """Key 104 (key half 1 of the second stage) scores 22*22 = 484 above the rest
+    (~62 log2 units after scaling; the other scores spread ~1.4 log2 units), so the
+    merge scales key half 0's O and l by ~2^-62 against half 1's: the result is the
+    masked oracle's, key 104's value row."""
+    rng = np.random.default_rng(77)
+    S = 256
+    q, k, v = (randn_bf16(rng, (1, 1, S, 128)) for _ in range(3))
+    qf = oracle.bf16_to_f32(q).reshape(q.shape).copy()
+    kf = oracle.bf16_to_f32(k).reshape(k.shape).copy()
+    qf[..., 0] = 22.0
+    kf[..., 0] = 0.0
+    kf[0, 0, 64 + 40, 0] = 22.0
+    q, k = oracle.f32_to_bf16(qf).reshape(q.shape), oracle.f32_to_bf16(kf).reshape(k.shape)
+    bmap = np.ones((1, 1, S // 64, S // 64), np.uint8)
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, 64, 64)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=64, blk_k=64)
+    assert_close_absmax(got, ref, what="sparse64 dominant key in key half 1")
+
+
 @pytest.mark.parametrize("blk,slope", [(64, 0.4), (128, 0.4), (128, 0.0383)])
 def test_sparse_running_max_rises(gpu, blk, slope):
     """Even rows see scores rising along the keys (~210 or ~20 log2 units per 64 keys),
