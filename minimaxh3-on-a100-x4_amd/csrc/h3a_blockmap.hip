@@ -15,6 +15,8 @@
 //                         consumes), the count, and optionally the 0/1 map.
 // Centring k by its sequence mean (SLA's K smoothing) shifts every score of a
 // row by the same amount, so it never changes the selection and is not needed.
+#include <type_traits>
+
 #include "h3a_device.h"
 #include "h3a_internal.h"
 
@@ -133,68 +135,78 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   };
   const int nchunks = (nk + 63) / 64;
-  // Rows of up to kSelRegChunks*64 key blocks keep their keys in registers
-  // for the counting rounds; longer rows re-read them from LDS each round.
-  constexpr int kSelRegChunks = 8;
-  const bool in_regs = nchunks <= kSelRegChunks;
-  for (int r = wave; r < nrows; r += kSelThreads / 64) {
-    const float *row_sc = sc + r * nk;
-    const int64_t row = bh * nq + i0 + r;
-    const int diag = (int)(((int64_t)(i0 + r) * blk_q) / blk_k);
-    int32_t *out = lut + row * max_k;
-    uint32_t kr[kSelRegChunks];  // valid keys; 0 (never counted: t >= 1 below) past nk
+  // NC > 0: the row's keys are held in NC registers per lane for the counting
+  // rounds (rows of up to NC*64 key blocks); NC = 0: longer rows re-read
+  // them from LDS each round.
+  auto select_rows = [&](auto nc_const) __attribute__((always_inline)) {
+    constexpr int NC = decltype(nc_const)::value;
+    constexpr int kSelRegChunks = NC > 0 ? NC : 1;
+    constexpr bool in_regs = NC > 0;
+    for (int r = wave; r < nrows; r += kSelThreads / 64) {
+      const float *row_sc = sc + r * nk;
+      const int64_t row = bh * nq + i0 + r;
+      const int diag = (int)(((int64_t)(i0 + r) * blk_q) / blk_k);
+      int32_t *out = lut + row * max_k;
+      uint32_t kr[kSelRegChunks];  // valid keys; 0 (never counted: t >= 1 below) past nk
 #pragma unroll
-    for (int c = 0; c < kSelRegChunks; ++c) {
-      const int j = c * 64 + lane;
-      kr[c] = (in_regs && j < nk) ? key_of(row_sc[j < nk ? j : 0]) : 0u;
-    }
-    // Number of the row's keys >= t.  Every t asked for is >= 1, every score
-    // that is not a NaN has a key > 0, and the padding key 0 is never counted.
-    auto count_ge = [&](uint32_t t) __attribute__((always_inline)) -> int {
-      int n = 0;
-      if (in_regs) {
+      for (int c = 0; c < kSelRegChunks; ++c) {
+        const int j = c * 64 + lane;
+        kr[c] = (in_regs && j < nk) ? key_of(row_sc[j < nk ? j : 0]) : 0u;
+      }
+      // Number of the row's keys >= t.  Every t asked for is >= 1, every score
+      // that is not a NaN has a key > 0, and the padding key 0 is never counted.
+      auto count_ge = [&](uint32_t t) __attribute__((always_inline)) -> int {
+        int n = 0;
+        if constexpr (in_regs) {
 #pragma unroll
-        for (int c = 0; c < kSelRegChunks; ++c) n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(kr[c] >= t));
-      } else {
-        for (int c = 0; c < nchunks; ++c) {
-          const int j = c * 64 + lane;
-          n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < nk && key_of(row_sc[j < nk ? j : 0]) >= t));
+          for (int c = 0; c < kSelRegChunks; ++c) n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(kr[c] >= t));
+        } else {
+          for (int c = 0; c < nchunks; ++c) {
+            const int j = c * 64 + lane;
+            n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < nk && key_of(row_sc[j < nk ? j : 0]) >= t));
+          }
         }
+        return n;
+      };
+      // T = the keep-th largest key: the largest t with count_ge(t) >= keep,
+      // built from the top bit down.  Then exactly the keys > T and the first
+      // (keep - #keys > T) keys == T in index order have rank < keep under
+      // (score desc, index asc).
+      uint32_t T = 0;
+      int need = 0;  // keys == T to keep
+      if (keep > 0) {
+        for (int bit = 31; bit >= 0; --bit) {
+          const uint32_t cand = T | (1u << bit);
+          if (count_ge(cand) >= keep) T = cand;
+        }
+        need = keep - (T == 0xffffffffu ? 0 : count_ge(T + 1));
       }
-      return n;
-    };
-    // T = the keep-th largest key: the largest t with count_ge(t) >= keep,
-    // built from the top bit down.  Then exactly the keys > T and the first
-    // (keep - #keys > T) keys == T in index order have rank < keep under
-    // (score desc, index asc).
-    uint32_t T = 0;
-    int need = 0;  // keys == T to keep
-    if (keep > 0) {
-      for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = T | (1u << bit);
-        if (count_ge(cand) >= keep) T = cand;
+      int base = 0, eq_before = 0;
+      for (int c = 0; c < nchunks; ++c) {
+        const int j = c * 64 + lane;
+        const uint32_t kj = j < nk ? key_of(row_sc[j < nk ? j : 0]) : 0u;
+        const bool eq = keep > 0 && j < nk && kj == T;
+        const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
+        const bool by_rank = keep > 0 && j < nk && (kj > T || (eq && eq_before + __builtin_popcountll(eqm & below) < need));
+        const bool kept = by_rank || (force_diag && j == diag && j < nk);
+        eq_before += __builtin_popcountll(eqm);
+        const uint64_t m = __builtin_amdgcn_ballot_w64(kept);
+        const int pos = base + __builtin_popcountll(m & below);
+        if (kept && pos < max_k) out[pos] = j;
+        if (map && j < nk) map[row * nk + j] = (uint8_t)kept;
+        base += __builtin_popcountll(m);
       }
-      need = keep - (T == 0xffffffffu ? 0 : count_ge(T + 1));
+      const int kept_n = base < max_k ? base : max_k;
+      for (int t = kept_n + lane; t < max_k; t += 64) out[t] = -1;
+      if (lane == 0) counts[row] = kept_n;
     }
-    int base = 0, eq_before = 0;
-    for (int c = 0; c < nchunks; ++c) {
-      const int j = c * 64 + lane;
-      const uint32_t kj = j < nk ? key_of(row_sc[j < nk ? j : 0]) : 0u;
-      const bool eq = keep > 0 && j < nk && kj == T;
-      const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
-      const bool by_rank = keep > 0 && j < nk && (kj > T || (eq && eq_before + __builtin_popcountll(eqm & below) < need));
-      const bool kept = by_rank || (force_diag && j == diag && j < nk);
-      eq_before += __builtin_popcountll(eqm);
-      const uint64_t m = __builtin_amdgcn_ballot_w64(kept);
-      const int pos = base + __builtin_popcountll(m & below);
-      if (kept && pos < max_k) out[pos] = j;
-      if (map && j < nk) map[row * nk + j] = (uint8_t)kept;
-      base += __builtin_popcountll(m);
-    }
-    const int kept_n = base < max_k ? base : max_k;
-    for (int t = kept_n + lane; t < max_k; t += 64) out[t] = -1;
-    if (lane == 0) counts[row] = kept_n;
-  }
+  };
+  if (nchunks <= 6)
+    select_rows(std::integral_constant<int, 6>{});
+  else if (nchunks <= 12)
+    select_rows(std::integral_constant<int, 12>{});
+  else
+    select_rows(std::integral_constant<int, 0>{});
 }
 
 int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int S, int blk,

@@ -262,11 +262,14 @@ def _select_ref(pq, pk, keep, blk_q, blk_k, diag, max_k):
 
 @pytest.mark.parametrize("nq,nk,keep,diag,max_k", [
     (9, 700, 37, True, 38), (17, 65, 1, False, 1), (1, 64, 64, False, 64), (9, 1, 1, True, 1),
-    (17, 700, 100, True, 50), (16, 200, 20, False, 20)])
+    (17, 700, 100, True, 50), (16, 200, 20, False, 20), (5, 384, 96, True, 97),
+    (3, 769, 10, False, 10), (5, 1000, 150, True, 151)])
 def test_block_select_exact_ties(gpu, nq, nk, keep, diag, max_k):
     """Integer pooled vectors make every score an exact fp32 integer, with many ties:
-    the kept set, its order and the truncation to max_k_blocks must match exactly
-    (row groups of up to 8 query blocks per workgroup, several 512-key ranking passes)."""
+    the kept set, its order and the truncation to max_k_blocks must match exactly.
+    Covers row groups of up to 8 query blocks per workgroup and all three counting
+    paths: keys held in 6 registers (nk <= 384), in 12 (nk <= 768), and re-read from
+    LDS (769, 1000)."""
     rng = np.random.default_rng(50 + nq + nk)
     pq = rng.integers(-2, 3, (1, 2, nq, 128)).astype(np.float32)
     pk = rng.integers(-2, 3, (1, 2, nk, 128)).astype(np.float32)
