@@ -544,18 +544,27 @@ attn_fwd_kernel(AttnArgs a) {
   } else {
     niter = (a.Skv + kBN - 1) / kBN;
   }
-  // First key of stage j.  Prefetches past the last stage and LUT entries
+  // First key of stage j, from its LUT entry kb (block-sparse; a key block
+  // of a.sub = 1 or 2 stages).  Prefetches past the last stage and LUT entries
   // outside the key range map to Skv: such a stage loads nothing (zeros).
-  auto key_base = [&](int j) __attribute__((always_inline)) -> int {
+  const int sub_sh = a.sub == 2 ? 1 : 0;
+  auto lut_entry = [&](int j) __attribute__((always_inline)) -> int {
+    if constexpr (kSparse) {
+      return j < niter ? lut_row[j >> sub_sh] : -1;
+    } else {
+      return 0;
+    }
+  };
+  auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
     if (j >= niter) return a.Skv;
     if constexpr (kSparse) {
-      const int kb = lut_row[j / a.sub];
-      const int key0 = kb * a.blk_k + (j % a.sub) * kBN;
+      const int key0 = kb * a.blk_k + (j & (a.sub - 1)) * kBN;
       return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
     } else {
       return j * kBN;
     }
   };
+  auto key_base = [&](int j) __attribute__((always_inline)) -> int { return key_of_entry(j, lut_entry(j)); };
 
   const int rq = kKeySplit ? (wave & 1) : wave;  // 32-row query slice
   const int kh = kKeySplit ? (wave >> 1) : 0;    // key half of each stage
@@ -612,14 +621,20 @@ attn_fwd_kernel(AttnArgs a) {
   auto land = [&]() __attribute__((always_inline)) {  // this wave's stage fetches are in LDS
     if constexpr (KStager::kAsync) wait_vmem_all();
   };
+  // Entering stage j: the first keys of stages j and j+1, and the LUT entry
+  // of stage j+2.  Stage j loads the entry of stage j+3 and uses it only in
+  // the next stage: with block-sparse LUTs that is a scalar load, whose wait
+  // is then the closing barrier's (which waits for the LDS writes anyway)
+  // rather than a wait for all LDS traffic at the top of the stage.
+  int kw0 = key_base(0), kw1 = key_base(1), e2 = lut_entry(2);
   f32x16 s[NS];
-  kst.start(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
-  vst.start(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+  kst.start(Kb, a.kss, kw0, a.Skv, kbuf[0]);
+  vst.start(Vb, a.vss, kw0, a.Skv, vbuf[0]);
   kst.finish(kbuf[0]);
   vst.finish(vbuf[0]);
   land();
   __syncthreads();
-  kst.start(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+  kst.start(Kb, a.kss, kw1, a.Skv, kbuf[1]);
   score_tile<L, NS>(kbuf[0], qf, k_rd, s);
   kst.finish(kbuf[1]);
   land();
@@ -627,12 +642,14 @@ attn_fwd_kernel(AttnArgs a) {
 
   auto stage = [&](auto phase, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(phase)::value;  // j & 1
-    kst.start(Kb, a.kss, key_base(j + 2), a.Skv, kbuf[P]);
-    vst.start(Vb, a.vss, key_base(j + 1), a.Skv, vbuf[P ^ 1]);
+    const int e3 = lut_entry(j + 3);
+    const int kw2 = key_of_entry(j + 2, e2);
+    kst.start(Kb, a.kss, kw2, a.Skv, kbuf[P]);
+    vst.start(Vb, a.vss, kw1, a.Skv, vbuf[P ^ 1]);
 
     // The two rare branches (tail mask, rescale) come first, so everything
     // after them is one basic block the scheduler can interleave freely.
-    const int key0 = key_base(j);
+    const int key0 = kw0;
     if (key0 + kBN > a.Skv) mask_tail<NS>(s, key0 + 32 * kh, a.Skv, g);
     const float mx = tile_max<NS>(s, a.sl2);
 #if H3A_LAZY_RESCALE
@@ -691,6 +708,9 @@ attn_fwd_kernel(AttnArgs a) {
     vst.finish(vbuf[P ^ 1]);
     land();
     __syncthreads();
+    kw0 = kw1;
+    kw1 = kw2;
+    e2 = e3;
   };
 
   for (int j = 0; j < niter; j += 2) {
