@@ -252,7 +252,7 @@ struct TileDma {
   // Buffer descriptor of the stage that starts at key0 (valid rows only).
   __device__ __forceinline__ u32x4 desc(const uint16_t *base, int64_t ss, int key0, int Skv) const {
     const int rows = Skv - key0 >= ROWS ? ROWS : (Skv > key0 ? Skv - key0 : 0);
-    return stage_desc(base + (int64_t)key0 * ss, ss, rows);
+    return stage_desc(stage_ptr(base, key0, ss), ss, rows);
   }
   // Instruction i (0 <= i < kInst, a compile-time index) of this wave's
   // share; `cur` is its offset cursor (first(), then next() once per
@@ -363,7 +363,7 @@ struct TileRegs {
   }
   __device__ __forceinline__ void start(const uint16_t *base, int64_t ss, int key0, int Skv, uint16_t *) {
     const int rows = Skv - key0 >= kBN ? kBN : (Skv > key0 ? Skv - key0 : 0);
-    const __amdgpu_buffer_rsrc_t res = stage_rsrc(base + (int64_t)key0 * ss, ss, rows);
+    const __amdgpu_buffer_rsrc_t res = stage_rsrc(stage_ptr(base, key0, ss), ss, rows);
 #pragma unroll
     for (int i = 0; i < kInst; ++i) r[i] = buffer_load_b128(res, goff + i * gstep);
   }
@@ -547,21 +547,23 @@ attn_fwd_kernel(AttnArgs a) {
   // First key of stage j, from its LUT entry kb (block-sparse; a key block
   // of a.sub = 1 or 2 stages).  Prefetches past the last stage and LUT entries
   // outside the key range map to Skv: such a stage loads nothing (zeros).
+  // Both are branch-free, so that the scalar work can be scheduled among
+  // the stage's MFMA and VALU instructions: the entry is loaded at a clamped
+  // index (niter >= 1 here) and discarded past the row's last stage.
   const int sub_sh = a.sub == 2 ? 1 : 0;
   auto lut_entry = [&](int j) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      return j < niter ? lut_row[j >> sub_sh] : -1;
+      return lut_row[(j < niter ? j : niter - 1) >> sub_sh];
     } else {
       return 0;
     }
   };
   auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
-    if (j >= niter) return a.Skv;
     if constexpr (kSparse) {
       const int key0 = kb * a.blk_k + (j & (a.sub - 1)) * kBN;
-      return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
+      return (j < niter && kb >= 0 && key0 < a.Skv) ? key0 : a.Skv;
     } else {
-      return j * kBN;
+      return j < niter ? j * kBN : a.Skv;
     }
   };
   auto key_base = [&](int j) __attribute__((always_inline)) -> int { return key_of_entry(j, lut_entry(j)); };

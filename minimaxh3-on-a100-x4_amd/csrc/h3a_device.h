@@ -53,9 +53,21 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // holding 128 bf16: num_records is the exact byte extent, so any access past
 // the last valid row returns zeros.  Word 3 is the gfx9-family default config.
 constexpr int kBufferConfig = 0x00020000;
+// Strides are below 2^24 elements and rows at most 128 (checked by the
+// entry points), so the byte extent is computed in 32 bits.
+__device__ __forceinline__ uint32_t stage_bytes(int64_t stride, int rows) {
+  return rows > 0 ? ((uint32_t)(rows - 1) * (uint32_t)stride + 128u) * 2u : 0u;
+}
+
+// base + key0 * stride elements, for 0 <= key0 and 0 <= stride < 2^24: one
+// unsigned 32x32 -> 64-bit multiply instead of a signed 64-bit one.
+__device__ __forceinline__ const uint16_t *stage_ptr(const uint16_t *base, int key0, int64_t stride) {
+  return base + (uint64_t)(uint32_t)key0 * (uint32_t)stride;
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t stage_rsrc(const uint16_t *base, int64_t stride,
                                                              int rows) {
-  const uint32_t bytes = rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + 128) * 2) : 0u;
+  const uint32_t bytes = stage_bytes(stride, rows);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), (short)0, (int)bytes,
                                            kBufferConfig);
 }
@@ -103,7 +115,7 @@ __device__ __forceinline__ uint32_t opaque_sadd(uint32_t x) {
 // operand is provably wave-uniform and lives in SGPRs whatever the register
 // pressure around the call.
 __device__ __forceinline__ u32x4 stage_desc(const uint16_t *base, int64_t stride, int rows) {
-  const uint32_t bytes = rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + 128) * 2) : 0u;
+  const uint32_t bytes = stage_bytes(stride, rows);
   const uint64_t addr = reinterpret_cast<uint64_t>(base);
   return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr),
                (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(addr >> 32) & 0xffffu)),
