@@ -85,10 +85,15 @@ namespace h3a {
 #ifndef H3A_PP_STALE_MAX
 #define H3A_PP_STALE_MAX 1
 #endif
-// Block-sparse attention with 128-row query blocks: ping-pong kernel over
-// pairs of query blocks (1), or the single-group attn_fwd_kernel (0).
+// Block-sparse attention with 128-row query blocks: key-split ping-pong
+// kernel (1), or the single-group attn_fwd_kernel (0).
 #ifndef H3A_SPARSE_PINGPONG
 #define H3A_SPARSE_PINGPONG 0
+#endif
+// Key-split ping-pong: group A issues its half of the fetch after its matrix
+// cluster (1) or before it (0).
+#ifndef H3A_SPARSE_PP_A_LATE
+#define H3A_SPARSE_PP_A_LATE 1
 #endif
 // Block-sparse attn_fwd_kernel: K/V staged through VGPRs (1) or by LDS DMA (0).
 #ifndef H3A_SPARSE_REGS
@@ -898,30 +903,31 @@ __device__ __forceinline__ void mid_barrier() {
 // from slot 2j+3 on, after every wave waited for its share of the DMA at the
 // end of slot 2j+2.
 //
-// kSparse: block-sparse attention over pairs of 128-row query blocks.  Group A
-// takes query block 2p and group B block 2p+1 of pair p, each with its own LUT
-// row, its own double-buffered K/V stages in LDS and its own DMA (its 4 waves
-// split each tile); the barrier slots are as above.  Both groups step through
-// the longer of their two stage lists; the shorter one's extra stages load
-// nothing and are fully masked.
+// kSparse: block-sparse attention on one 128-row query block, key-split.  A
+// stage is 128 keys in LDS: two 64-key halves of the block's LUT list (half t
+// is 64-key stage t of the list: key block t / sub, part t % sub), half
+// 2j + grp of stage j for group grp.  Every wave takes the 32 query rows of
+// slice wave & 3 against its group's half only, with its own running max,
+// row sum and O; each group fetches its own half (its 4 waves split it).  The
+// barrier slots are as above.  At the end group B hands (O, m, l) to the
+// group-A wave of the same slice through LDS, which merges them as the
+// split-tail combine does and stores O.
 template <class L, int NSUB, bool kSparse = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   constexpr int NW = 8;
   constexpr int BN = 32 * NSUB;  // keys per stage
-  constexpr int kKE = StageBytes<L, BN>::kK / 2, kVE = StageBytes<L, BN>::kV / 2;  // elements
-  constexpr int NG = kSparse ? 2 : 1;  // K/V streams
-  static_assert(!kSparse || BN == kBN, "block-sparse stages are 64 keys");
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[NG][2][kKE];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[NG][2][kVE];
+  constexpr int RB = kSparse ? 2 * BN : BN;  // key rows per stage buffer (sparse: two halves)
+  constexpr int kKE = StageBytes<L, RB>::kK / 2, kVE = StageBytes<L, RB>::kV / 2;  // elements
+  static_assert(!kSparse || BN == kBN, "block-sparse halves are 64 keys");
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kKE];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kVE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const bool lead = wave_u < NW / 2;  // group A
-  const int grp = kSparse ? (lead ? 0 : 1) : 0;
-  uint16_t(*kbuf)[kKE] = kbuf_all[grp];
-  uint16_t(*vbuf)[kVE] = vbuf_all[grp];
+  const int grp = kSparse ? (lead ? 0 : 1) : 0;  // sparse: key half
   const int nstages = (a.Skv + BN - 1) / BN;
   // Work item of this workgroup.  With a split tail, the first
   // a.split_first items are whole query tiles; each later tile is cut into
@@ -948,45 +954,42 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     j0 = (int)((int64_t)nstages * p / a.split_pieces);
     niter = (int)((int64_t)nstages * (p + 1) / a.split_pieces) - j0;  // >= 1
   }
-  // Sparse: a.nqt counts 128-row query blocks and w runs over (b, h, pair).
-  const int nw_bh = kSparse ? (a.nqt + 1) / 2 : a.nqt;
-  const int qt = w % nw_bh, bh = w / nw_bh;
+  // Sparse: a.nqt counts 128-row query blocks.
+  const int qt = w % a.nqt, bh = w / a.nqt;
   const int h = bh % a.H, b = bh / a.H;
   const uint16_t *Qb = a.q + b * a.qsb + h * a.qsh;
   const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
   const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
   uint16_t *Ob = a.o + b * a.osb + h * a.osh;
-  const int qrow = kSparse ? (2 * qt + grp) * 128 + (wave_u & 3) * 32 + l32 : qt * 256 + wave * 32 + l32;
-  // This group's stage count and LUT row (sparse).
-  int ngrp = niter;
+  const int qrow = kSparse ? qt * 128 + (wave_u & 3) * 32 + l32 : qt * 256 + wave * 32 + l32;
+  // Sparse: the block's LUT row, its length in 64-key halves, and the stage
+  // count (two halves per stage).
+  int n64 = 0;
   const int32_t *lut_row = nullptr;
+  const int sub_sh = a.sub == 2 ? 1 : 0;
   if constexpr (kSparse) {
-    auto stages_of = [&](int qb) __attribute__((always_inline)) -> int {
-      if (qb >= a.nqt) return 0;
-      const int cnt = a.counts[(int64_t)bh * a.nqt + qb];
-      return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
-    };
-    const int qb = 2 * qt + grp;
-    ngrp = stages_of(qb);
-    const int nother = stages_of(2 * qt + 1 - grp);
-    niter = ngrp > nother ? ngrp : nother;
-    lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
+    const int cnt = a.counts[(int64_t)bh * a.nqt + qt];
+    n64 = (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
+    niter = (n64 + 1) / 2;
+    lut_row = a.lut + ((int64_t)bh * a.nqt + qt) * a.lut_stride;
   }
-  // First key of local stage j; past this group's last stage, and for LUT
-  // entries that name no key block, it is Skv, which loads nothing (zeros).
+  // First key of this group's part of local stage j (sparse: of half
+  // 2j + grp); past the list's end, and for LUT entries that name no key
+  // block, it is Skv, which loads nothing (zeros).
   auto key_base = [&](int j) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      if (j >= ngrp) return a.Skv;
-      const int kb = lut_row[j / a.sub];
-      const int key0 = kb * a.blk_k + (j % a.sub) * BN;
+      const int t = 2 * j + grp;
+      if (t >= n64) return a.Skv;
+      const int kb = lut_row[t >> sub_sh];
+      const int key0 = kb * a.blk_k + (t & (a.sub - 1)) * BN;
       return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
     } else {
       return j < niter ? (j0 + j) * BN : a.Skv;
     }
   };
   if (kSparse && niter == 0) {
-    // Neither query block of the pair keeps a key block: O = 0.
-    if (qrow < a.Sq) {
+    // The query block keeps no key block: O = 0.
+    if (qrow < a.Sq && lead) {
       uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
 #pragma unroll
       for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
@@ -1008,11 +1011,14 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
-  const int k_rd = L::k_base(l32, g);
-  const int v_rd = L::v_base(lane);
+  // Sparse: group grp reads and fetches rows 64*grp .. 64*grp+63 of each
+  // stage buffer (an offset neither layout's per-step offsets interact with).
+  const int k_rd = L::k_base(l32, g) + grp * BN * L::kKRow;
+  const int v_rd = L::v_base(lane) + grp * BN * L::kVRow;
+  const int kho = grp * BN * L::kKRow / 2, vho = grp * BN * L::kVRow / 2;  // elements
 
   // Each K/V stream is fetched by the waves that read it: all 8 (dense) or
-  // the 4 of the group (sparse).
+  // the 4 of the group (sparse: its half).
   // Dense with H3A_PP_A_KINST >= 0: waves w and w+4 share one column of
   // the 4-wave layout, split between them as the knobs say.
   constexpr bool kSplitDma = !kSparse && H3A_PP_A_KINST >= 0;
@@ -1083,9 +1089,9 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   };
 
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
-  fetch_k(Kb, key_base(0), kbuf[0]);
-  fetch_v(Vb, key_base(0), vbuf[0]);
-  fetch_k(Kb, key_base(1), kbuf[1]);
+  fetch_k(Kb, key_base(0), kbuf[0] + kho);
+  fetch_v(Vb, key_base(0), vbuf[0] + vho);
+  fetch_k(Kb, key_base(1), kbuf[1] + kho);
   wait_vmem_all();
   __syncthreads();
   f32x16 s[NSUB];
@@ -1097,14 +1103,15 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   auto dma = [&](auto par, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;  // j & 1
     if constexpr (kSparse) {
-      fetch_k(Kb, key_base(j + 2), kbuf[P]);
-      fetch_v(Vb, key_base(j + 1), vbuf[P ^ 1]);
+      fetch_k(Kb, key_base(j + 2), kbuf[P] + kho);
+      fetch_v(Vb, key_base(j + 1), vbuf[P ^ 1] + vho);
     } else {
       fetch_k_cur(kbuf[P]);
       fetch_v_cur(vbuf[P ^ 1]);
     }
   };
-  constexpr bool kALate = kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
+  constexpr bool kALate =
+      kSparse ? H3A_SPARSE_PP_A_LATE != 0 : kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
   // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
@@ -1182,6 +1189,35 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     }
   }
 
+  if constexpr (kSparse) {
+    // Both loops ended on the same barrier after their last LDS access, so
+    // the stage buffers hold the exchange: the group-B wave of each slice
+    // writes O (lane-major, 64 consecutive floats per register) into kbuf
+    // and m, l into vbuf; its group-A partner merges them.
+    static_assert(sizeof(kbuf) >= 4 * 64 * 64 * sizeof(float), "O exchange fits kbuf");
+    static_assert(sizeof(vbuf) >= 4 * 2 * 64 * sizeof(float), "m/l exchange fits vbuf");
+    float *xo = reinterpret_cast<float *>(&kbuf[0][0]) + (wave_u & 3) * 64 * 64;
+    float *xm = reinterpret_cast<float *>(&vbuf[0][0]) + (wave_u & 3) * 2 * 64;
+    if (!lead) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(16 * dt + r) * 64 + lane] = o[dt][r];
+      xm[lane] = m;
+      xm[64 + lane] = lsum;
+    }
+    __syncthreads();
+    if (!lead) return;  // no barrier follows
+    const float m2 = xm[lane], l2 = xm[64 + lane];
+    const float mn = fmaxf(m, m2);
+    const float a1 = m == kNegInf ? 0.f : fast_exp2(m - mn);
+    const float a2 = m2 == kNegInf ? 0.f : fast_exp2(m2 - mn);
+    lsum = lsum * a1 + l2 * a2;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a1 + xo[(16 * dt + r) * 64 + lane] * a2;
+  }
   const float ltot = half_swap_sum(lsum);
   if (piece >= 0) {
     // Partial result of one key range: unnormalised O, the reference max m
@@ -1400,11 +1436,7 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   if (H3A_SPARSE_PINGPONG && blk_q == 128) {
-    AttnArgs p = a;
-    const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
-    if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
-    p.total = (int)pairs;
-    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SwzLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
+    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SwzLayout, 2, true>), dim3(a.total), dim3(512), 0, s, a);
     return check_launch("attn_fwd_pingpong_kernel<sparse>");
   }
   if (blk_q == 128) {
