@@ -25,7 +25,7 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.
 # HBM bytes per launch of the dense kernel at this shape, from the rocprofv3
 # FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0) passes recorded in
 # profiles/attn_dense_h56_s42120_counters.txt (scales from a 2048 MiB copy).
-MEASURED_TRAFFIC_BYTES = 9.06e9
+MEASURED_TRAFFIC_BYTES = 9.58e9
 B, H, S, D, LAYERS = 1, 56, 42120, 128, 50
 
 
@@ -241,7 +241,7 @@ def run_sparse(args, torch, h3attn, dev):
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": f"attn_fwd_kernel<{blk // 32},PadLayout,regs,sparse>", "flop_per_launch": flops,
+                     "kernel": "attn_fwd_kernel<4,PadLayout,regs,sparse>" + (", key-split" if blk == 64 else ""), "flop_per_launch": flops,
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     })
     return res
