@@ -28,9 +28,11 @@
 //    overflows its bound.  A split tail cuts the last, partly filled round of
 //    query tiles into key ranges merged by split_combine_kernel.
 //  * Block-sparse (attn_fwd_kernel with kSparse): the LUT row of a query block
-//    lists the key stages; 4 waves per workgroup, two workgroups per CU, K/V
-//    staged through VGPRs into padded LDS rows, lazy rescale (the running max
-//    is refreshed only when a row outgrows it by 2^8).
+//    lists the key stages, read one stage ahead; 4 waves per workgroup, two
+//    workgroups per CU, K/V staged through VGPRs into padded LDS rows, lazy
+//    rescale (the running max is refreshed only when a row outgrows it by
+//    2^8).  64-row query blocks split each stage's keys between two pairs of
+//    waves and merge the halves at the end (kKeySplit).
 //  * Every stage's buffer resource is rebased on its first key and covers only
 //    the valid rows, so rows past Skv arrive as zeros and offsets stay
 //    loop-invariant; exp2-based softmax with scale*log2(e) folded into one
