@@ -56,6 +56,34 @@ def test_sparse_vs_masked_oracle(gpu, blk, S, H):
     assert_close_absmax(got, ref, what=f"sparse blk={blk}")
 
 
+@pytest.mark.parametrize("blk", [64, 128])
+def test_sparse_wide_kv_stride(gpu, blk):
+    """K and V as views with a sequence stride just below the 2^24-element limit, so
+    a (b,h) slice spans 6.7 GB and stage addresses pass 2^32 bytes from the slice
+    base: each stage's buffer resource is rebased on its first row with 64-bit
+    arithmetic.  Same result as the masked oracle on the gathered rows."""
+    rng = np.random.default_rng(4000 + blk)
+    S, ss = 200, (1 << 24) - 8
+    q, k, v = (randn_bf16(rng, (1, 1, S, 128)) for _ in range(3))
+    nk = -(-S // blk)
+    bmap = oracle.block_map(q, k, blk, blk, keep=max(1, nk // 2), force_diag=True)
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    n = (S - 1) * ss + 128
+
+    def wide(bits):
+        base = torch.empty(n, dtype=torch.bfloat16, device=gpu)
+        view = base.as_strided((1, 1, S, 128), (n, n, ss, 1))
+        view.copy_(to_dev_bf16(bits, gpu))
+        return view
+
+    kd, vd = wide(k), wide(v)
+    o = h3attn.attn_fwd_blocksparse(to_dev_bf16(q, gpu), kd, vd, lut, cnt, blk, blk)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
+    del kd, vd
+    assert_close_absmax(got, ref, what=f"sparse blk={blk} wide K/V stride")
+
+
 @pytest.mark.parametrize("blk_k", [64, 128])
 def test_all_blocks_kept_equals_dense(gpu, blk_k):
     """A full block map visits the key stages in the dense order: bit-identical output
