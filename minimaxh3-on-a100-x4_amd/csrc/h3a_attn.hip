@@ -27,12 +27,16 @@
 //    a stale reference max and takes a row max only when a stage's p sum
 //    overflows its bound.  A split tail cuts the last, partly filled round of
 //    query tiles into key ranges merged by split_combine_kernel.
-//  * Block-sparse (attn_fwd_kernel with kSparse): the LUT row of a query block
-//    lists the key stages, read one stage ahead; 4 waves per workgroup, two
-//    workgroups per CU, K/V staged through VGPRs into padded LDS rows, lazy
-//    rescale (the running max is refreshed only when a row outgrows it by
-//    2^8).  64-row query blocks split each stage's keys between two pairs of
-//    waves and merge the halves at the end (kKeySplit).
+//  * Block-sparse, 128-row query blocks (attn_fwd_pingpong_kernel with
+//    kSparse): the ping-pong over a pair of query blocks, one per group, each
+//    with its own LUT row and K/V stream staged through VGPRs into padded LDS
+//    rows; a group issues its loads right after its matrix cluster and
+//    writes LDS at the end of its softmax slot.  LUT entries are read ahead.
+//  * Block-sparse, 64-row query blocks (attn_fwd_kernel with kSparse and
+//    kKeySplit): 4 waves split each stage's keys between two pairs of waves
+//    and merge the halves at the end; two workgroups per CU, register-staged
+//    K/V, lazy rescale (the running max is refreshed only when a row outgrows
+//    it by 2^8).
 //  * Every stage's buffer resource is rebased on its first key and covers only
 //    the valid rows, so rows past Skv arrive as zeros and offsets stay
 //    loop-invariant; exp2-based softmax with scale*log2(e) folded into one
@@ -87,15 +91,16 @@ namespace h3a {
 #ifndef H3A_PP_STALE_MAX
 #define H3A_PP_STALE_MAX 1
 #endif
-// Block-sparse attention with 128-row query blocks: key-split ping-pong
-// kernel (1), or the single-group attn_fwd_kernel (0).
+// Block-sparse attention with 128-row query blocks: ping-pong kernel over
+// pairs of query blocks with register-staged K/V (1), or the single-group
+// attn_fwd_kernel (0).
 #ifndef H3A_SPARSE_PINGPONG
-#define H3A_SPARSE_PINGPONG 0
+#define H3A_SPARSE_PINGPONG 1
 #endif
-// Key-split ping-pong: group A issues its half of the fetch after its matrix
-// cluster (1) or before it (0).
-#ifndef H3A_SPARSE_PP_A_LATE
-#define H3A_SPARSE_PP_A_LATE 1
+// Sparse ping-pong: a group issues its K/V loads right after its matrix
+// cluster (1) instead of at the top of its softmax slot (0).
+#ifndef H3A_SPARSE_PP_EARLY
+#define H3A_SPARSE_PP_EARLY 1
 #endif
 // Block-sparse attn_fwd_kernel: K/V staged through VGPRs (1) or by LDS DMA (0).
 #ifndef H3A_SPARSE_REGS
@@ -905,31 +910,36 @@ __device__ __forceinline__ void mid_barrier() {
 // from slot 2j+3 on, after every wave waited for its share of the DMA at the
 // end of slot 2j+2.
 //
-// kSparse: block-sparse attention on one 128-row query block, key-split.  A
-// stage is 128 keys in LDS: two 64-key halves of the block's LUT list (half t
-// is 64-key stage t of the list: key block t / sub, part t % sub), half
-// 2j + grp of stage j for group grp.  Every wave takes the 32 query rows of
-// slice wave & 3 against its group's half only, with its own running max,
-// row sum and O; each group fetches its own half (its 4 waves split it).  The
-// barrier slots are as above.  At the end group B hands (O, m, l) to the
-// group-A wave of the same slice through LDS, which merges them as the
-// split-tail combine does and stores O.
+// kSparse: block-sparse attention over pairs of 128-row query blocks, in
+// PadLayout.  Group A takes query block 2p and group B block 2p+1 of pair p,
+// each with its own LUT row and its own double-buffered K/V stages in LDS;
+// both step through the longer of the two stage lists (the shorter one's
+// extra stages load nothing and are fully masked).  A group stages its K/V
+// through VGPRs in its softmax slot: the global loads at the top, the LDS
+// writes at the end, so the registers are free again in its matrix slot.
+//   slot 2j+1:  A: MFMA(j)                    B: load K(j+2) V(j+1), SOFT(j-1), write
+//   slot 2j+2:  A: load K(j+2) V(j+1), SOFT(j), write     B: MFMA(j)
+// A group writes kbuf[j&1] and vbuf[(j+1)&1], last read by its own MFMA(j-1)
+// in an earlier slot, and reads them in MFMA(j+1), after the slot's barrier.
 template <class L, int NSUB, bool kSparse = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   constexpr int NW = 8;
   constexpr int BN = 32 * NSUB;  // keys per stage
-  constexpr int RB = kSparse ? 2 * BN : BN;  // key rows per stage buffer (sparse: two halves)
-  constexpr int kKE = StageBytes<L, RB>::kK / 2, kVE = StageBytes<L, RB>::kV / 2;  // elements
-  static_assert(!kSparse || BN == kBN, "block-sparse halves are 64 keys");
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kKE];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kVE];
+  constexpr int kKE = StageBytes<L, BN>::kK / 2, kVE = StageBytes<L, BN>::kV / 2;  // elements
+  constexpr int NG = kSparse ? 2 : 1;  // K/V streams: one per group (sparse)
+  static_assert(!kSparse || BN == kBN, "block-sparse stages are 64 keys");
+  static_assert(!kSparse || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[NG][2][kKE];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[NG][2][kVE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const bool lead = wave_u < NW / 2;  // group A
-  const int grp = kSparse ? (lead ? 0 : 1) : 0;  // sparse: key half
+  const int grp = kSparse ? (lead ? 0 : 1) : 0;
+  uint16_t(*kbuf)[kKE] = kbuf_all[grp];
+  uint16_t(*vbuf)[kVE] = vbuf_all[grp];
   const int nstages = (a.Skv + BN - 1) / BN;
   // Work item of this workgroup.  With a split tail, the first
   // a.split_first items are whole query tiles; each later tile is cut into
@@ -956,42 +966,58 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     j0 = (int)((int64_t)nstages * p / a.split_pieces);
     niter = (int)((int64_t)nstages * (p + 1) / a.split_pieces) - j0;  // >= 1
   }
-  // Sparse: a.nqt counts 128-row query blocks.
-  const int qt = w % a.nqt, bh = w / a.nqt;
+  // Sparse: a.nqt counts 128-row query blocks and w runs over (b, h, pair).
+  const int nw_bh = kSparse ? (a.nqt + 1) / 2 : a.nqt;
+  const int qt = w % nw_bh, bh = w / nw_bh;
   const int h = bh % a.H, b = bh / a.H;
   const uint16_t *Qb = a.q + b * a.qsb + h * a.qsh;
   const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
   const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
   uint16_t *Ob = a.o + b * a.osb + h * a.osh;
-  const int qrow = kSparse ? qt * 128 + (wave_u & 3) * 32 + l32 : qt * 256 + wave * 32 + l32;
-  // Sparse: the block's LUT row, its length in 64-key halves, and the stage
-  // count (two halves per stage).
-  int n64 = 0;
+  const int qrow = kSparse ? (2 * qt + grp) * 128 + (wave_u & 3) * 32 + l32 : qt * 256 + wave * 32 + l32;
+  // Sparse: this group's stage count and LUT row; both groups run the longer
+  // of the two lists.
+  int ngrp = niter;
   const int32_t *lut_row = nullptr;
   const int sub_sh = a.sub == 2 ? 1 : 0;
   if constexpr (kSparse) {
-    const int cnt = a.counts[(int64_t)bh * a.nqt + qt];
-    n64 = (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
-    niter = (n64 + 1) / 2;
-    lut_row = a.lut + ((int64_t)bh * a.nqt + qt) * a.lut_stride;
+    auto stages_of = [&](int qb) __attribute__((always_inline)) -> int {
+      if (qb >= a.nqt) return 0;
+      const int cnt = a.counts[(int64_t)bh * a.nqt + qb];
+      return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
+    };
+    const int qb = 2 * qt + grp;
+    ngrp = stages_of(qb);
+    const int nother = stages_of(2 * qt + 1 - grp);
+    niter = ngrp > nother ? ngrp : nother;
+    lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
   }
-  // First key of this group's part of local stage j (sparse: of half
-  // 2j + grp); past the list's end, and for LUT entries that name no key
-  // block, it is Skv, which loads nothing (zeros).
-  auto key_base = [&](int j) __attribute__((always_inline)) -> int {
+  // Sparse: LUT entry of local stage j (a key block of a.sub stages; read
+  // through the constant address space, so it is a scalar load), and the
+  // stage's first key from it.  Past this group's last stage, and for LUT
+  // entries that name no key block, the key is Skv, which loads nothing.
+  auto lut_entry = [&](int j) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      const int t = 2 * j + grp;
-      if (t >= n64) return a.Skv;
-      const int kb = lut_row[t >> sub_sh];
-      const int key0 = kb * a.blk_k + (t & (a.sub - 1)) * BN;
-      return (kb < 0 || key0 >= a.Skv) ? a.Skv : key0;
+      if (ngrp == 0) return -1;
+      const __attribute__((address_space(4))) int32_t *row =
+          (const __attribute__((address_space(4))) int32_t *)lut_row;
+      return row[(j < ngrp ? j : ngrp - 1) >> sub_sh];
+    } else {
+      return 0;
+    }
+  };
+  auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
+    if constexpr (kSparse) {
+      const int key0 = kb * a.blk_k + (j & (a.sub - 1)) * BN;
+      return (j < ngrp && kb >= 0 && key0 < a.Skv) ? key0 : a.Skv;
     } else {
       return j < niter ? (j0 + j) * BN : a.Skv;
     }
   };
+  auto key_base = [&](int j) __attribute__((always_inline)) -> int { return key_of_entry(j, lut_entry(j)); };
   if (kSparse && niter == 0) {
-    // The query block keeps no key block: O = 0.
-    if (qrow < a.Sq && lead) {
+    // Neither query block of the pair keeps a key block: O = 0.
+    if (qrow < a.Sq) {
       uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
 #pragma unroll
       for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
@@ -1013,14 +1039,12 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
-  // Sparse: group grp reads and fetches rows 64*grp .. 64*grp+63 of each
-  // stage buffer (an offset neither layout's per-step offsets interact with).
-  const int k_rd = L::k_base(l32, g) + grp * BN * L::kKRow;
-  const int v_rd = L::v_base(lane) + grp * BN * L::kVRow;
-  const int kho = grp * BN * L::kKRow / 2, vho = grp * BN * L::kVRow / 2;  // elements
+  const int k_rd = L::k_base(l32, g);
+  const int v_rd = L::v_base(lane);
 
-  // Each K/V stream is fetched by the waves that read it: all 8 (dense) or
-  // the 4 of the group (sparse: its half).
+  // Dense: each K/V stage is fetched by LDS DMA (all 8 waves, or split
+  // between the groups as the knobs say).  Sparse: each group stages its own
+  // stream through VGPRs (TileRegs, its 4 waves).
   // Dense with H3A_PP_A_KINST >= 0: waves w and w+4 share one column of
   // the 4-wave layout, split between them as the knobs say.
   constexpr bool kSplitDma = !kSparse && H3A_PP_A_KINST >= 0;
@@ -1090,11 +1114,26 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     }
   };
 
+  // Sparse: each group's 4 waves stage its K/V stream through VGPRs.
+  TileRegs<NW / 2, false> kst;
+  TileRegs<NW / 2, true> vst;
+  kst.init(a.kss, tid & 255);
+  vst.init(a.vss, tid & 255);
+
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
-  fetch_k(Kb, key_base(0), kbuf[0] + kho);
-  fetch_v(Vb, key_base(0), vbuf[0] + vho);
-  fetch_k(Kb, key_base(1), kbuf[1] + kho);
-  wait_vmem_all();
+  if constexpr (kSparse) {
+    kst.start(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
+    vst.start(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+    kst.finish(kbuf[0]);
+    vst.finish(vbuf[0]);
+    kst.start(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+    kst.finish(kbuf[1]);
+  } else {
+    fetch_k(Kb, key_base(0), kbuf[0]);
+    fetch_v(Vb, key_base(0), vbuf[0]);
+    fetch_k(Kb, key_base(1), kbuf[1]);
+    wait_vmem_all();
+  }
   __syncthreads();
   f32x16 s[NSUB];
   u32x4 pf[2 * NSUB];
@@ -1104,16 +1143,40 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 
   auto dma = [&](auto par, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;  // j & 1
-    if constexpr (kSparse) {
-      fetch_k(Kb, key_base(j + 2), kbuf[P] + kho);
-      fetch_v(Vb, key_base(j + 1), vbuf[P ^ 1] + vho);
-    } else {
-      fetch_k_cur(kbuf[P]);
-      fetch_v_cur(vbuf[P ^ 1]);
-    }
+    fetch_k_cur(kbuf[P]);
+    fetch_v_cur(vbuf[P ^ 1]);
   };
-  constexpr bool kALate =
-      kSparse ? H3A_SPARSE_PP_A_LATE != 0 : kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
+  // Sparse: the group's loads of K(j+2) and V(j+1) at the top of its softmax
+  // slot (or after its matrix cluster), and their LDS writes at the end of
+  // the softmax slot.  Entering stage j the group holds the first keys of
+  // stages j, j+1 and j+2 and the LUT entry of stage j+3.  lut_next(j),
+  // issued after a barrier, loads the entry of stage j+4 for the next
+  // stage_in, so the scalar load's wait falls on the following barrier with
+  // a softmax cluster in between.  The softmax masks with a held key too:
+  // stage j+1's for group A (SOFT(j)), stage j's for group B (SOFT(j-1)).
+  int kw0 = key_base(0), kw1 = key_base(1), kw2 = key_base(2), e3 = lut_entry(3);
+  int soft_key = 0;
+  auto stage_in = [&](int j) __attribute__((always_inline)) {
+    // Group A calls this in stage j before SOFT(j), which masks S(j+1); group
+    // B before SOFT(j-1) (at the top of stage j, or after MFMA(j-1) when
+    // H3A_SPARSE_PP_EARLY), which masks S(j).
+    soft_key = lead ? kw1 : kw0;
+    const int kw3 = key_of_entry(j + 3, e3);
+    kst.start(Kb, a.kss, kw2, a.Skv, nullptr);
+    vst.start(Vb, a.vss, kw1, a.Skv, nullptr);
+    kw0 = kw1;
+    kw1 = kw2;
+    kw2 = kw3;
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto lut_next = [&](int j) __attribute__((always_inline)) { e3 = lut_entry(j + 4); };
+  auto stage_out = [&](auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    kst.finish(kbuf[P]);
+    vst.finish(vbuf[P ^ 1]);
+  };
+  constexpr bool kALate = kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
   // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
@@ -1140,10 +1203,11 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   };
   auto soft = [&](int j) __attribute__((always_inline)) {
     if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(1);
+    const int key0 = kSparse ? soft_key : key_base(j + 1);
 #if H3A_PP_STALE_MAX
-    softmax_stage_stale<NSUB, kSparse>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
+    softmax_stage_stale<NSUB, kSparse>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
 #else
-    softmax_stage<NSUB>(s, key_base(j + 1), a.Skv, g, a.sl2, m, lsum, o, pf);
+    softmax_stage<NSUB>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
 #endif
 #if H3A_PP_PIN_SOFTMAX
 #pragma unroll
@@ -1156,6 +1220,17 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 
   if (lead) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
+      if constexpr (kSparse) {
+        mfma(par);
+        if (H3A_SPARSE_PP_EARLY) stage_in(j);
+        mid_barrier();
+        if (!H3A_SPARSE_PP_EARLY) stage_in(j);
+        lut_next(j);
+        if (j + 1 < niter) soft(j);
+        stage_out(par);
+        slot_barrier();
+        return;
+      }
       if constexpr (!kALate) dma(par, j);
       mfma(par);
       if constexpr (kALate) {
@@ -1175,6 +1250,17 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     // kFirst: stage 0, which has no softmax before its matrix cluster (P(0)
     // came from the prologue); peeled off so that the loop body has no branch.
     auto stage = [&](auto par, int j, auto first) __attribute__((always_inline)) {
+      if constexpr (kSparse) {
+        if (!H3A_SPARSE_PP_EARLY) stage_in(j);
+        lut_next(j);
+        if constexpr (!decltype(first)::value) soft(j - 1);
+        stage_out(par);
+        mid_barrier();
+        mfma(par);
+        if (H3A_SPARSE_PP_EARLY && j + 1 < niter) stage_in(j + 1);
+        slot_barrier();
+        return;
+      }
       dma(par, j);
       if constexpr (!decltype(first)::value) soft(j - 1);
       mid_barrier();
@@ -1184,6 +1270,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
+    if (kSparse && H3A_SPARSE_PP_EARLY) stage_in(0);
     stage(C0{}, 0, std::true_type{});
     for (int j = 1; j < niter; j += 2) {
       stage(C1{}, j, std::false_type{});
@@ -1191,35 +1278,6 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     }
   }
 
-  if constexpr (kSparse) {
-    // Both loops ended on the same barrier after their last LDS access, so
-    // the stage buffers hold the exchange: the group-B wave of each slice
-    // writes O (lane-major, 64 consecutive floats per register) into kbuf
-    // and m, l into vbuf; its group-A partner merges them.
-    static_assert(sizeof(kbuf) >= 4 * 64 * 64 * sizeof(float), "O exchange fits kbuf");
-    static_assert(sizeof(vbuf) >= 4 * 2 * 64 * sizeof(float), "m/l exchange fits vbuf");
-    float *xo = reinterpret_cast<float *>(&kbuf[0][0]) + (wave_u & 3) * 64 * 64;
-    float *xm = reinterpret_cast<float *>(&vbuf[0][0]) + (wave_u & 3) * 2 * 64;
-    if (!lead) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) xo[(16 * dt + r) * 64 + lane] = o[dt][r];
-      xm[lane] = m;
-      xm[64 + lane] = lsum;
-    }
-    __syncthreads();
-    if (!lead) return;  // no barrier follows
-    const float m2 = xm[lane], l2 = xm[64 + lane];
-    const float mn = fmaxf(m, m2);
-    const float a1 = m == kNegInf ? 0.f : fast_exp2(m - mn);
-    const float a2 = m2 == kNegInf ? 0.f : fast_exp2(m2 - mn);
-    lsum = lsum * a1 + l2 * a2;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a1 + xo[(16 * dt + r) * 64 + lane] * a2;
-  }
   const float ltot = half_swap_sum(lsum);
   if (piece >= 0) {
     // Partial result of one key range: unnormalised O, the reference max m
@@ -1438,7 +1496,11 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   if (H3A_SPARSE_PINGPONG && blk_q == 128) {
-    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SwzLayout, 2, true>), dim3(a.total), dim3(512), 0, s, a);
+    AttnArgs p = a;
+    const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
+    if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
+    p.total = (int)pairs;
+    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<PadLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
     return check_launch("attn_fwd_pingpong_kernel<sparse>");
   }
   if (blk_q == 128) {
@@ -1501,7 +1563,11 @@ int attn_kernel_attrs(int which, double out[6]) {
                         64 * H3A_DENSE_WAVES, out);
 #endif
     case H3A_KERNEL_ATTN_SPARSE_128:
+#if H3A_SPARSE_PINGPONG
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<PadLayout, 2, true>), 512, out);
+#else
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), 256, out);
+#endif
     case H3A_KERNEL_ATTN_SPARSE_64:
 #if H3A_SPARSE64_KEYSPLIT
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true, true>),
