@@ -98,7 +98,8 @@ namespace h3a {
 #define H3A_SPARSE_PINGPONG 1
 #endif
 // Sparse ping-pong: a group issues its K/V loads right after its matrix
-// cluster (1) instead of at the top of its softmax slot (0).
+// cluster (1), at the top of its softmax slot (0), or the K loads after the
+// matrix cluster and the V loads at the top of the softmax slot (2).
 #ifndef H3A_SPARSE_PP_EARLY
 #define H3A_SPARSE_PP_EARLY 1
 #endif
@@ -1151,24 +1152,35 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   // the softmax slot.  Entering stage j the group holds the first keys of
   // stages j, j+1 and j+2 and the LUT entry of stage j+3.  lut_next(j),
   // issued after a barrier, loads the entry of stage j+4 for the next
-  // stage_in, so the scalar load's wait falls on the following barrier with
+  // stage_keys, so the scalar load's wait falls on the following barrier with
   // a softmax cluster in between.  The softmax masks with a held key too:
   // stage j+1's for group A (SOFT(j)), stage j's for group B (SOFT(j-1)).
   int kw0 = key_base(0), kw1 = key_base(1), kw2 = key_base(2), e3 = lut_entry(3);
   int soft_key = 0;
-  auto stage_in = [&](int j) __attribute__((always_inline)) {
-    // Group A calls this in stage j before SOFT(j), which masks S(j+1); group
-    // B before SOFT(j-1) (at the top of stage j, or after MFMA(j-1) when
-    // H3A_SPARSE_PP_EARLY), which masks S(j).
+  // stage_keys(j) takes stage j's keys (K(j+2), V(j+1), the softmax mask)
+  // and moves the window on; load_k / load_v issue the loads.  Group A calls
+  // it in stage j before SOFT(j), which masks S(j+1); group B before
+  // SOFT(j-1) (at the top of stage j, or after MFMA(j-1) when the loads go
+  // early), which masks S(j).
+  int key_k = 0, key_v = 0;
+  auto stage_keys = [&](int j) __attribute__((always_inline)) {
     soft_key = lead ? kw1 : kw0;
+    key_k = kw2;
+    key_v = kw1;
     const int kw3 = key_of_entry(j + 3, e3);
-    kst.start(Kb, a.kss, kw2, a.Skv, nullptr);
-    vst.start(Vb, a.vss, kw1, a.Skv, nullptr);
     kw0 = kw1;
     kw1 = kw2;
     kw2 = kw3;
+  };
+  auto load_k = [&]() __attribute__((always_inline)) {
+    kst.start(Kb, a.kss, key_k, a.Skv, nullptr);
     __builtin_amdgcn_sched_barrier(0);
   };
+  auto load_v = [&]() __attribute__((always_inline)) {
+    vst.start(Vb, a.vss, key_v, a.Skv, nullptr);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  constexpr int kEarly = H3A_SPARSE_PP_EARLY;  // 0: none, 1: K and V, 2: K only
   auto lut_next = [&](int j) __attribute__((always_inline)) { e3 = lut_entry(j + 4); };
   auto stage_out = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
@@ -1222,9 +1234,17 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
       if constexpr (kSparse) {
         mfma(par);
-        if (H3A_SPARSE_PP_EARLY) stage_in(j);
+        if constexpr (kEarly > 0) {
+          stage_keys(j);
+          load_k();
+          if constexpr (kEarly == 1) load_v();
+        }
         mid_barrier();
-        if (!H3A_SPARSE_PP_EARLY) stage_in(j);
+        if constexpr (kEarly == 0) {
+          stage_keys(j);
+          load_k();
+        }
+        if constexpr (kEarly != 1) load_v();
         lut_next(j);
         if (j + 1 < niter) soft(j);
         stage_out(par);
@@ -1251,13 +1271,21 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     // came from the prologue); peeled off so that the loop body has no branch.
     auto stage = [&](auto par, int j, auto first) __attribute__((always_inline)) {
       if constexpr (kSparse) {
-        if (!H3A_SPARSE_PP_EARLY) stage_in(j);
+        if constexpr (kEarly == 0) {
+          stage_keys(j);
+          load_k();
+        }
+        if constexpr (kEarly != 1) load_v();
         lut_next(j);
         if constexpr (!decltype(first)::value) soft(j - 1);
         stage_out(par);
         mid_barrier();
         mfma(par);
-        if (H3A_SPARSE_PP_EARLY && j + 1 < niter) stage_in(j + 1);
+        if (kEarly > 0 && j + 1 < niter) {
+          stage_keys(j + 1);
+          load_k();
+          if constexpr (kEarly == 1) load_v();
+        }
         slot_barrier();
         return;
       }
@@ -1270,7 +1298,11 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
-    if (kSparse && H3A_SPARSE_PP_EARLY) stage_in(0);
+    if constexpr (kSparse && kEarly > 0) {
+      stage_keys(0);
+      load_k();
+      if constexpr (kEarly == 1) load_v();
+    }
     stage(C0{}, 0, std::true_type{});
     for (int j = 1; j < niter; j += 2) {
       stage(C1{}, j, std::false_type{});
