@@ -98,8 +98,9 @@ namespace h3a {
 #define H3A_SPARSE_PINGPONG 1
 #endif
 // Sparse ping-pong: a group issues its K/V loads right after its matrix
-// cluster (1), at the top of its softmax slot (0), or the K loads after the
-// matrix cluster and the V loads at the top of the softmax slot (2).
+// cluster (1), at the top of its softmax slot (0), the K loads after the
+// matrix cluster and the V loads at the top of the softmax slot (2), or
+// interleaved with the last 8 MFMAs of the matrix cluster (3).
 #ifndef H3A_SPARSE_PP_EARLY
 #define H3A_SPARSE_PP_EARLY 1
 #endif
@@ -1180,7 +1181,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     vst.start(Vb, a.vss, key_v, a.Skv, nullptr);
     __builtin_amdgcn_sched_barrier(0);
   };
-  constexpr int kEarly = H3A_SPARSE_PP_EARLY;  // 0: none, 1: K and V, 2: K only
+  constexpr int kEarly = H3A_SPARSE_PP_EARLY;  // 0: none, 1: K and V, 2: K only, 3: in the cluster
   auto lut_next = [&](int j) __attribute__((always_inline)) { e3 = lut_entry(j + 4); };
   auto stage_out = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
@@ -1203,12 +1204,20 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     score_tile<L, NSUB>(kbuf[P ^ 1], qf, k_rd, s);
     pv_tile<L, 2 * NSUB>(vbuf[P], pf, v_rd, o);
 #endif
+    constexpr bool kLoadsIn = kSparse && kEarly == 3;
+    if constexpr (kLoadsIn) {
+      // Sparse: the group's next K/V loads (stage_keys ran before), one after
+      // each of the last 8 MFMAs, whose execution hides part of their issue.
+      kst.start(Kb, a.kss, key_k, a.Skv, nullptr);
+      vst.start(Vb, a.vss, key_v, a.Skv, nullptr);
+    }
 #if H3A_PP_READ_AHEAD
     __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
 #pragma unroll
     for (int i = 0; i < 16 * NSUB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
+      if (kLoadsIn && i >= 16 * NSUB - 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
 #endif
     if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(0);
@@ -1233,8 +1242,9 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   if (lead) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
       if constexpr (kSparse) {
+        if constexpr (kEarly == 3) stage_keys(j);
         mfma(par);
-        if constexpr (kEarly > 0) {
+        if constexpr (kEarly == 1 || kEarly == 2) {
           stage_keys(j);
           load_k();
           if constexpr (kEarly == 1) load_v();
@@ -1244,7 +1254,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
           stage_keys(j);
           load_k();
         }
-        if constexpr (kEarly != 1) load_v();
+        if constexpr (kEarly == 0 || kEarly == 2) load_v();
         lut_next(j);
         if (j + 1 < niter) soft(j);
         stage_out(par);
@@ -1275,13 +1285,16 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
           stage_keys(j);
           load_k();
         }
-        if constexpr (kEarly != 1) load_v();
+        if constexpr (kEarly == 0 || kEarly == 2) load_v();
         lut_next(j);
         if constexpr (!decltype(first)::value) soft(j - 1);
         stage_out(par);
         mid_barrier();
+        // kEarly == 3: the loads for stage j+1 go inside the matrix cluster,
+        // also after the last stage (keys past the list: nothing is read).
+        if constexpr (kEarly == 3) stage_keys(j + 1);
         mfma(par);
-        if (kEarly > 0 && j + 1 < niter) {
+        if ((kEarly == 1 || kEarly == 2) && j + 1 < niter) {
           stage_keys(j + 1);
           load_k();
           if constexpr (kEarly == 1) load_v();
@@ -1301,7 +1314,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     if constexpr (kSparse && kEarly > 0) {
       stage_keys(0);
       load_k();
-      if constexpr (kEarly == 1) load_v();
+      if constexpr (kEarly != 2) load_v();
     }
     stage(C0{}, 0, std::true_type{});
     for (int j = 1; j < niter; j += 2) {
@@ -1309,6 +1322,9 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       if (j + 1 < niter) stage(C0{}, j + 1, std::false_type{});
     }
   }
+  // Sparse, loads inside the matrix cluster: group B's last stage issued
+  // loads (of nothing: keys past its list) that no stage writes out.
+  if constexpr (kSparse) wait_vmem_all();
 
   const float ltot = half_swap_sum(lsum);
   if (piece >= 0) {
