@@ -16,6 +16,7 @@
 // Centring k by its sequence mean (SLA's K smoothing) shifts every score of a
 // row by the same amount, so it never changes the selection and is not needed.
 #include <type_traits>
+#include <utility>
 
 #include "h3a_device.h"
 #include "h3a_internal.h"
@@ -61,19 +62,57 @@ __global__ void __launch_bounds__(256) block_pool_kernel(const uint16_t *x, int6
 }
 
 constexpr int kSelThreads = 256;
-#ifndef H3A_SEL_ROWS
-#define H3A_SEL_ROWS 8
-#endif
-constexpr int kSelRowsMax = H3A_SEL_ROWS;  // query blocks per workgroup (at most)
-constexpr int kSelKeyChunk = 32;        // pooled key vectors staged in LDS at a time
+constexpr int kSelRowsPerWave = 4;
+constexpr int kSelRowsMax = kSelRowsPerWave * (kSelThreads / 64);  // query blocks per workgroup
+constexpr int kSelKeyChunk = 64;         // pooled key vectors staged in LDS at a time (one per lane)
 constexpr int kSelKeyPitch = kPoolD + 4; // floats per staged key row (bank spread)
-// LDS for the score rows: 64 KiB minus the query rows and the key chunk.
-constexpr int kSelScoreBytes = 65536 - (H3A_SEL_ROWS * kPoolD + kSelKeyChunk * kSelKeyPitch) * 4;
+constexpr int kSelChunkBytes = kSelKeyChunk * kSelKeyPitch * 4;
+// LDS per workgroup (two fit on a CU): the key chunk, then the score rows.
+constexpr int kSelLdsBytes = 81920;
+constexpr int kSelScoreBytes = kSelLdsBytes - kSelChunkBytes;
+
+// acc += q_J * k with q_J = lane J of q's 16-lane row (DPP row_newbcast:J on
+// src0).  As inline asm because the compiler keeps the broadcast as a separate
+// v_mov_b32_dpp.  q is written by loads only (never by a VALU instruction just
+// before), so the VALU-write / DPP-read hazard does not arise.
+template <int J>
+__device__ __forceinline__ float fmac_bcast(float acc, float q, float k) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc)
+      : "v"(q), "v"(k), "i"(J));
+  return acc;
+}
+// Four query rows' dot products with one key vector (lane l: key block
+// kc + l), advanced over dim D.  Register qv[i][m] of lane l holds
+// q_i[16m + l%16], so row_newbcast:(D%16) on qv[i][D/16] gives every lane
+// q_i[D]: one FMA per (row, dim), in the order d = 0..127.
+template <int D>
+__device__ __forceinline__ void score_dim(float (&acc)[4], const float (&qv)[4][kPoolD / 16], float k) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = fmac_bcast<D & 15>(acc[i], qv[i][D >> 4], k);
+}
+template <int D4>
+__device__ __forceinline__ void score_dims(float (&acc)[4], const float (&qv)[4][kPoolD / 16],
+                                           const float *kr) {
+  const float4 k4 = *(const float4 *)(kr + 4 * D4);
+  score_dim<4 * D4 + 0>(acc, qv, k4.x);
+  score_dim<4 * D4 + 1>(acc, qv, k4.y);
+  score_dim<4 * D4 + 2>(acc, qv, k4.z);
+  score_dim<4 * D4 + 3>(acc, qv, k4.w);
+}
+template <int... D4>
+__device__ __forceinline__ void score_key(float (&acc)[4], const float (&qv)[4][kPoolD / 16],
+                                          const float *kr, std::integer_sequence<int, D4...>) {
+  (score_dims<D4>(acc, qv, kr), ...);
+}
 
 // R (<= kSelRowsMax) query blocks of one (b,h) per workgroup, so each pooled
-// key vector is read from memory once per R rows.  Scores of all R rows go to
-// LDS (same fp32 FMA order as a plain dot product over d = 0..127).  Then wave
-// w selects rows w, w+4, with lane l on key blocks j = 64c + l: a bitwise
+// key vector is read from memory once per R rows.  Scores: lane l of every
+// wave takes key block kc + l of a 64-block chunk staged in LDS, and wave w
+// takes query rows w, w+4, w+8, w+12, held in registers across the DPP rows;
+// each dot product is the plain fp32 FMA chain over d = 0..127.
+// The R score rows go to LDS.  Then wave
+// w selects rows w, w+4, ..., with lane l on key blocks j = 64c + l: a bitwise
 // search over order-preserving keys finds the row's keep-th largest score in
 // 32 counting rounds (ballot + popcount), which fixes the kept set under
 // (score desc, index asc) order without ranking every pair.  Kept indices are
@@ -82,8 +121,7 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     const float *pq, const float *pk, int nq, int nk, int rows_per_wg, int keep, int force_diag,
     int blk_q, int blk_k, int32_t *lut, int32_t *counts, int max_k, uint8_t *map) {
   extern __shared__ float sel_lds[];
-  float *qs = sel_lds;                                   // [kSelRowsMax][128] pooled query blocks
-  float *ks = qs + kSelRowsMax * kPoolD;                 // [kSelKeyChunk][kSelKeyPitch] key chunk
+  float *ks = sel_lds;                                   // [kSelKeyChunk][kSelKeyPitch] key chunk
   float *sc = ks + kSelKeyChunk * kSelKeyPitch;          // [R][nk] scores
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int R = rows_per_wg;
@@ -91,40 +129,51 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
   const int64_t bh = blockIdx.x / ngroups;
   const int i0 = (int)(blockIdx.x % ngroups) * R;
   const int nrows = nq - i0 < R ? nq - i0 : R;
-  for (int t = tid; t < kSelRowsMax * kPoolD; t += kSelThreads) {
-    const int r = t / kPoolD;
-    qs[t] = r < nrows ? pq[((bh * nq) + i0 + r) * kPoolD + (t % kPoolD)] : 0.f;
+  // This wave's query rows, clamped to a valid row (results past nrows are
+  // not stored), as score_dims wants them.
+  static_assert(kSelRowsPerWave == 4, "score_dims takes four rows");
+  float qv[kSelRowsPerWave][kPoolD / 16];
+#pragma unroll
+  for (int i = 0; i < kSelRowsPerWave; ++i) {
+    const int r = wave + 4 * i < nrows ? wave + 4 * i : nrows - 1;
+    const float *qp = pq + (bh * nq + i0 + r) * kPoolD + (lane & 15);
+#pragma unroll
+    for (int m = 0; m < kPoolD / 16; ++m) qv[i][m] = qp[16 * m];
   }
-  // Scores, kSelKeyChunk key blocks at a time: the chunk is staged with
-  // coalesced 16-byte loads, then thread (r, kk) forms one dot product in
-  // the order d = 0..127.
+  // Key chunks go through registers with coalesced 16-byte loads, the next
+  // chunk's loads in flight while the current one is scored.  Rows past nk
+  // repeat the last key block (the chunk after the last one too); their
+  // scores are never stored.
   const float *pkh = pk + bh * (int64_t)nk * kPoolD;
-  const int my_r = tid / kSelKeyChunk, my_k = tid % kSelKeyChunk;
-  static_assert(kSelRowsMax * kSelKeyChunk <= kSelThreads, "one dot product per thread per chunk");
+  constexpr int kStage = kSelKeyChunk * (kPoolD / 4) / kSelThreads;  // float4 per thread per chunk
+  const int st_kk = tid / (kPoolD / 4), st_f4 = tid % (kPoolD / 4);
+  constexpr int kRowsPerPass = kSelThreads / (kPoolD / 4);
+  typedef float f32x4 __attribute__((ext_vector_type(4)));  // (HIP's float4 struct stays in scratch here)
+  f32x4 pre[kStage];
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int j = st_kk + u * kRowsPerPass < nk ? st_kk + u * kRowsPerPass : nk - 1;
+    pre[u] = *(const f32x4 *)(pkh + (int64_t)j * kPoolD + 4 * st_f4);
+  }
   for (int kc = 0; kc < nk; kc += kSelKeyChunk) {
-    __syncthreads();  // qs written / previous chunk consumed
-    for (int t = tid; t < kSelKeyChunk * (kPoolD / 4); t += kSelThreads) {
-      const int kk = t / (kPoolD / 4), f4 = t % (kPoolD / 4);
-      const float4 v = kc + kk < nk ? *(const float4 *)(pkh + (int64_t)(kc + kk) * kPoolD + 4 * f4)
-                                    : float4{0.f, 0.f, 0.f, 0.f};
-      *(float4 *)(ks + kk * kSelKeyPitch + 4 * f4) = v;
-    }
+    __syncthreads();  // previous chunk consumed
+#pragma unroll
+    for (int u = 0; u < kStage; ++u)
+      *(f32x4 *)(ks + (st_kk + u * kRowsPerPass) * kSelKeyPitch + 4 * st_f4) = pre[u];
     __syncthreads();
-    if (my_r < nrows && kc + my_k < nk) {
-      const float *qr = qs + my_r * kPoolD;
-      const float *kr = ks + my_k * kSelKeyPitch;
-      float acc = 0.f;
-#pragma unroll 8
-      for (int d = 0; d < kPoolD; d += 4) {
-        const float4 q4 = *(const float4 *)(qr + d);
-        const float4 k4 = *(const float4 *)(kr + d);
-        acc = fmaf(q4.x, k4.x, acc);
-        acc = fmaf(q4.y, k4.y, acc);
-        acc = fmaf(q4.z, k4.z, acc);
-        acc = fmaf(q4.w, k4.w, acc);
-      }
-      sc[my_r * nk + kc + my_k] = acc;
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int jn = kc + kSelKeyChunk + st_kk + u * kRowsPerPass;
+      pre[u] = *(const f32x4 *)(pkh + (int64_t)(jn < nk ? jn : nk - 1) * kPoolD + 4 * st_f4);
     }
+    const float *kr = ks + lane * kSelKeyPitch;
+    float acc[kSelRowsPerWave];
+#pragma unroll
+    for (int i = 0; i < kSelRowsPerWave; ++i) acc[i] = 0.f;
+    score_key(acc, qv, kr, std::make_integer_sequence<int, kPoolD / 4>{});
+#pragma unroll
+    for (int i = 0; i < kSelRowsPerWave; ++i)
+      if (wave + 4 * i < nrows && kc + lane < nk) sc[(wave + 4 * i) * nk + kc + lane] = acc[i];
   }
   __syncthreads();
 
@@ -135,45 +184,94 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   };
   const int nchunks = (nk + 63) / 64;
-  // NC > 0: the row's keys are held in NC registers per lane for the counting
-  // rounds (rows of up to NC*64 key blocks); NC = 0: longer rows re-read
-  // them from LDS each round.
-  auto select_rows = [&](auto nc_const) __attribute__((always_inline)) {
+  // Kept set of row r from its threshold: exactly the keys > T and the first
+  // `need` keys == T in index order (rank < keep under (score desc, index
+  // asc)), plus the optional diagonal; indices written in ascending order.
+  auto write_row = [&](int r, uint32_t T, int need) __attribute__((always_inline)) {
+    const float *row_sc = sc + r * nk;
+    const int64_t row = bh * nq + i0 + r;
+    const int diag = (int)(((int64_t)(i0 + r) * blk_q) / blk_k);
+    int32_t *out = lut + row * max_k;
+    int base = 0, eq_before = 0;
+    for (int c = 0; c < nchunks; ++c) {
+      const int j = c * 64 + lane;
+      const uint32_t kj = j < nk ? key_of(row_sc[j < nk ? j : 0]) : 0u;
+      const bool eq = keep > 0 && j < nk && kj == T;
+      const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
+      const bool by_rank = keep > 0 && j < nk && (kj > T || (eq && eq_before + __builtin_popcountll(eqm & below) < need));
+      const bool kept = by_rank || (force_diag && j == diag && j < nk);
+      eq_before += __builtin_popcountll(eqm);
+      const uint64_t m = __builtin_amdgcn_ballot_w64(kept);
+      const int pos = base + __builtin_popcountll(m & below);
+      if (kept && pos < max_k) out[pos] = j;
+      if (map && j < nk) map[row * nk + j] = (uint8_t)kept;
+      base += __builtin_popcountll(m);
+    }
+    const int kept_n = base < max_k ? base : max_k;
+    for (int t = kept_n + lane; t < max_k; t += 64) out[t] = -1;
+    if (lane == 0) counts[row] = kept_n;
+  };
+  // T = the keep-th largest key of a row: the largest t with (number of the
+  // row's keys >= t) >= keep, built from the top bit down; need = keep - the
+  // number of keys > T.  Every t asked for is >= 1, every score that is not a
+  // NaN has a key > 0, and the padding key 0 is never counted.
+  //
+  // Rows of up to NC*64 key blocks (NC = 6 or 12): the keys of all of this
+  // wave's rows (wave + 4i) sit in registers, NC per lane per row, and the
+  // rows' searches run interleaved, so their 32 dependent counting rounds
+  // overlap.
+  auto select_rows_regs = [&](auto nc_const) __attribute__((always_inline)) {
     constexpr int NC = decltype(nc_const)::value;
-    constexpr int kSelRegChunks = NC > 0 ? NC : 1;
-    constexpr bool in_regs = NC > 0;
+    uint32_t T[kSelRowsPerWave], kr[kSelRowsPerWave][NC];
+    int need[kSelRowsPerWave];
+#pragma unroll
+    for (int i = 0; i < kSelRowsPerWave; ++i) {
+      const int r = wave + 4 * i;
+      const float *row_sc = sc + (r < nrows ? r : 0) * nk;
+      T[i] = 0;
+      need[i] = 0;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int j = c * 64 + lane;
+        kr[i][c] = (r < nrows && j < nk) ? key_of(row_sc[j < nk ? j : 0]) : 0u;
+      }
+    }
+    auto count_ge = [&](const uint32_t(&k)[NC], uint32_t t) __attribute__((always_inline)) -> int {
+      int n = 0;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(k[c] >= t));
+      return n;
+    };
+    if (keep > 0) {
+      for (int bit = 31; bit >= 0; --bit) {
+#pragma unroll
+        for (int i = 0; i < kSelRowsPerWave; ++i) {
+          const uint32_t cand = T[i] | (1u << bit);
+          T[i] = count_ge(kr[i], cand) >= keep ? cand : T[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kSelRowsPerWave; ++i)
+        need[i] = keep - (T[i] == 0xffffffffu ? 0 : count_ge(kr[i], T[i] + 1));
+    }
+#pragma unroll
+    for (int i = 0; i < kSelRowsPerWave; ++i)
+      if (wave + 4 * i < nrows) write_row(wave + 4 * i, T[i], need[i]);
+  };
+  // Longer rows: one row at a time, keys re-read from LDS every round.
+  auto select_rows_lds = [&]() __attribute__((always_inline)) {
     for (int r = wave; r < nrows; r += kSelThreads / 64) {
       const float *row_sc = sc + r * nk;
-      const int64_t row = bh * nq + i0 + r;
-      const int diag = (int)(((int64_t)(i0 + r) * blk_q) / blk_k);
-      int32_t *out = lut + row * max_k;
-      uint32_t kr[kSelRegChunks];  // valid keys; 0 (never counted: t >= 1 below) past nk
-#pragma unroll
-      for (int c = 0; c < kSelRegChunks; ++c) {
-        const int j = c * 64 + lane;
-        kr[c] = (in_regs && j < nk) ? key_of(row_sc[j < nk ? j : 0]) : 0u;
-      }
-      // Number of the row's keys >= t.  Every t asked for is >= 1, every score
-      // that is not a NaN has a key > 0, and the padding key 0 is never counted.
       auto count_ge = [&](uint32_t t) __attribute__((always_inline)) -> int {
         int n = 0;
-        if constexpr (in_regs) {
-#pragma unroll
-          for (int c = 0; c < kSelRegChunks; ++c) n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(kr[c] >= t));
-        } else {
-          for (int c = 0; c < nchunks; ++c) {
-            const int j = c * 64 + lane;
-            n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < nk && key_of(row_sc[j < nk ? j : 0]) >= t));
-          }
+        for (int c = 0; c < nchunks; ++c) {
+          const int j = c * 64 + lane;
+          n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < nk && key_of(row_sc[j < nk ? j : 0]) >= t));
         }
         return n;
       };
-      // T = the keep-th largest key: the largest t with count_ge(t) >= keep,
-      // built from the top bit down.  Then exactly the keys > T and the first
-      // (keep - #keys > T) keys == T in index order have rank < keep under
-      // (score desc, index asc).
       uint32_t T = 0;
-      int need = 0;  // keys == T to keep
+      int need = 0;
       if (keep > 0) {
         for (int bit = 31; bit >= 0; --bit) {
           const uint32_t cand = T | (1u << bit);
@@ -181,32 +279,15 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
         }
         need = keep - (T == 0xffffffffu ? 0 : count_ge(T + 1));
       }
-      int base = 0, eq_before = 0;
-      for (int c = 0; c < nchunks; ++c) {
-        const int j = c * 64 + lane;
-        const uint32_t kj = j < nk ? key_of(row_sc[j < nk ? j : 0]) : 0u;
-        const bool eq = keep > 0 && j < nk && kj == T;
-        const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
-        const bool by_rank = keep > 0 && j < nk && (kj > T || (eq && eq_before + __builtin_popcountll(eqm & below) < need));
-        const bool kept = by_rank || (force_diag && j == diag && j < nk);
-        eq_before += __builtin_popcountll(eqm);
-        const uint64_t m = __builtin_amdgcn_ballot_w64(kept);
-        const int pos = base + __builtin_popcountll(m & below);
-        if (kept && pos < max_k) out[pos] = j;
-        if (map && j < nk) map[row * nk + j] = (uint8_t)kept;
-        base += __builtin_popcountll(m);
-      }
-      const int kept_n = base < max_k ? base : max_k;
-      for (int t = kept_n + lane; t < max_k; t += 64) out[t] = -1;
-      if (lane == 0) counts[row] = kept_n;
+      write_row(r, T, need);
     }
   };
   if (nchunks <= 6)
-    select_rows(std::integral_constant<int, 6>{});
+    select_rows_regs(std::integral_constant<int, 6>{});
   else if (nchunks <= 12)
-    select_rows(std::integral_constant<int, 12>{});
+    select_rows_regs(std::integral_constant<int, 12>{});
   else
-    select_rows(std::integral_constant<int, 0>{});
+    select_rows_lds();
 }
 
 int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int S, int blk,
@@ -223,7 +304,15 @@ int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, 
                         int max_k, uint8_t *map, hipStream_t s) {
   int rows = kSelScoreBytes / (nk * (int)sizeof(float));
   rows = rows < 1 ? 1 : (rows > kSelRowsMax ? kSelRowsMax : rows);
-  const size_t lds = (size_t)(kSelRowsMax * kPoolD + kSelKeyChunk * kSelKeyPitch + rows * nk) * sizeof(float);
+  const size_t lds = (size_t)kSelChunkBytes + (size_t)rows * nk * sizeof(float);
+  // Above 64 KiB of dynamic LDS the kernel is allowed the larger size first
+  // (on the current device; a host-side setting, no stream work).
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&block_select_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kSelLdsBytes);
+    if (e != hipSuccess)
+      return fail(H3A_ERR_HIP, "block_select_kernel: %zu bytes of LDS refused: %s", lds, hipGetErrorString(e));
+  }
   const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
   hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)groups), dim3(kSelThreads), lds, s, pq, pk, nq,
                      nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);

@@ -320,9 +320,10 @@ def _select_ref(pq, pk, keep, blk_q, blk_k, diag, max_k):
 def test_block_select_exact_ties(gpu, nq, nk, keep, diag, max_k):
     """Integer pooled vectors make every score an exact fp32 integer, with many ties:
     the kept set, its order and the truncation to max_k_blocks must match exactly.
-    Covers row groups of up to 8 query blocks per workgroup and all three counting
-    paths: keys held in 6 registers (nk <= 384), in 12 (nk <= 768), and re-read from
-    LDS (769, 1000)."""
+    Covers row groups of up to 16 query blocks per workgroup (fewer where the score
+    rows fill LDS: 15 at nk 769, 12 at nk 1000) and all three counting paths: keys
+    held in 6 registers (nk <= 384), in 12 (nk <= 768), and re-read from LDS (769,
+    1000)."""
     rng = np.random.default_rng(50 + nq + nk)
     pq = rng.integers(-2, 3, (1, 2, nq, 128)).astype(np.float32)
     pk = rng.integers(-2, 3, (1, 2, nk, 128)).astype(np.float32)
