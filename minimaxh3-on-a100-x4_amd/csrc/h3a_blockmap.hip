@@ -214,7 +214,9 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
   // T = the keep-th largest key of a row: the largest t with (number of the
   // row's keys >= t) >= keep, built from the top bit down; need = keep - the
   // number of keys > T.  Every t asked for is >= 1, every score that is not a
-  // NaN has a key > 0, and the padding key 0 is never counted.
+  // NaN has a key > 0, and the padding key 0 is never counted.  The search
+  // stops early once exactly keep keys are >= the candidate c: the kept set
+  // is then {keys >= c}, written as T = c - 1, need = 0.
   //
   // Rows of up to NC*64 key blocks (NC = 6 or 12): the keys of all of this
   // wave's rows (wave + 4i) sit in registers, NC per lane per row, and the
@@ -243,16 +245,29 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
       return n;
     };
     if (keep > 0) {
+      bool done[kSelRowsPerWave];
+#pragma unroll
+      for (int i = 0; i < kSelRowsPerWave; ++i) done[i] = wave + 4 * i >= nrows;
       for (int bit = 31; bit >= 0; --bit) {
 #pragma unroll
         for (int i = 0; i < kSelRowsPerWave; ++i) {
+          if (done[i]) continue;
           const uint32_t cand = T[i] | (1u << bit);
-          T[i] = count_ge(kr[i], cand) >= keep ? cand : T[i];
+          const int n = count_ge(kr[i], cand);
+          if (n >= keep) T[i] = cand;
+          if (n == keep) {
+            T[i] = cand - 1;
+            done[i] = true;
+          }
         }
+        bool all = true;
+#pragma unroll
+        for (int i = 0; i < kSelRowsPerWave; ++i) all = all && done[i];
+        if (all) break;
       }
 #pragma unroll
       for (int i = 0; i < kSelRowsPerWave; ++i)
-        need[i] = keep - (T[i] == 0xffffffffu ? 0 : count_ge(kr[i], T[i] + 1));
+        need[i] = done[i] ? 0 : keep - (T[i] == 0xffffffffu ? 0 : count_ge(kr[i], T[i] + 1));
     }
 #pragma unroll
     for (int i = 0; i < kSelRowsPerWave; ++i)
@@ -273,11 +288,17 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
       uint32_t T = 0;
       int need = 0;
       if (keep > 0) {
-        for (int bit = 31; bit >= 0; --bit) {
+        bool done = false;
+        for (int bit = 31; bit >= 0 && !done; --bit) {
           const uint32_t cand = T | (1u << bit);
-          if (count_ge(cand) >= keep) T = cand;
+          const int n = count_ge(cand);
+          if (n >= keep) T = cand;
+          if (n == keep) {
+            T = cand - 1;
+            done = true;
+          }
         }
-        need = keep - (T == 0xffffffffu ? 0 : count_ge(T + 1));
+        if (!done) need = keep - (T == 0xffffffffu ? 0 : count_ge(T + 1));
       }
       write_row(r, T, need);
     }
