@@ -14,7 +14,7 @@ import torch
 
 import h3attn
 import standin_dit
-from h3attn import graphs, hooks, profiling
+from h3attn import graphs, hooks, ops, profiling
 
 pytestmark = pytest.mark.gpu
 
@@ -55,6 +55,33 @@ def test_graph_replay_matches_eager(gpu):
         torch.cuda.synchronize()
         for i, (o, w) in enumerate(zip(outs, want)):
             assert torch.equal(o, w), f"replay {r}, layer {i} differs from the eager run"
+
+
+def test_graph_capture_of_wide_block_select(gpu):
+    """Block select over 700 key blocks per row, where the kernel takes more than 64 KiB
+    of LDS and each call first raises its dynamic-LDS limit (a host-side setting):
+    captured into a graph, every replay equals the eager call."""
+    g = torch.Generator(device=gpu).manual_seed(41)
+    pq = torch.randn(1, 2, 20, 128, generator=g, device=gpu)
+    pk = torch.randn(1, 2, 700, 128, generator=g, device=gpu)
+    want = [t.clone() for t in ops.block_select(pq, pk, 175, 64, 64)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.block_select(pq, pk, 175, 64, 64)  # warm-up off the default stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = ops.block_select(pq, pk, 175, 64, 64)
+    other = torch.randn(1, 2, 300, 128, device=gpu, dtype=torch.bfloat16)
+    for r in range(3):
+        h3attn.attn_fwd(other, other, other)  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, o, w in zip(("map", "lut", "counts"), outs, want):
+            assert torch.equal(o, w), f"replay {r}: {name} differs from the eager call"
 
 
 def test_graph_capture_requires_capture_before_replay(gpu):
