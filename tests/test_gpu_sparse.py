@@ -316,14 +316,15 @@ def _select_ref(pq, pk, keep, blk_q, blk_k, diag, max_k):
 @pytest.mark.parametrize("nq,nk,keep,diag,max_k", [
     (9, 700, 37, True, 38), (17, 65, 1, False, 1), (1, 64, 64, False, 64), (9, 1, 1, True, 1),
     (17, 700, 100, True, 50), (16, 200, 20, False, 20), (5, 384, 96, True, 97),
-    (3, 769, 10, False, 10), (5, 1000, 150, True, 151)])
+    (3, 769, 10, False, 10), (5, 1000, 150, True, 151), (3, 5000, 40, True, 41),
+    (2, 7000, 100, False, 100)])
 def test_block_select_exact_ties(gpu, nq, nk, keep, diag, max_k):
     """Integer pooled vectors make every score an exact fp32 integer, with many ties:
     the kept set, its order and the truncation to max_k_blocks must match exactly.
     Covers row groups of up to 16 query blocks per workgroup (fewer where the score
-    rows fill LDS: 15 at nk 769, 12 at nk 1000) and all three counting paths: keys
-    held in 6 registers (nk <= 384), in 12 (nk <= 768), and re-read from LDS (769,
-    1000)."""
+    rows fill LDS: 15 at nk 769, 12 at nk 1000, 2 at nk 5000, 1 at the 7000 maximum)
+    and all three counting paths: keys held in 6 registers (nk <= 384), in 12
+    (nk <= 768), and re-read from LDS (769 and above)."""
     rng = np.random.default_rng(50 + nq + nk)
     pq = rng.integers(-2, 3, (1, 2, nq, 128)).astype(np.float32)
     pk = rng.integers(-2, 3, (1, 2, nk, 128)).astype(np.float32)
