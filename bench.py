@@ -241,7 +241,8 @@ def run_sparse(args, torch, h3attn, dev):
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": ("attn_fwd_pingpong_kernel<PadLayout,2,sparse> (pairs of query blocks)" if blk == 128
+                     "kernel": ("attn_fwd_pingpong_kernel<PadLayout,2,sparse> (pairs of query blocks; "
+                                "+ split_combine_kernel for the split tail)" if blk == 128
                                 else "attn_fwd_kernel<4,PadLayout,regs,sparse,key-split>"), "flop_per_launch": flops,
                      "avg_launch_ms": round(avg_kernel_ms, 3)},
     })

@@ -108,6 +108,29 @@ int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *
                              float scale, h3a_stream_t stream);
 
 /*
+ * h3a_attn_fwd_blocksparse with a caller-supplied device workspace, as
+ * h3a_attn_fwd_ws is to h3a_attn_fwd: with blk_q = 128, the pairs of query
+ * blocks in the last, partly filled round of workgroups are each split into
+ * ranges of their kept-block lists that run side by side, merged by a second
+ * kernel on the same stream (results equal h3a_attn_fwd_blocksparse's within
+ * floating-point rounding).  h3a_attn_fwd_blocksparse_workspace_size gives the
+ * bytes needed on the current device (0: nothing is split, and workspace may
+ * be NULL); the workspace rules are those of h3a_attn_fwd_ws.  This entry
+ * point has no counterpart in the reference; h3a_attn_fwd_blocksparse is the
+ * drop-in for the h3_sla path.
+ */
+int h3a_attn_fwd_blocksparse_workspace_size(int B, int H, int Sq, int Skv, int D,
+                                            int blk_q, int blk_k, int max_k_blocks, size_t *bytes);
+int h3a_attn_fwd_blocksparse_ws(const void *q, const void *k, const void *v, void *o,
+                                int B, int H, int Sq, int Skv, int D,
+                                const int64_t q_strides[3], const int64_t k_strides[3],
+                                const int64_t v_strides[3], const int64_t o_strides[3],
+                                const int32_t *lut, const int32_t *counts,
+                                int blk_q, int blk_k, int max_k_blocks,
+                                float scale, void *workspace, size_t workspace_bytes,
+                                h3a_stream_t stream);
+
+/*
  * Compact a boolean block map [B,H,nq,nk] (uint8, 0/1, contiguous) into the
  * LUT form h3a_attn_fwd_blocksparse consumes: lut [B,H,nq,max_k_blocks]
  * (kept key-block indices in ascending order, tail entries set to -1) and

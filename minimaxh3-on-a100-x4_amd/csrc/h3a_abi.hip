@@ -136,13 +136,13 @@ int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o, int B,
   return launch_attn_dense_split(a, plan, workspace, as_stream(stream));
 }
 
-int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o, int B, int H,
-                             int Sq, int Skv, int D, const int64_t q_strides[3],
-                             const int64_t k_strides[3], const int64_t v_strides[3],
-                             const int64_t o_strides[3], const int32_t *lut, const int32_t *counts,
-                             int blk_q, int blk_k, int max_k_blocks, float scale,
-                             h3a_stream_t stream) {
-  clear_error();
+namespace {
+
+// Checks shared by the block-sparse entry points; fills `a` on success.
+int prepare_blocksparse(AttnArgs &a, const void *q, const void *k, const void *v, void *o, int B, int H,
+                        int Sq, int Skv, int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                        const int64_t v_strides[3], const int64_t o_strides[3], const int32_t *lut,
+                        const int32_t *counts, int blk_q, int blk_k, int max_k_blocks, float scale) {
   int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
   if (rc) return rc;
   if (!lut || !counts) return fail(H3A_ERR_INVALID_ARG, "null lut/counts pointer");
@@ -154,7 +154,6 @@ int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *
   const int64_t nqt = (Sq + blk_q - 1) / blk_q;
   const int64_t total = (int64_t)B * H * nqt;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
-  AttnArgs a;
   fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
   a.nqt = (int)nqt;
   a.total = (int)total;
@@ -163,7 +162,65 @@ int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *
   a.lut_stride = max_k_blocks;
   a.blk_k = blk_k;
   a.sub = blk_k / 64;
+  return H3A_OK;
+}
+
+}  // namespace
+
+int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o, int B, int H,
+                             int Sq, int Skv, int D, const int64_t q_strides[3],
+                             const int64_t k_strides[3], const int64_t v_strides[3],
+                             const int64_t o_strides[3], const int32_t *lut, const int32_t *counts,
+                             int blk_q, int blk_k, int max_k_blocks, float scale,
+                             h3a_stream_t stream) {
+  clear_error();
+  AttnArgs a;
+  const int rc = prepare_blocksparse(a, q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides,
+                                     o_strides, lut, counts, blk_q, blk_k, max_k_blocks, scale);
+  if (rc) return rc;
   return launch_attn_sparse(a, blk_q, as_stream(stream));
+}
+
+int h3a_attn_fwd_blocksparse_workspace_size(int B, int H, int Sq, int Skv, int D, int blk_q, int blk_k,
+                                            int max_k_blocks, size_t *bytes) {
+  clear_error();
+  if (!bytes) return fail(H3A_ERR_INVALID_ARG, "null output pointer");
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
+  if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
+  if (blk_q != 64 && blk_q != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_q %d unsupported (64 or 128)", blk_q);
+  if (blk_k != 64 && blk_k != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_k %d unsupported (64 or 128)", blk_k);
+  const int64_t nkb = (Skv + blk_k - 1) / blk_k;
+  if (max_k_blocks <= 0 || max_k_blocks > nkb)
+    return fail(H3A_ERR_INVALID_ARG, "max_k_blocks %d outside [1, %lld]", max_k_blocks, (long long)nkb);
+  SplitPlan plan;
+  const int rc = plan_attn_sparse_split(B, H, Sq, blk_q, blk_k, max_k_blocks, &plan);
+  if (rc) return rc;
+  *bytes = plan.bytes;
+  return H3A_OK;
+}
+
+int h3a_attn_fwd_blocksparse_ws(const void *q, const void *k, const void *v, void *o, int B, int H,
+                                int Sq, int Skv, int D, const int64_t q_strides[3],
+                                const int64_t k_strides[3], const int64_t v_strides[3],
+                                const int64_t o_strides[3], const int32_t *lut, const int32_t *counts,
+                                int blk_q, int blk_k, int max_k_blocks, float scale, void *workspace,
+                                size_t workspace_bytes, h3a_stream_t stream) {
+  clear_error();
+  AttnArgs a;
+  int rc = prepare_blocksparse(a, q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides,
+                               lut, counts, blk_q, blk_k, max_k_blocks, scale);
+  if (rc) return rc;
+  SplitPlan plan;
+  rc = plan_attn_sparse_split(B, H, Sq, blk_q, blk_k, max_k_blocks, &plan);
+  if (rc) return rc;
+  if (plan.pieces > 1) {
+    if (!workspace || workspace_bytes < plan.bytes)
+      return fail(H3A_ERR_INVALID_ARG, "workspace of %zu bytes needed, %zu given", plan.bytes,
+                  workspace ? workspace_bytes : (size_t)0);
+    if (!aligned16(workspace)) return fail(H3A_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+  }
+  return launch_attn_sparse_split(a, blk_q, plan, workspace, as_stream(stream));
 }
 
 int h3a_block_map_to_lut(const uint8_t *block_map, int B, int H, int nq, int nk, int32_t *lut,

@@ -947,14 +947,14 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   // a.split_first items are whole query tiles; each later tile is cut into
   // a.split_pieces contiguous ranges of stages, one per workgroup, whose
   // partial results are merged by split_combine_kernel.
-  int w, piece = -1, j0 = 0, niter = nstages;
-  if (kSparse) {
-#if H3A_XCD_REMAP
-    w = xcd_remap(blockIdx.x, a.total);
-#else
-    w = blockIdx.x;
-#endif
-  } else if ((int)blockIdx.x < a.split_first) {
+  // Sparse pairs split the same way, each piece taking the same fraction of
+  // each group's own stage list (split_part).
+  int w, piece = -1, j0 = 0, niter = nstages, split_part = -1;
+  if (kSparse && (int)blockIdx.x >= a.split_first) {
+    piece = blockIdx.x - a.split_first;
+    w = a.split_first + piece / a.split_pieces;
+    split_part = piece % a.split_pieces;
+  } else if (kSparse || (int)blockIdx.x < a.split_first) {
     const int whole = a.split_first < a.total ? a.split_first : a.total;
 #if H3A_XCD_REMAP
     w = xcd_remap(blockIdx.x, whole);
@@ -978,8 +978,9 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   uint16_t *Ob = a.o + b * a.osb + h * a.osh;
   const int qrow = kSparse ? (2 * qt + grp) * 128 + (wave_u & 3) * 32 + l32 : qt * 256 + wave * 32 + l32;
   // Sparse: this group's stage count and LUT row; both groups run the longer
-  // of the two lists.
-  int ngrp = niter;
+  // of the two lists.  A piece of a split pair runs stages [gj0, gj0 + ngrp)
+  // of the group's list.
+  int ngrp = niter, gj0 = 0;
   const int32_t *lut_row = nullptr;
   const int sub_sh = a.sub == 2 ? 1 : 0;
   if constexpr (kSparse) {
@@ -988,9 +989,18 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       const int cnt = a.counts[(int64_t)bh * a.nqt + qb];
       return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
     };
+    auto part_of = [&](int n, int &first) __attribute__((always_inline)) -> int {
+      if (split_part < 0) {
+        first = 0;
+        return n;
+      }
+      first = (int)((int64_t)n * split_part / a.split_pieces);
+      return (int)((int64_t)n * (split_part + 1) / a.split_pieces) - first;
+    };
     const int qb = 2 * qt + grp;
-    ngrp = stages_of(qb);
-    const int nother = stages_of(2 * qt + 1 - grp);
+    int other_j0;
+    ngrp = part_of(stages_of(qb), gj0);
+    const int nother = part_of(stages_of(2 * qt + 1 - grp), other_j0);
     niter = ngrp > nother ? ngrp : nother;
     lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
   }
@@ -1003,14 +1013,14 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       if (ngrp == 0) return -1;
       const __attribute__((address_space(4))) int32_t *row =
           (const __attribute__((address_space(4))) int32_t *)lut_row;
-      return row[(j < ngrp ? j : ngrp - 1) >> sub_sh];
+      return row[(gj0 + (j < ngrp ? j : ngrp - 1)) >> sub_sh];
     } else {
       return 0;
     }
   };
   auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      const int key0 = kb * a.blk_k + (j & (a.sub - 1)) * BN;
+      const int key0 = kb * a.blk_k + ((gj0 + j) & (a.sub - 1)) * BN;
       return (j < ngrp && kb >= 0 && key0 < a.Skv) ? key0 : a.Skv;
     } else {
       return j < niter ? (j0 + j) * BN : a.Skv;
@@ -1018,7 +1028,19 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   };
   auto key_base = [&](int j) __attribute__((always_inline)) -> int { return key_of_entry(j, lut_entry(j)); };
   if (kSparse && niter == 0) {
-    // Neither query block of the pair keeps a key block: O = 0.
+    // Neither query block of the pair keeps a key block (in this piece): O = 0,
+    // or an empty partial result (m = -inf, l = 0, O = 0).
+    if (piece >= 0) {
+      const int row = wave * 32 + l32;
+      float *po = a.ws + ((int64_t)piece * 256 + row) * kD + 4 * g;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) *(float4 *)(po + 8 * c) = float4{0.f, 0.f, 0.f, 0.f};
+      if (g == 0) {
+        float *pml = a.ws + (int64_t)(a.total - a.split_first) * 256 * kD + ((int64_t)piece * 256 + row) * 2;
+        *(float2 *)pml = float2{kNegInf, 0.f};
+      }
+      return;
+    }
     if (qrow < a.Sq) {
       uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
 #pragma unroll
@@ -1369,7 +1391,8 @@ __global__ void __launch_bounds__(256) split_combine_kernel(AttnArgs a) {
   if (item >= (int64_t)ntiles * 256) return;
   const int t = (int)(item / 256), row = (int)(item % 256), d = 4 * (threadIdx.x & 31);
   const int tile = a.split_first + t;
-  const int qt = tile % a.nqt, bh = tile / a.nqt;
+  const int tiles_bh = a.lut ? (a.nqt + 1) / 2 : a.nqt;  // sparse: pairs of 128-row blocks
+  const int qt = tile % tiles_bh, bh = tile / tiles_bh;
   const int h = bh % a.H, b = bh / a.H;
   const int qrow = qt * 256 + row;
   if (qrow >= a.Sq) return;
@@ -1495,8 +1518,7 @@ int launch_attn_dense(AttnArgs a, hipStream_t s) {
 // the chip idles but N for N < CUs).  Those r tiles are cut into P key
 // ranges each, P = CUs / r (at least kMinSplitStages 64-key stages per
 // range), so the last round is ~1/P as long.
-int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
-  constexpr int kMinSplitStages = 4;
+static int device_cu_count(int *cus_out) {
   static std::atomic<int> cu_cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(H3A_ERR_HIP, "hipGetDevice failed");
@@ -1506,11 +1528,20 @@ int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
       return fail(H3A_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
     if (dev >= 0 && dev < 64) cu_cache[dev].store(cus, std::memory_order_relaxed);
   }
-  const int64_t tiles = (int64_t)B * H * ((Sq + 255) / 256);
-  const int stages = (Skv + H3A_DENSE_BN - 1) / H3A_DENSE_BN;
+  *cus_out = cus;
+  return H3A_OK;
+}
+
+// `tiles` 256-row work items of up to `stages` stages each, split when
+// `splittable`.
+static int plan_tiles(int64_t tiles, int stages, bool splittable, SplitPlan *plan) {
+  constexpr int kMinSplitStages = 4;
+  int cus = 0;
+  const int rc = device_cu_count(&cus);
+  if (rc) return rc;
   const int64_t r = tiles >= cus ? tiles % cus : tiles;
   int pieces = 1;
-  if (H3A_DENSE_PINGPONG && r > 0) {
+  if (splittable && r > 0) {
     const int64_t by_cus = cus / r, by_len = stages / kMinSplitStages;
     pieces = (int)(by_cus < by_len ? by_cus : by_len);
   }
@@ -1523,6 +1554,19 @@ int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
   plan->pieces = pieces;
   plan->bytes = (size_t)r * pieces * 256 * (kD + 2) * sizeof(float);
   return H3A_OK;
+}
+
+int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
+  return plan_tiles((int64_t)B * H * ((Sq + 255) / 256), (Skv + H3A_DENSE_BN - 1) / H3A_DENSE_BN,
+                    H3A_DENSE_PINGPONG, plan);
+}
+
+// The longest list a query block can hold (max_k_blocks key blocks) stands in
+// for the stage count.
+int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k_blocks, SplitPlan *plan) {
+  const int64_t nqb = (Sq + blk_q - 1) / blk_q;
+  return plan_tiles((int64_t)B * H * ((nqb + 1) / 2), max_k_blocks * (blk_k / 64),
+                    H3A_SPARSE_PINGPONG && blk_q == 128, plan);
 }
 
 int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s) {
@@ -1540,6 +1584,23 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
   const int64_t rows = (int64_t)(plan.tiles - plan.first) * 256;
   hipLaunchKernelGGL(split_combine_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, a);
   return check_launch("split_combine_kernel");
+}
+
+int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s) {
+  if (plan.pieces < 2) return launch_attn_sparse(a, blk_q, s);
+  AttnArgs p = a;
+  p.split_first = plan.first;
+  p.split_pieces = plan.pieces;
+  p.ws = static_cast<float *>(ws);
+  const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
+  if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
+  p.total = (int)total;
+  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<PadLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
+  int rc = check_launch("attn_fwd_pingpong_kernel<sparse, split>");
+  if (rc) return rc;
+  const int64_t rows = (int64_t)(plan.tiles - plan.first) * 256;
+  hipLaunchKernelGGL(split_combine_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, p);
+  return check_launch("split_combine_kernel<sparse>");
 }
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {

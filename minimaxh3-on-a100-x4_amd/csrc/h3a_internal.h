@@ -57,6 +57,10 @@ int launch_attn_dense(AttnArgs a, hipStream_t s);  // sets nqt/total from its ti
 int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan);
 int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s);
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s);
+// Block-sparse split tail: pairs of 128-row query blocks play the part of
+// the dense tiles (no split for other block heights).
+int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k_blocks, SplitPlan *plan);
+int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s);
 int launch_block_map_to_lut(const uint8_t *map, int B, int H, int nq, int nk, int32_t *lut,
                             int32_t *counts, int max_k_blocks, hipStream_t s);
 int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int S, int blk,

@@ -112,13 +112,26 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | N
     return out
 
 
+def sparse_workspace_bytes(B: int, H: int, Sq: int, Skv: int, blk_q: int, blk_k: int, max_k_blocks: int,
+                           D: int = HEAD_DIM) -> int:
+    """Workspace bytes h3a_attn_fwd_blocksparse_ws needs on the current device (0: no split)."""
+    n = ctypes.c_size_t(0)
+    check("h3a_attn_fwd_blocksparse_workspace_size",
+          lib().h3a_attn_fwd_blocksparse_workspace_size(B, H, Sq, Skv, D, int(blk_q), int(blk_k),
+                                                        int(max_k_blocks), ctypes.byref(n)))
+    return int(n.value)
+
+
 def attn_fwd_blocksparse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lut: torch.Tensor,
                          counts: torch.Tensor, blk_q: int, blk_k: int, scale: float | None = None,
-                         out: torch.Tensor | None = None) -> torch.Tensor:
+                         out: torch.Tensor | None = None, split_tail: bool = True) -> torch.Tensor:
     """Block-sparse attention over the kept key blocks listed in `lut`.
 
     lut: int32 [B,H,ceil(Sq/blk_q),max_k_blocks] ascending key-block indices;
     counts: int32 [B,H,ceil(Sq/blk_q)] number of valid entries per row.
+    split_tail: as for attn_fwd (h3a_attn_fwd_blocksparse_ws with a workspace
+    from torch's allocator); False runs h3a_attn_fwd_blocksparse, which never
+    splits.
     """
     q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
     nqb = -(-Sq // blk_q)
@@ -133,11 +146,19 @@ def attn_fwd_blocksparse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lut:
     lut = lut.contiguous()
     counts = counts.contiguous()
     sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    rc = lib().h3a_attn_fwd_blocksparse(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Skv, D,
-        _bhs(q), _bhs(k), _bhs(v), _bhs(out), lut.data_ptr(), counts.data_ptr(),
-        int(blk_q), int(blk_k), int(lut.shape[3]), sc, _stream(q))
-    check("h3a_attn_fwd_blocksparse", rc)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Skv, D,
+            _bhs(q), _bhs(k), _bhs(v), _bhs(out), lut.data_ptr(), counts.data_ptr(),
+            int(blk_q), int(blk_k), int(lut.shape[3]), sc)
+    with torch.cuda.device(q.device):
+        nbytes = (sparse_workspace_bytes(B, H, Sq, Skv, blk_q, blk_k, int(lut.shape[3]), D)
+                  if split_tail else 0)
+        if nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+            rc = lib().h3a_attn_fwd_blocksparse_ws(*args, ws.data_ptr(), nbytes, _stream(q))
+            check("h3a_attn_fwd_blocksparse_ws", rc)
+        else:
+            rc = lib().h3a_attn_fwd_blocksparse(*args, _stream(q))
+            check("h3a_attn_fwd_blocksparse", rc)
     return out
 
 

@@ -81,6 +81,38 @@ def test_sparse_pairs_uneven_lists(gpu, S, blk_k):
                 assert not got[0, h, 128 * i:128 * (i + 1)].any(), f"empty row h={h} block={i}"
 
 
+@pytest.mark.parametrize("S,blk_k", [(1300, 128), (2000, 64), (640, 64)])
+def test_sparse_split_tail_matches_unsplit(gpu, S, blk_k):
+    """The split-tail path (h3a_attn_fwd_blocksparse_ws): each pair of 128-row query blocks
+    in the last, partly filled round of workgroups is cut into ranges of both blocks'
+    lists, and the combine kernel merges the partial results.  Uneven, empty and unpaired
+    lists, so some pieces hold no stage of one block or of both.  Equal to the oracle and
+    to the unsplit kernel at the attention tolerance; empty rows stay exactly 0."""
+    rng = np.random.default_rng(9100 + S + blk_k)
+    q, k, v = (randn_bf16(rng, (1, 2, S, 128)) for _ in range(3))
+    nq, nk = -(-S // 128), -(-S // blk_k)
+    bmap = np.zeros((1, 2, nq, nk), np.uint8)
+    for h in range(2):
+        for i in range(nq):
+            n = int(rng.integers(0, nk + 1)) if i % 3 else 0
+            bmap[0, h, i, rng.choice(nk, size=n, replace=False)] = 1
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    assert ops.sparse_workspace_bytes(1, 2, S, S, 128, blk_k, lut.shape[3]) > 0, "meant to split"
+    qd, kd, vd = (to_dev_bf16(x, gpu) for x in (q, k, v))
+    o_split = ops.attn_fwd_blocksparse(qd, kd, vd, lut, cnt, 128, blk_k)
+    o_whole = ops.attn_fwd_blocksparse(qd, kd, vd, lut, cnt, 128, blk_k, split_tail=False)
+    got = oracle.bf16_to_f32(from_dev_bf16(o_split)).reshape(o_split.shape)
+    whole = oracle.bf16_to_f32(from_dev_bf16(o_whole)).reshape(o_whole.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=128, blk_k=blk_k)
+    assert_close_absmax(got, ref, what=f"sparse split S={S} blk_k={blk_k} vs oracle")
+    assert_close_absmax(whole, ref, what=f"sparse unsplit S={S} blk_k={blk_k} vs oracle")
+    assert_close_absmax(got, whole, what="sparse split vs unsplit")
+    for h in range(2):
+        for i in range(nq):
+            if not bmap[0, h, i].any():
+                assert not got[0, h, 128 * i:128 * (i + 1)].any(), f"empty row h={h} block={i}"
+
+
 @pytest.mark.parametrize("blk", [64, 128])
 def test_sparse_wide_kv_stride(gpu, blk):
     """K and V as views with a sequence stride just below the 2^24-element limit, so
@@ -112,14 +144,15 @@ def test_sparse_wide_kv_stride(gpu, blk):
 @pytest.mark.parametrize("blk_k", [64, 128])
 def test_all_blocks_kept_equals_dense(gpu, blk_k):
     """A full block map visits the key stages in the dense order: bit-identical output
-    to the unsplit dense kernel (h3a_attn_fwd).  Holds for the default build, whose
-    dense kernel also works in 64-key stages (a 128-key build sums in another order)."""
+    to the unsplit dense kernel (h3a_attn_fwd), both without the split tail.  Holds for
+    the default build, whose dense kernel also works in 64-key stages (a 128-key build
+    sums in another order)."""
     rng = np.random.default_rng(21)
     S = 1000
     q, k, v = (to_dev_bf16(randn_bf16(rng, (1, 2, S, 128)), gpu) for _ in range(3))
     nq, nk = -(-S // 128), -(-S // blk_k)
     lut, cnt = h3attn.block_map_to_lut(torch.ones(1, 2, nq, nk, dtype=torch.uint8, device=gpu))
-    o_s = h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, 128, blk_k)
+    o_s = h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, 128, blk_k, split_tail=False)
     o_d = h3attn.attn_fwd(q, k, v, split_tail=False)
     torch.cuda.synchronize()
     assert torch.equal(o_s, o_d)
@@ -223,8 +256,9 @@ def test_lut_leading_invalid_entry_changes_nothing(gpu, bad):
     cnt_a = torch.full((1, 2, nq), 3, dtype=torch.int32)
     lut_b = torch.tensor([[bad, bad] + row for row in kept], dtype=torch.int32).view(1, 2, nq, 5)
     cnt_b = torch.full((1, 2, nq), 5, dtype=torch.int32)
-    o_a = h3attn.attn_fwd_blocksparse(q, k, v, lut_a.to(gpu), cnt_a.to(gpu), blk, blk)
-    o_b = h3attn.attn_fwd_blocksparse(q, k, v, lut_b.to(gpu), cnt_b.to(gpu), blk, blk)
+    # unsplit: a split tail would cut the two lists (3 and 5 entries) at different places
+    o_a = h3attn.attn_fwd_blocksparse(q, k, v, lut_a.to(gpu), cnt_a.to(gpu), blk, blk, split_tail=False)
+    o_b = h3attn.attn_fwd_blocksparse(q, k, v, lut_b.to(gpu), cnt_b.to(gpu), blk, blk, split_tail=False)
     torch.cuda.synchronize()
     assert torch.equal(o_a, o_b)
 
