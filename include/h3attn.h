@@ -59,6 +59,12 @@ const char *h3a_last_error(void);
  * attn_sm80/fa3_sm80_h3.cu:405-420).  Sq != Skv is allowed (pad path,
  * harness/sp_runtime.py:106-109).  scale > 0 (1/sqrt(128) for the DiT).
  * The seq strides of k and v must be < 2^24 elements (H3A_ERR_UNSUPPORTED).
+ * Range: the softmax runs against a stale reference max that is refreshed
+ * once a stage's p values would exceed 2^16, so the unnormalised fp32 O is
+ * bounded by 2^17 * ceil(Skv/64) * max|v|; results are finite for
+ * max|v| < 2^128 / (2^17 * ceil(Skv/64)), about 3.9e30 at Skv = 42120 (the
+ * reference's max-subtracted softmax, with every p <= 1, stays finite up to
+ * 2^128 / Skv, about 8e33 there).
  * Replaces fa3_sm80_h3_launch (attn_sm80/fa3_sm80_h3.cu:460-470), which
  * ignored B, fixed the scale and launched on the legacy default stream.
  */
@@ -96,8 +102,10 @@ int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o,
  * (key-block indices in units of blk_k keys; nqb = ceil(Sq/blk_q)).
  * Skipped blocks contribute nothing; a query block with no kept key block
  * gets O = 0.  LUT entries that name no key block (negative, or at or past
- * ceil(Skv/blk_k)) are skipped as well.  blk_q in {64,128}; blk_k in
- * {64,128}.  Other arguments as h3a_attn_fwd.
+ * ceil(Skv/blk_k)) are skipped as well.  blk_q and blk_k each in
+ * {64, 128, 192, 256} (multiples of the kernels' 64-key stage; the h3_sla
+ * node's other sizes, custom_nodes/h3_sla/__init__.py:315, give
+ * H3A_ERR_UNSUPPORTED).  Other arguments as h3a_attn_fwd.
  */
 int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o,
                              int B, int H, int Sq, int Skv, int D,
@@ -201,6 +209,30 @@ int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D,
  * (attn_sm80/fa3_sm80_h3.cu:485-512).  Queries the current device.
  */
 int h3a_kernel_attrs(int which, double out[6]);
+
+/*
+ * Phase profile of the dense kernel: the counterpart of the reference's
+ * -DPROFILE build and its get_prof / reset_prof (attn_sm80/fa3_sm80_h3.cu:96-105,
+ * 572-582).  Only the profile build of this library (libh3attn_prof.so, compiled
+ * with H3A_PROFILE=1) records anything.  There, every dense launch of
+ * h3a_attn_fwd / h3a_attn_fwd_ws has its workgroup 0 write, for each of its
+ * H3A_PROF_WAVES waves, H3A_PROF_SLOTS values (row-major [wave][slot]):
+ *   [0] DMA issue (and the loop's branch)  [1] first cluster  [2] mid-stage barrier
+ *   [3] second cluster  [4] DMA wait  [5] end-of-stage barrier  [6] stages run
+ *   [7] whole stage loop  [8] whole stage loop in 100 MHz ticks (s_memrealtime)
+ *   [9] epilogue  [10] prologue  [11] 0
+ * in shader-clock ticks (s_memtime) except [6] and [8]; [0]-[5] sum to [7].
+ * Waves 0-3 run the matrix cluster (QK^T and PV MFMAs) first and the softmax
+ * second, waves 4-7 the other way round.  A later launch overwrites the slots.
+ *   h3a_prof_enabled: 1 in the profile build, 0 otherwise.
+ *   h3a_prof_read:    synchronises the current device, copies the slots to out.
+ *   h3a_prof_reset:   synchronises the current device, zeroes the slots.
+ */
+#define H3A_PROF_WAVES 8
+#define H3A_PROF_SLOTS 12
+int h3a_prof_enabled(void);
+int h3a_prof_read(uint64_t out[H3A_PROF_WAVES * H3A_PROF_SLOTS]);
+int h3a_prof_reset(void);
 
 /*
  * Fragment tests on one wavefront through the same LDS staging and MFMA

@@ -3,6 +3,9 @@
 Same surface as attn_sm80/attn_sm80.py:10-42:
     _build()            -> extension object (fa3, fa3_pp, kernel_attrs, pp_attrs,
                            get_prof, reset_prof, test_qk, test_pv), cached
+    _build(profile=True)-> the same over the phase-profile build (the reference
+                           built a second extension with -DPROFILE for this,
+                           attn_sm80/report_metrics.py:77-80)
     fa3_sm80_h3(q,k,v)  -> O via the hand-written kernel
     sdpa_flash(q,k,v)   -> O via torch SDPA forced to the FLASH backend
     attn(q,k,v,backend) -> dispatch; unknown backend raises ValueError(backend)
@@ -33,11 +36,13 @@ _ext_lock = threading.Lock()
 class _Ext:
     """Object with the reference extension's method names (fa3_sm80_h3.cu:584-593)."""
 
-    @staticmethod
-    def fa3(Q, K, V, O):
+    profile = False
+
+    def fa3(self, Q, K, V, O):
         _ops.attn_fwd(Q, K, V, out=O)
 
-    fa3_pp = fa3  # the reference's pipelined variant; pipelining is internal here
+    def fa3_pp(self, Q, K, V, O):  # the reference's pipelined variant; pipelining is internal here
+        self.fa3(Q, K, V, O)
 
     @staticmethod
     def kernel_attrs():
@@ -45,16 +50,25 @@ class _Ext:
 
     pp_attrs = kernel_attrs
 
-    @staticmethod
-    def get_prof():
-        # The reference fills its phase counters only in -DPROFILE builds and
-        # returns zeros otherwise (fa3_sm80_h3.cu:96-105, 572-582); phase
-        # timing here comes from rocprofv3 instead.
-        return torch.zeros(5, dtype=torch.float64)
+    def get_prof(self):
+        """float64[5]: wait, qk, softmax, pv, epilogue (fa3_sm80_h3.cu:96, 572-577).
 
-    @staticmethod
-    def reset_prof():
-        return None
+        The phase ticks of wave 0 (group A) of workgroup 0 in the last dense
+        launch, in shader-clock ticks summed over its stages: wait = DMA issue,
+        DMA wait and both barriers; qk = the matrix cluster, where the QK^T
+        and PV MFMAs are interleaved (so pv is 0: it is inside qk); softmax =
+        the softmax cluster; epilogue = normalise and store.  Only the profile
+        build records them; the product build returns zeros, as the
+        reference's non-PROFILE build does.
+        """
+        if not self.profile:
+            return torch.zeros(5, dtype=torch.float64)
+        w0 = _ops.prof_read(profile=True)[0]
+        return torch.tensor([w0[0] + w0[2] + w0[4] + w0[5], w0[1], w0[3], 0, w0[9]], dtype=torch.float64)
+
+    def reset_prof(self):
+        if self.profile:
+            _ops.prof_reset(profile=True)
 
     @staticmethod
     def test_qk(Q, K, S):
@@ -73,15 +87,35 @@ class _Ext:
         O.copy_(_ops.test_pv(Pp, V)[:r])
 
 
-def _build():
-    """Return the (prebuilt) kernel extension; raises if libh3attn.so is missing."""
-    global _ext
-    if _ext is None:
-        with _ext_lock:
-            if _ext is None:
-                _lib.lib()  # loads or raises: no silent fallback
-                _ext = _Ext()
-    return _ext
+class _ProfExt(_Ext):
+    """The extension over libh3attn_prof.so: fa3 runs the unsplit dense kernel of the
+    profile build, and get_prof / reset_prof read and clear its phase ticks."""
+
+    profile = True
+
+    def fa3(self, Q, K, V, O):
+        _ops.attn_fwd_profiled(Q, K, V, out=O)
+
+
+_prof_ext = None
+
+
+def _build(profile: bool = False):
+    """Return the (prebuilt) kernel extension; raises if its library is missing.
+
+    profile=True returns the phase-profile build's extension instead.
+    """
+    global _ext, _prof_ext
+    with _ext_lock:
+        if profile:
+            if _prof_ext is None:
+                _lib.lib(profile=True)  # loads or raises: no silent fallback
+                _prof_ext = _ProfExt()
+            return _prof_ext
+        if _ext is None:
+            _lib.lib()
+            _ext = _Ext()
+        return _ext
 
 
 def fa3_sm80_h3(q, k, v):
@@ -90,8 +124,12 @@ def fa3_sm80_h3(q, k, v):
 
 
 def sdpa_flash(q, k, v):
-    with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
-        return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=False)
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=False)
+    except RuntimeError as e:
+        raise RuntimeError(f"sdpa_flash: torch's FLASH_ATTENTION SDPA backend cannot run these inputs "
+                           f"on this build/device ({e})") from e
 
 
 def sdpa(q, k, v):

@@ -1,6 +1,7 @@
 """Build libh3attn.so (gfx950) in-tree from csrc/*.hip with hipcc.
 
-Usage: python build_lib.py [--verbose]
+Usage: python build_lib.py [--verbose] [--profile] [-DKNOB=VALUE ...] [--out=PATH]
+  --profile builds the phase-profile library h3attn/libh3attn_prof.so as well.
 
 The library lands next to the Python package (h3attn/libh3attn.so) so it
 travels with the source tree.  Every call rebuilds: compile each translation
@@ -20,6 +21,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT_DIR = os.path.join(HERE, "h3attn")
 LIB_NAME = "libh3attn.so"
+# The phase-profile build (H3A_PROFILE=1) of the same sources.
+PROF_LIB_OUT = os.path.join(OUT_DIR, "libh3attn_prof.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 
 ARCH = "gfx950"
@@ -83,3 +86,5 @@ if __name__ == "__main__":
     defs = [a[2:] for a in args if a.startswith("-D")]
     outp = next((a.split("=", 1)[1] for a in args if a.startswith("--out=")), None)
     print(build(verbose="--verbose" in args, defines=defs, out=outp))
+    if "--profile" in args:
+        print(build(verbose="--verbose" in args, defines=defs + ["H3A_PROFILE=1"], out=PROF_LIB_OUT))

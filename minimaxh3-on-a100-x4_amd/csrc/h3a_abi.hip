@@ -8,6 +8,12 @@
 
 #include "h3a_internal.h"
 
+#ifdef H3A_PROFILE
+#define H3A_PROFILE_BUILD (H3A_PROFILE != 0)
+#else
+#define H3A_PROFILE_BUILD 0
+#endif
+
 namespace h3a {
 
 static thread_local char g_err[512] = "";
@@ -76,6 +82,7 @@ void fill_attn_args(AttnArgs &a, const void *q, const void *k, const void *v, vo
   a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv;
   a.sl2 = scale * 1.4426950408889634f;
   a.lut = nullptr; a.counts = nullptr; a.lut_stride = 0; a.sub = 1; a.blk_k = 64;
+  a.nkb = 0; a.nqb = 0; a.qmul = 1;
   a.split_first = INT_MAX; a.split_pieces = 1; a.ws = nullptr;
 }
 
@@ -138,6 +145,12 @@ int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o, int B,
 
 namespace {
 
+int check_blocks(int blk_q, int blk_k) {
+  if (!sparse_block_ok(blk_q)) return fail(H3A_ERR_UNSUPPORTED, "blk_q %d unsupported (64, 128, 192 or 256)", blk_q);
+  if (!sparse_block_ok(blk_k)) return fail(H3A_ERR_UNSUPPORTED, "blk_k %d unsupported (64, 128, 192 or 256)", blk_k);
+  return H3A_OK;
+}
+
 // Checks shared by the block-sparse entry points; fills `a` on success.
 int prepare_blocksparse(AttnArgs &a, const void *q, const void *k, const void *v, void *o, int B, int H,
                         int Sq, int Skv, int D, const int64_t q_strides[3], const int64_t k_strides[3],
@@ -146,22 +159,26 @@ int prepare_blocksparse(AttnArgs &a, const void *q, const void *k, const void *v
   int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
   if (rc) return rc;
   if (!lut || !counts) return fail(H3A_ERR_INVALID_ARG, "null lut/counts pointer");
-  if (blk_q != 64 && blk_q != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_q %d unsupported (64 or 128)", blk_q);
-  if (blk_k != 64 && blk_k != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_k %d unsupported (64 or 128)", blk_k);
+  rc = check_blocks(blk_q, blk_k);
+  if (rc) return rc;
   const int64_t nkb = (Skv + blk_k - 1) / blk_k;
   if (max_k_blocks <= 0 || max_k_blocks > nkb)
     return fail(H3A_ERR_INVALID_ARG, "max_k_blocks %d outside [1, %lld]", max_k_blocks, (long long)nkb);
-  const int64_t nqt = (Sq + blk_q - 1) / blk_q;
-  const int64_t total = (int64_t)B * H * nqt;
+  const int rows = sparse_sub_block_rows(blk_q);
+  const int64_t nsub = (Sq + rows - 1) / rows;
+  const int64_t total = (int64_t)B * H * nsub;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
   fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
-  a.nqt = (int)nqt;
+  a.nqt = (int)nsub;
   a.total = (int)total;
   a.lut = lut;
   a.counts = counts;
   a.lut_stride = max_k_blocks;
   a.blk_k = blk_k;
   a.sub = blk_k / 64;
+  a.nkb = (int)nkb;
+  a.nqb = (int)((Sq + blk_q - 1) / blk_q);
+  a.qmul = blk_q / rows;
   return H3A_OK;
 }
 
@@ -188,13 +205,13 @@ int h3a_attn_fwd_blocksparse_workspace_size(int B, int H, int Sq, int Skv, int D
   if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0)
     return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
   if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
-  if (blk_q != 64 && blk_q != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_q %d unsupported (64 or 128)", blk_q);
-  if (blk_k != 64 && blk_k != 128) return fail(H3A_ERR_UNSUPPORTED, "blk_k %d unsupported (64 or 128)", blk_k);
+  int rc = check_blocks(blk_q, blk_k);
+  if (rc) return rc;
   const int64_t nkb = (Skv + blk_k - 1) / blk_k;
   if (max_k_blocks <= 0 || max_k_blocks > nkb)
     return fail(H3A_ERR_INVALID_ARG, "max_k_blocks %d outside [1, %lld]", max_k_blocks, (long long)nkb);
   SplitPlan plan;
-  const int rc = plan_attn_sparse_split(B, H, Sq, blk_q, blk_k, max_k_blocks, &plan);
+  rc = plan_attn_sparse_split(B, H, Sq, blk_q, blk_k, max_k_blocks, &plan);
   if (rc) return rc;
   *bytes = plan.bytes;
   return H3A_OK;
@@ -311,6 +328,19 @@ int h3a_kernel_attrs(int which, double out[6]) {
   if (which < H3A_KERNEL_ATTN_DENSE || which > H3A_KERNEL_ATTN_SPARSE_64)
     return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
   return attn_kernel_attrs(which, out);
+}
+
+int h3a_prof_enabled(void) { return H3A_PROFILE_BUILD; }
+
+int h3a_prof_read(uint64_t out[H3A_PROF_WAVES * H3A_PROF_SLOTS]) {
+  clear_error();
+  if (!out) return fail(H3A_ERR_INVALID_ARG, "null output array");
+  return attn_prof_read(out);
+}
+
+int h3a_prof_reset(void) {
+  clear_error();
+  return attn_prof_reset();
 }
 
 int h3a_test_qk(const void *Q, const void *K, float *S, h3a_stream_t stream) {

@@ -47,6 +47,7 @@
 
 #include "h3a_device.h"
 #include "h3a_internal.h"
+#include "h3a_lut.h"
 
 namespace h3a {
 
@@ -153,10 +154,25 @@ namespace h3a {
 #define H3A_ROWSUM_BF16 0
 #endif
 
+// Phase profile build (libh3attn_prof.so): the dense ping-pong kernel stamps
+// the shader clock at its cluster boundaries (see PhaseClock).
+#ifndef H3A_PROFILE
+#define H3A_PROFILE 0
+#endif
+
 constexpr int kD = 128;
 constexpr int kBN = 64;               // keys per pipeline stage
 constexpr float kRescaleSlack = 8.f;  // log2 headroom before the running max is refreshed
-constexpr float kStaleSumLimit = 0x1p64f;  // largest stage p sum accepted without a refresh
+// Largest stage p sum (per lane: 32 keys of one query row) accepted without a
+// refresh of the stale reference max.  Every p of a stage is then <= 2^16, so
+// a row's unnormalised O is bounded by 2 * 2^16 * ceil(Skv/64) * max|v|: it
+// stays finite for max|v| < 2^128 / (2^17 * ceil(Skv/64)), about 3.9e30 at
+// Skv = 42120 (a max-subtracted softmax with p <= 1 allows up to ~8e33 there).
+constexpr float kStaleSumLimit = 0x1p16f;
+
+__device__ __forceinline__ int stage_key0(const AttnArgs &a, int t, int kb) {
+  return lut_stage_key0(t, kb, a.nkb, a.blk_k, a.sub, a.Skv);
+}
 
 // ---------------------------------------------------------------------------
 // LDS layouts of a 64-key K or V stage.  A layout fixes the row pitch, which
@@ -551,7 +567,9 @@ attn_fwd_kernel(AttnArgs a) {
   int niter;
   const int32_t *lut_row = nullptr;
   if constexpr (kSparse) {
-    const int64_t row = (int64_t)bh * a.nqt + qt;
+    // A LUT row serves a.qmul consecutive query sub-blocks (blk_q = 192:
+    // three 64-row sub-blocks; blk_q = 256 with 128-row sub-blocks: two).
+    const int64_t row = (int64_t)bh * a.nqb + qt / a.qmul;
     const int cnt = a.counts[row];
     niter = (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
     lut_row = a.lut + row * a.lut_stride;
@@ -559,23 +577,21 @@ attn_fwd_kernel(AttnArgs a) {
     niter = (a.Skv + kBN - 1) / kBN;
   }
   // First key of stage j, from its LUT entry kb (block-sparse; a key block
-  // of a.sub = 1 or 2 stages).  Prefetches past the last stage and LUT entries
+  // of a.sub = 1..4 stages).  Prefetches past the last stage and LUT entries
   // outside the key range map to Skv: such a stage loads nothing (zeros).
   // Both are branch-free, so that the scalar work can be scheduled among
   // the stage's MFMA and VALU instructions: the entry is loaded at a clamped
   // index (niter >= 1 here) and discarded past the row's last stage.
-  const int sub_sh = a.sub == 2 ? 1 : 0;
   auto lut_entry = [&](int j) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      return lut_row[(j < niter ? j : niter - 1) >> sub_sh];
+      return lut_row[block_of_stage(j < niter ? j : niter - 1, a.sub)];
     } else {
       return 0;
     }
   };
   auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      const int key0 = kb * a.blk_k + (j & (a.sub - 1)) * kBN;
-      return (j < niter && kb >= 0 && key0 < a.Skv) ? key0 : a.Skv;
+      return j < niter ? stage_key0(a, j, kb) : a.Skv;
     } else {
       return j < niter ? j * kBN : a.Skv;
     }
@@ -870,6 +886,74 @@ __device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0,
   lsum += ps;
 }
 
+// Phase profile of the dense ping-pong kernel (H3A_PROFILE builds; every
+// method compiles to nothing otherwise).  Workgroup 0's 8 waves each sum
+// s_memtime ticks (the shader clock) per phase of their stage loop, in
+// registers, and store them once after the loop, one row per wave:
+//   [0] DMA issue, and the loop's own branch   [1] first cluster
+//   [2] mid-stage barrier                       [3] second cluster
+//   [4] wait for the DMA (vmcnt)                [5] end-of-stage barrier
+//   [6] stages run                              [7] loop, s_memtime ticks
+//   [8] loop, s_memrealtime ticks (100 MHz)     [9] epilogue (normalise, store)
+//   [10] prologue (kernel start to loop start)
+// Group A's first cluster is its matrix cluster (QK^T and PV MFMAs, which are
+// interleaved and cannot be timed apart) and its second the softmax; group B
+// the other way round.  Phases [0]-[5] tile the loop: their sum is [7].
+constexpr int kProfSlots = H3A_PROF_SLOTS;
+static_assert(H3A_PROF_WAVES == 8, "one row per wave of the dense workgroup");
+__device__ unsigned long long g_prof[H3A_PROF_WAVES][kProfSlots];
+
+struct PhaseClock {
+  uint32_t ph[kProfSlots];  // a phase sums < 2^32 ticks for any stage count here
+  uint64_t last, t_loop, rt_loop;
+  bool on;
+  __device__ __forceinline__ void begin(bool enabled) {
+    if constexpr (H3A_PROFILE) {
+      on = enabled;
+#pragma unroll
+      for (int i = 0; i < kProfSlots; ++i) ph[i] = 0;  // [7]-[10] are assigned, not summed
+      last = __builtin_amdgcn_s_memtime();
+    }
+  }
+  // Ticks since the previous mark go to phase i.
+  __device__ __forceinline__ void mark(int i) {
+    if constexpr (H3A_PROFILE) {
+      const uint64_t t = __builtin_amdgcn_s_memtime();
+      ph[i] += (uint32_t)(t - last);
+      last = t;
+    }
+  }
+  __device__ __forceinline__ void loop_begin() {
+    if constexpr (H3A_PROFILE) {
+      t_loop = __builtin_amdgcn_s_memtime();
+      ph[10] = (uint32_t)(t_loop - last);
+      last = t_loop;
+      rt_loop = __builtin_amdgcn_s_memrealtime();
+    }
+  }
+  __device__ __forceinline__ void stage_done() {
+    if constexpr (H3A_PROFILE) ph[6] += 1;
+  }
+  __device__ __forceinline__ void loop_end() {
+    if constexpr (H3A_PROFILE) {
+      ph[7] = (uint32_t)(last - t_loop);
+      ph[8] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - rt_loop);
+      last = __builtin_amdgcn_s_memtime();
+    }
+  }
+  // After the epilogue's stores: phase 9, then one row per wave to g_prof.
+  __device__ __forceinline__ void finish(int wave, int lane) {
+    if constexpr (H3A_PROFILE) {
+      if (on) {
+        ph[9] = (uint32_t)(__builtin_amdgcn_s_memtime() - last);
+        if (lane == 0)
+#pragma unroll
+          for (int i = 0; i < kProfSlots; ++i) g_prof[wave][i] = ph[i];
+      }
+    }
+  }
+};
+
 // Pin values to this point of the program: an empty volatile asm that reads
 // and rewrites them.  Everything they depend on must be computed before it,
 // and volatile asm keeps its place relative to the workgroup barriers.  Without
@@ -935,6 +1019,8 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[NG][2][kKE];
   __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[NG][2][kVE];
 
+  PhaseClock pc;
+  pc.begin(!kSparse && blockIdx.x == 0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -982,11 +1068,12 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   // of the group's list.
   int ngrp = niter, gj0 = 0;
   const int32_t *lut_row = nullptr;
-  const int sub_sh = a.sub == 2 ? 1 : 0;
   if constexpr (kSparse) {
+    // 128-row query sub-block qb reads LUT row qb / a.qmul (blk_q = 256: the
+    // two blocks of a pair share one row).
     auto stages_of = [&](int qb) __attribute__((always_inline)) -> int {
       if (qb >= a.nqt) return 0;
-      const int cnt = a.counts[(int64_t)bh * a.nqt + qb];
+      const int cnt = a.counts[(int64_t)bh * a.nqb + qb / a.qmul];
       return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
     };
     auto part_of = [&](int n, int &first) __attribute__((always_inline)) -> int {
@@ -1002,7 +1089,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     ngrp = part_of(stages_of(qb), gj0);
     const int nother = part_of(stages_of(2 * qt + 1 - grp), other_j0);
     niter = ngrp > nother ? ngrp : nother;
-    lut_row = a.lut + ((int64_t)bh * a.nqt + (qb < a.nqt ? qb : 0)) * a.lut_stride;
+    lut_row = a.lut + ((int64_t)bh * a.nqb + (qb < a.nqt ? qb : 0) / a.qmul) * a.lut_stride;
   }
   // Sparse: LUT entry of local stage j (a key block of a.sub stages; read
   // through the constant address space, so it is a scalar load), and the
@@ -1013,15 +1100,14 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       if (ngrp == 0) return -1;
       const __attribute__((address_space(4))) int32_t *row =
           (const __attribute__((address_space(4))) int32_t *)lut_row;
-      return row[(gj0 + (j < ngrp ? j : ngrp - 1)) >> sub_sh];
+      return row[block_of_stage(gj0 + (j < ngrp ? j : ngrp - 1), a.sub)];
     } else {
       return 0;
     }
   };
   auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      const int key0 = kb * a.blk_k + ((gj0 + j) & (a.sub - 1)) * BN;
-      return (j < ngrp && kb >= 0 && key0 < a.Skv) ? key0 : a.Skv;
+      return j < ngrp ? stage_key0(a, gj0 + j, kb) : a.Skv;
     } else {
       return j < niter ? (j0 + j) * BN : a.Skv;
     }
@@ -1261,6 +1347,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(0);
   };
 
+  pc.loop_begin();
   if (lead) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
       if constexpr (kSparse) {
@@ -1284,15 +1371,22 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         return;
       }
       if constexpr (!kALate) dma(par, j);
+      pc.mark(0);
       mfma(par);
       if constexpr (kALate) {
         __builtin_amdgcn_sched_barrier(0);
         dma(par, j);
       }
+      pc.mark(1);
       mid_barrier();
+      pc.mark(2);
       if (j + 1 < niter) soft(j);
+      pc.mark(3);
       wait_vmem_all();
+      pc.mark(4);
       slot_barrier();
+      pc.mark(5);
+      pc.stage_done();
     };
     for (int j = 0; j < niter; j += 2) {
       stage(std::integral_constant<int, 0>{}, j);
@@ -1325,11 +1419,18 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         return;
       }
       dma(par, j);
+      pc.mark(0);
       if constexpr (!decltype(first)::value) soft(j - 1);
+      pc.mark(1);
       mid_barrier();
+      pc.mark(2);
       mfma(par);
+      pc.mark(3);
       wait_vmem_all();
+      pc.mark(4);
       slot_barrier();
+      pc.mark(5);
+      pc.stage_done();
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -1344,6 +1445,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       if (j + 1 < niter) stage(C0{}, j + 1, std::false_type{});
     }
   }
+  pc.loop_end();
   // Sparse, loads inside the matrix cluster: group B's last stage issued
   // loads (of nothing: keys past its list) that no stage writes out.
   if constexpr (kSparse) wait_vmem_all();
@@ -1365,6 +1467,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       float *pml = a.ws + (int64_t)(a.total - a.split_first) * 256 * kD + ((int64_t)piece * 256 + row) * 2;
       *(float2 *)pml = float2{m, ltot};
     }
+    pc.finish(wave, lane);
     return;
   }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
@@ -1380,6 +1483,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       }
     }
   }
+  pc.finish(wave, lane);
 }
 
 // Merge the key-range pieces of the split tiles:
@@ -1493,7 +1597,11 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 // ---------------------------------------------------------------------------
 using DenseLayout = std::conditional_t<H3A_DENSE_LAYOUT == 1, PadLayout, SwzLayout>;
 constexpr int kDenseSub = H3A_DENSE_BN / 32;
-static_assert(kDenseSub == 2 || kDenseSub == 4, "dense stages of 64 or 128 keys");
+// 128-key dense stages (H3A_DENSE_BN=128) measured 22 % slower, and one
+// build of them gave wrong output when the compiler made the softmax lambda an
+// out-of-line call; that cause was never shown from the code, so the variant
+// does not build.
+static_assert(kDenseSub == 2, "dense stages are 64 keys (H3A_DENSE_BN=64)");
 
 int launch_attn_dense(AttnArgs a, hipStream_t s) {
 #if H3A_DENSE_PINGPONG
@@ -1564,9 +1672,10 @@ int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
 // The longest list a query block can hold (max_k_blocks key blocks) stands in
 // for the stage count.
 int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k_blocks, SplitPlan *plan) {
-  const int64_t nqb = (Sq + blk_q - 1) / blk_q;
-  return plan_tiles((int64_t)B * H * ((nqb + 1) / 2), max_k_blocks * (blk_k / 64),
-                    H3A_SPARSE_PINGPONG && blk_q == 128, plan);
+  const int rows = sparse_sub_block_rows(blk_q);
+  const int64_t nsub = (Sq + rows - 1) / rows;
+  return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_k_blocks * (blk_k / 64),
+                    H3A_SPARSE_PINGPONG && rows == 128, plan);
 }
 
 int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s) {
@@ -1588,6 +1697,7 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
 
 int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s) {
   if (plan.pieces < 2) return launch_attn_sparse(a, blk_q, s);
+  if (sparse_sub_block_rows(blk_q) != 128) return fail(H3A_ERR_INVALID_ARG, "split plan for 64-row query blocks");
   AttnArgs p = a;
   p.split_first = plan.first;
   p.split_pieces = plan.pieces;
@@ -1604,7 +1714,8 @@ int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan
 }
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
-  if (H3A_SPARSE_PINGPONG && blk_q == 128) {
+  const int rows = sparse_sub_block_rows(blk_q);
+  if (H3A_SPARSE_PINGPONG && rows == 128) {
     AttnArgs p = a;
     const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
     if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
@@ -1612,7 +1723,7 @@ int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
     hipLaunchKernelGGL((attn_fwd_pingpong_kernel<PadLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
     return check_launch("attn_fwd_pingpong_kernel<sparse>");
   }
-  if (blk_q == 128) {
+  if (rows == 128) {
     hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(256), 0, s, a);
   } else if (H3A_SPARSE64_KEYSPLIT) {
     hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true, true>), dim3(a.total), dim3(256), 0,
@@ -1659,6 +1770,23 @@ static int fill_attrs(const void *fn, int threads, double out[6]) {
   out[3] = clk;
   out[4] = max_threads > 0 ? (double)(blocks * threads) / max_threads : 0.0;
   out[5] = threads;
+  return H3A_OK;
+}
+
+// Phase profile readout (profile build; zeros otherwise).  Synchronises the
+// device first, as the reference's cudaMemcpyFromSymbol did implicitly.
+int attn_prof_read(uint64_t *out) {
+  if (hipDeviceSynchronize() != hipSuccess) return fail(H3A_ERR_HIP, "hipDeviceSynchronize failed");
+  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prof), sizeof(g_prof), 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(H3A_ERR_HIP, "hipMemcpyFromSymbol(g_prof) failed");
+  return H3A_OK;
+}
+
+int attn_prof_reset() {
+  static const unsigned long long zeros[H3A_PROF_WAVES][kProfSlots] = {};
+  if (hipDeviceSynchronize() != hipSuccess) return fail(H3A_ERR_HIP, "hipDeviceSynchronize failed");
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_prof), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice) != hipSuccess)
+    return fail(H3A_ERR_HIP, "hipMemcpyToSymbol(g_prof) failed");
   return H3A_OK;
 }
 

@@ -28,21 +28,31 @@ struct AttnArgs {
   int64_t vsb, vsh, vss;
   int64_t osb, osh, oss;
   int B, H, Sq, Skv;
-  int nqt;    // query tiles per (b,h)
+  int nqt;    // query tiles per (b,h) (block-sparse: query sub-blocks of 64 or 128 rows)
   int total;  // B*H*nqt workgroups
   float sl2;  // softmax scale * log2(e)
   // block-sparse only
   const int32_t *lut;
   const int32_t *counts;
   int lut_stride;  // max_k_blocks
-  int sub;         // 64-key stages per key block (blk_k / 64)
+  int sub;         // 64-key stages per key block (blk_k / 64: 1..4)
   int blk_k;
+  int nkb;         // key blocks, ceil(Skv / blk_k): LUT entries outside [0, nkb) name none
+  int nqb;         // LUT rows per (b,h), ceil(Sq / blk_q)
+  int qmul;        // query sub-blocks per LUT row (blk_q / sub-block height: 1..3)
   // dense split tail (see launch_attn_dense): work items >= split_first are
   // cut into split_pieces key ranges whose partial results go to ws
   int split_first;
   int split_pieces;
   float *ws;
 };
+
+// Block sizes of the block-sparse path: multiples of the 64-key stage up to
+// 256.  Query blocks run as sub-blocks of 128 rows (blk_q 128, 256: the pairs
+// kernel) or 64 rows (blk_q 64, 192: the key-split kernel); a key block is
+// blk_k / 64 stages.
+inline bool sparse_block_ok(int blk) { return blk == 64 || blk == 128 || blk == 192 || blk == 256; }
+inline int sparse_sub_block_rows(int blk_q) { return blk_q % 128 == 0 ? 128 : 64; }
 
 // Dense split-tail plan for a problem on the current device.
 struct SplitPlan {
@@ -71,6 +81,8 @@ int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, 
 int launch_test_qk(const uint16_t *Q, const uint16_t *K, float *S, hipStream_t s);
 int launch_test_pv(const uint16_t *P, const uint16_t *V, float *O, hipStream_t s);
 int attn_kernel_attrs(int which, double out[6]);
+int attn_prof_read(uint64_t *out);  // H3A_PROF_WAVES x H3A_PROF_SLOTS
+int attn_prof_reset();
 
 struct RopeArgs {
   uint16_t *q, *k;

@@ -14,6 +14,9 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("H3ATTN_LIB", os.path.join(_HERE, "libh3attn.so"))
+# The phase-profile build of the same sources (H3A_PROFILE=1): its dense kernel
+# stamps the shader clock at cluster boundaries (h3a_prof_read).
+PROF_LIB_PATH = os.path.join(_HERE, "libh3attn_prof.so")
 
 H3A_OK = 0
 H3A_ERR_INVALID_ARG = 1
@@ -55,12 +58,15 @@ SIGNATURES = {
     "h3a_block_pool": (_i, [_vp, _i, _i, _i, _i, _c_i64_3, _i, _vp, _vp]),
     "h3a_block_select": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp]),
     "h3a_kernel_attrs": (_i, [_i, ctypes.POINTER(ctypes.c_double)]),
+    "h3a_prof_enabled": (_i, []),
+    "h3a_prof_read": (_i, [ctypes.POINTER(ctypes.c_uint64)]),
+    "h3a_prof_reset": (_i, []),
     "h3a_test_qk": (_i, [_vp, _vp, _vp, _vp]),
     "h3a_test_pv": (_i, [_vp, _vp, _vp, _vp]),
 }
 
 _lock = threading.Lock()
-_lib = None
+_handles: dict = {}
 
 
 class H3AError(RuntimeError):
@@ -71,29 +77,30 @@ class H3AError(RuntimeError):
         self.code = code
 
 
-def lib() -> ctypes.CDLL:
-    """Load (once) and return the library; raise if it is not built."""
-    global _lib
-    if _lib is not None:
-        return _lib
+def lib(profile: bool = False) -> ctypes.CDLL:
+    """Load (once) and return the library (profile=True: its phase-profile build); raise if not built."""
+    path = PROF_LIB_PATH if profile else LIB_PATH
+    handle = _handles.get(path)
+    if handle is not None:
+        return handle
     with _lock:
-        if _lib is None:
-            if not os.path.exists(LIB_PATH):
+        if path not in _handles:
+            if not os.path.exists(path):
                 raise RuntimeError(
-                    f"libh3attn.so not found at {LIB_PATH}; build it first "
+                    f"{os.path.basename(path)} not found at {path}; build it first "
                     "(python __graft_entry__.py build, or build_lib.py)")
-            handle = ctypes.CDLL(LIB_PATH)
+            h = ctypes.CDLL(path)
             for name, (res, args) in SIGNATURES.items():
-                fn = getattr(handle, name)
+                fn = getattr(h, name)
                 fn.restype = res
                 fn.argtypes = args
-            _lib = handle
-    return _lib
+            _handles[path] = h
+    return _handles[path]
 
 
-def check(fn: str, rc: int) -> None:
+def check(fn: str, rc: int, handle: ctypes.CDLL | None = None) -> None:
     if rc != H3A_OK:
-        msg = lib().h3a_last_error().decode(errors="replace")
+        msg = (handle or lib()).h3a_last_error().decode(errors="replace")
         if rc in (H3A_ERR_INVALID_ARG, H3A_ERR_UNSUPPORTED, H3A_ERR_ALIGNMENT):
             raise ValueError(f"{fn}: {msg} (code {rc})")
         raise H3AError(fn, rc, msg)

@@ -24,6 +24,7 @@ is written directly in the [S, H*D] layout out_proj consumes.
 """
 from __future__ import annotations
 
+import os
 import threading
 from typing import Callable
 
@@ -112,25 +113,65 @@ def in_dit_scope() -> bool:
 
 
 class Schedule:
-    """Per-layer keep ratios (custom_nodes/h3_sla/__init__.py:139-212, without the status file)."""
+    """Per-layer keep ratios (custom_nodes/h3_sla/__init__.py:139-212, without the status file).
 
-    def __init__(self, name: str, keeps, blk: int = 64, force_diag: bool = False, smooth_k: bool = True):
-        self.name, self.keeps, self.blk = name, list(keeps), int(blk)
+    blk is checked here, when the schedule is built, as the node checks its
+    kernel when it patches the model (h3_sla:331): an unsupported size raises
+    ValueError instead of turning every sparse layer into a dense one later.
+    timing (default: env H3_SLA_TIMING == "1", as at h3_sla:147) records HIP
+    events around each sparse layer; they are resolved at the last layer of a
+    step (h3_sla:199-212) into attn_ms / attn_n per layer.
+    """
+
+    def __init__(self, name: str, keeps, blk: int = 64, force_diag: bool = False, smooth_k: bool = True,
+                 timing: bool | None = None):
+        self.name, self.keeps, self.blk = name, [float(x) for x in keeps], sla.check_block(blk)
         self.force_diag, self.smooth_k = force_diag, smooth_k
         self.default_keep = max(set(self.keeps), key=self.keeps.count) if self.keeps else 1.0
+        self.summary = sla.schedule_summary(name, self.keeps, self.blk) if self.keeps else None
+        self.timing = (os.environ.get("H3_SLA_TIMING") == "1") if timing is None else bool(timing)
+        self._ev = []
+        self.attn_ms = [0.0] * len(self.keeps)
+        self.attn_n = [0] * len(self.keeps)
 
     def keep_for(self, layer):
         if layer is None or not (0 <= layer < len(self.keeps)):
             return self.default_keep
         return self.keeps[layer]
 
+    def flush_timing(self) -> None:
+        """Resolve the recorded events into attn_ms / attn_n (synchronises on the last one)."""
+        if not self._ev:
+            return
+        self._ev[-1][2].synchronize()
+        for layer, a, b in self._ev:
+            self.attn_ms[layer] += a.elapsed_time(b)
+            self.attn_n[layer] += 1
+        self._ev = []
+
+    def attn_ms_per_layer_call(self):
+        """Mean sparse-attention ms per call for each layer (None where it never ran)."""
+        return [round(m / n, 3) if n else None for m, n in zip(self.attn_ms, self.attn_n)]
+
+    def _sparse(self, q, k, v, keep):
+        return sla.sparse_attention(q, k, v, keep, self.blk, force_diag=self.force_diag, smooth_k=self.smooth_k)
+
     def run(self, layer, q, k, v, transformer_options=None):
         """[1,H,S,D] sparse output, or None (keep >= 1: caller runs dense)."""
         keep = self.keep_for(layer)
         if keep >= 1.0:
             return None
-        return sla.sparse_attention(q, k, v, keep, self.blk, force_diag=self.force_diag,
-                                    smooth_k=self.smooth_k)
+        if self.timing and layer is not None and 0 <= layer < len(self.keeps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            o = self._sparse(q, k, v, keep)
+            b.record()
+            self._ev.append((layer, a, b))
+            if layer == len(self.keeps) - 1:  # end of a denoise step
+                self.flush_timing()
+            return o
+        return self._sparse(q, k, v, keep)
 
 
 def make_sla_override(topk: float = 0.35, blk: int = 64, schedule: Schedule | None = None,
@@ -139,7 +180,10 @@ def make_sla_override(topk: float = 0.35, blk: int = 64, schedule: Schedule | No
 
     Active only inside DiT-block attention (install_scope_patch) with mask=None
     and head_dim 128; returns [1,S,H*D]; any exception falls back to `func`.
+    The block size is checked here (ValueError), not at the first call.
     """
+    blk = sla.check_block(blk)
+
     def override(func, *args, **kwargs):
         try:
             if in_dit_scope() and _gate(args, kwargs):
@@ -244,18 +288,41 @@ def uninstall(attention_cls=None) -> bool:
 def install_optimized_attention(module=None) -> bool:
     """Replace module.optimized_attention (as h3_profiler does, custom_nodes/h3_profiler/__init__.py:35,76)
     with a version that runs libh3attn for mask-free head_dim-128 bf16 calls and
-    defers to the original otherwise.  Idempotent."""
+    defers to the original otherwise.  A transformer_options override (the
+    h3_sla sparse path) still receives every call first.  Idempotent."""
     if module is None:
         import comfy.ldm.minimax.model as module
     orig = module.optimized_attention
     if getattr(orig, "_h3attn_patched", False):
         return False
 
-    def optimized_attention(q, k, v, heads, mask=None, *a, **kw):
+    def without_override(kw):
+        opts = kw.get("transformer_options")
+        if isinstance(opts, dict) and "optimized_attention_override" in opts:
+            kw = dict(kw)
+            kw["transformer_options"] = {n: x for n, x in opts.items() if n != "optimized_attention_override"}
+        return kw
+
+    def attention(q, k, v, heads, mask=None, *a, **kw):
         dim_ok = (q.shape[-1] == 128) if kw.get("skip_reshape", False) else (q.shape[-1] == heads * 128)
         if mask is None and not a and q.is_cuda and q.dtype == torch.bfloat16 and dim_ok:
             return hip_optimized_attention(q, k, v, heads, mask=None, **kw)
-        return orig(q, k, v, heads, mask, *a, **kw)
+        # Any override has been applied by now: the original must not apply it again.
+        return orig(q, k, v, heads, mask, *a, **without_override(kw))
+
+    def optimized_attention(q, k, v, heads, mask=None, *a, **kw):
+        # ComfyUI's optimized_attention hands every call to
+        # transformer_options["optimized_attention_override"] when one is set,
+        # as override(func, q, k, v, heads, mask=..., ...), func being the
+        # attention it would otherwise run; the h3_sla override relies on it
+        # (custom_nodes/h3_sla/__init__.py:265-284).
+        opts = kw.get("transformer_options")
+        override = opts.get("optimized_attention_override") if isinstance(opts, dict) else None
+        if override is not None:
+            if a:
+                return override(attention, q, k, v, heads, mask, *a, **kw)
+            return override(attention, q, k, v, heads, mask=mask, **kw)
+        return attention(q, k, v, heads, mask, *a, **kw)
 
     optimized_attention._h3attn_patched = True
     optimized_attention._h3attn_orig = orig

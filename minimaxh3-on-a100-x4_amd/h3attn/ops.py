@@ -112,6 +112,46 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | N
     return out
 
 
+PROF_WAVES = 8
+PROF_SLOTS = 12
+
+
+def attn_fwd_profiled(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """attn_fwd through the phase-profile build (libh3attn_prof.so), unsplit (h3a_attn_fwd).
+
+    Workgroup 0 of the launch records its per-wave phase ticks; read them with
+    prof_read().  The profile build stamps the shader clock inside the stage
+    loop, so it runs a little slower than the product build.
+    """
+    q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    L = lib(profile=True)
+    with torch.cuda.device(q.device):
+        rc = L.h3a_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Skv, D,
+                            _bhs(q), _bhs(k), _bhs(v), _bhs(out), sc, _stream(q))
+    check("h3a_attn_fwd (profile build)", rc, L)
+    return out
+
+
+def prof_enabled(profile: bool = True) -> bool:
+    """Whether the library (profile=True: the profile build) records phases."""
+    return bool(lib(profile=profile).h3a_prof_enabled())
+
+
+def prof_read(profile: bool = True) -> list[list[int]]:
+    """[8 waves][12 slots] phase ticks of the last dense launch's workgroup 0 (h3a_prof_read)."""
+    L = lib(profile=profile)
+    buf = (ctypes.c_uint64 * (PROF_WAVES * PROF_SLOTS))()
+    check("h3a_prof_read", L.h3a_prof_read(buf), L)
+    return [[int(buf[w * PROF_SLOTS + i]) for i in range(PROF_SLOTS)] for w in range(PROF_WAVES)]
+
+
+def prof_reset(profile: bool = True) -> None:
+    L = lib(profile=profile)
+    check("h3a_prof_reset", L.h3a_prof_reset(), L)
+
+
 def sparse_workspace_bytes(B: int, H: int, Sq: int, Skv: int, blk_q: int, blk_k: int, max_k_blocks: int,
                            D: int = HEAD_DIM) -> int:
     """Workspace bytes h3a_attn_fwd_blocksparse_ws needs on the current device (0: no split)."""

@@ -80,7 +80,66 @@ def resolve_schedule(preset="off", topk=0.35, layer_keep="", n_layers=50):
     return name, keeps
 
 
+def _ranges_str(layers) -> str:
+    """[31, 32, 33, 46] -> '31-33,46' (the inverse of parse_ranges)."""
+    ls = sorted(layers)
+    out = []
+    i = 0
+    while i < len(ls):
+        j = i
+        while j + 1 < len(ls) and ls[j + 1] == ls[j] + 1:
+            j += 1
+        out.append(f"{ls[i]}-{ls[j]}" if j > i else f"{ls[i]}")
+        i = j + 1
+    return ",".join(out)
+
+
+def schedule_summary(name: str, keeps, blk: int = 64) -> dict:
+    """Summary of a per-layer schedule (custom_nodes/h3_sla/__init__.py:110-124).
+
+    Same keys as the node's, except its latency predictions, which are fits of
+    A100 SP-2 measurements and do not describe this hardware.
+    """
+    keeps = [float(x) for x in keeps]
+    counts: dict[str, int] = {}
+    for kv in keeps:
+        key = f"{round(kv * 100)}"
+        counts[key] = counts.get(key, 0) + 1
+    default = max(set(keeps), key=keeps.count)
+    by = {f"SLA{round(kv * 100)}": _ranges_str([i for i, x in enumerate(keeps) if x == kv])
+          for kv in sorted(set(keeps)) if kv != default}
+    return {"preset": name, "research_name": PRESETS.get(name, {}).get("research_name"),
+            "default_keep": default, "layers_by_keep": by, "counts": counts,
+            "keeps": [round(x, 4) for x in keeps], "blk": int(blk)}
+
+
+def format_summary(sm: dict) -> str:
+    """Log lines of a schedule summary (custom_nodes/h3_sla/__init__.py:127-136), '[h3_sla] '-prefixed."""
+    head = f"SLA preset: {sm['preset']}"
+    if sm.get("research_name"):
+        head += f" (research {sm['research_name']})"
+    lines = [head, f"default keep: {round(sm['default_keep'] * 100)}%"]
+    for name, ranges in sm["layers_by_keep"].items():
+        lines.append(f"{name} layers: {ranges}")
+    lines.append("layer counts: " + ", ".join(f"SLA{k}={v}" for k, v in sorted(sm["counts"].items())))
+    return "\n".join("[h3_sla] " + x for x in lines)
+
+
 # ---------------------------------------------------------------------------
+# Block sizes the block-sparse kernels take (query and key blocks alike):
+# multiples of their 64-key stage.  The h3_sla node offers 16..256 in steps of
+# 16 (custom_nodes/h3_sla/__init__.py:315); the others are refused up front.
+SUPPORTED_BLOCKS = (64, 128, 192, 256)
+
+
+def check_block(blk) -> int:
+    """Return blk as an int, or raise ValueError if the kernels cannot run it."""
+    b = int(blk)
+    if b not in SUPPORTED_BLOCKS:
+        raise ValueError(f"SLA block size {blk} unsupported by libh3attn; use one of {SUPPORTED_BLOCKS}")
+    return b
+
+
 def keep_count(topk_ratio: float, nk: int) -> int:
     """Key blocks kept by score per query block: floor(ratio * nk), at least 1, at most nk."""
     return max(1, min(nk, int(math.floor(topk_ratio * nk + 1e-9))))
@@ -100,6 +159,7 @@ def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int
     towards the lower key-block index.
     """
     del smooth_k  # selection-invariant, see above
+    BLKQ, BLKK = check_block(BLKQ), check_block(BLKK)
     pq = ops.block_pool(q, BLKQ)
     pk = ops.block_pool(k, BLKK)
     kc = keep_count(topk_ratio, pk.shape[2])
@@ -109,6 +169,7 @@ def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int
 def sparse_attention(q, k, v, topk_ratio: float, blk: int = 64, force_diag: bool = False,
                      smooth_k: bool = True):
     """[1,H,S,D] -> [1,H,S,D] block-sparse attention (SLA sparse branch only; h3_sla:226-235)."""
+    blk = check_block(blk)
     out_dtype = q.dtype
     q16, k16, v16 = (t.to(torch.bfloat16) for t in (q, k, v))
     _, lut, counts = get_block_map(q16, k16, topk_ratio, blk, blk, force_diag=force_diag,

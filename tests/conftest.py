@@ -44,6 +44,28 @@ def assert_close_absmax(out, ref, max_rel=MAX_REL, mean_rel=MEAN_REL, what=""):
     return mx, mean, amax
 
 
+def assert_prologue_close(got_bits, ref_bits, what, min_exact=0.99):
+    """Prologue output (kernel, fp32 math) vs the oracle (fp64 math), both rounded once to bf16.
+
+    Allowed per value: one bf16 ulp of the result (<= 2^-7 |r|) plus the fp32
+    error of the rotation before rounding, ~1e-6 * (|y_i| + |y_{i+rot/2}|)
+    with |y| <= ~8 here, taken as an absolute 1e-5.  The second term only
+    matters where the rotation cancels to a value near zero.  At least
+    `min_exact` of the values must be bit-identical.
+    """
+    import oracle
+    g = oracle.bf16_to_f32(got_bits).reshape(got_bits.shape).astype(np.float64)
+    r = oracle.bf16_to_f32(ref_bits).reshape(ref_bits.shape).astype(np.float64)
+    exact = np.mean(got_bits == ref_bits)
+    tol = np.abs(r) * 2.0 ** -7 + 1e-5
+    bad = np.abs(g - r) > tol
+    if bad.any():
+        i = np.unravel_index(np.argmax(np.abs(g - r) - tol), r.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} values off by more than 1 ulp + 1e-5; "
+                             f"worst at {i}: got {g[i]!r} want {r[i]!r}")
+    assert exact >= min_exact, f"{what}: only {exact:.4f} bit-exact"
+
+
 def bf16_bits(x_f32: np.ndarray) -> np.ndarray:
     import oracle
     return oracle.f32_to_bf16(x_f32)

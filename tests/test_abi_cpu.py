@@ -71,11 +71,14 @@ def test_blocksparse_argument_errors():
                                           bq, bk, maxk, 0.1, None)
 
     assert call(lut=None) == _lib.H3A_ERR_INVALID_ARG
-    assert call(bq=32) == _lib.H3A_ERR_UNSUPPORTED
-    assert call(bk=256) == _lib.H3A_ERR_UNSUPPORTED
+    for bq, bk in ((32, 128), (48, 128), (320, 128), (128, 96), (128, 16), (128, 512)):
+        assert call(bq=bq, bk=bk) == _lib.H3A_ERR_UNSUPPORTED
+        assert b"unsupported" in L.h3a_last_error()
     assert call(maxk=0) == _lib.H3A_ERR_INVALID_ARG
     assert call(maxk=4) == _lib.H3A_ERR_INVALID_ARG  # 300 keys = 3 blocks of 128
     assert b"max_k_blocks" in L.h3a_last_error()
+    assert call(bk=256, maxk=3) == _lib.H3A_ERR_INVALID_ARG  # 2 blocks of 256
+    assert call(bk=192, maxk=3) == _lib.H3A_ERR_INVALID_ARG  # 2 blocks of 192
 
 
 def test_lut_and_prologue_argument_errors():

@@ -131,13 +131,33 @@ def test_running_max_rises(gpu, S, slope):
     """Even query rows see scores rising steadily along the keys: 64*slope/sqrt(128)
     per key, i.e. ~700, ~210 and ~20 (log2 units) per 64-key stage for the three cases,
     ~3300 / ~3300 / ~310 in all.  exp2 against the first stage's max would overflow, so
-    the running max is refreshed at every stage (first two) or every few stages, with
-    p up to 2^64 accepted in between (third).  Odd rows fall and underflow to zero."""
+    the running max is refreshed at every stage (all three: p may reach 2^16 between
+    refreshes, and 20 log2 units per stage exceed that).  Odd rows fall and underflow
+    to zero."""
     rng = np.random.default_rng(30)
     q, k, v = ramp_case(rng, S, slope=slope, q0=64.0)
     o = _run(q, k, v, gpu)
     assert np.isfinite(o).all()
     assert_close_absmax(o, oracle.attn_fwd(q, k, v, round_p=True), what="rising max")
+
+
+@pytest.mark.parametrize("vscale,rise", [(1e16, 20.0), (1e28, 40.0), (1e30, 12.0)])
+def test_large_values_with_rising_max(gpu, vscale, rise):
+    """|v| far above activation scale while the running max rises `rise` log2 units per
+    64-key stage (even rows; odd rows fall).  Between refreshes of the stale reference
+    max p may reach 2^16, so O is bounded by 2^17 * ceil(S/64) * max|v| and stays finite
+    for max|v| < 2^128 / (2^17 * ceil(S/64)), 8.1e31 at S = 2048 (the header's bound).
+    A rise of 12 units per stage leaves p below the refresh limit for one stage and
+    above it for the next, so both paths run at |v| = 1e30."""
+    rng = np.random.default_rng(32)
+    S = 2048
+    q0 = 64.0
+    slope = rise * math.sqrt(128) / (64 * q0 * math.log2(math.e))
+    q, k, v = ramp_case(rng, S, slope=slope, q0=q0)
+    v = oracle.f32_to_bf16(oracle.bf16_to_f32(v).reshape(v.shape) * np.float32(vscale))
+    o = _run(q, k, v, gpu)
+    assert np.isfinite(o).all(), "non-finite output"
+    assert_close_absmax(o, oracle.attn_fwd(q, k, v, round_p=True), what=f"|v|~{vscale:g} rise {rise}")
 
 
 def test_lone_dominant_key(gpu):

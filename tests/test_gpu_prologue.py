@@ -14,7 +14,7 @@ import torch
 
 import h3attn
 import oracle
-from conftest import from_dev_bf16, to_dev_bf16
+from conftest import assert_prologue_close, from_dev_bf16, to_dev_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -25,26 +25,6 @@ def _inputs(rng, S, H, spread=True):
         x *= rng.uniform(0.5, 4.0, size=(2, S, 1, 1)).astype(np.float32)
     w = (1.0 + 0.05 * rng.standard_normal((2, 128))).astype(np.float32)
     return oracle.f32_to_bf16(x), oracle.f32_to_bf16(w)
-
-
-def _compare(got_bits, ref_bits, what):
-    """Kernel (fp32 math) vs oracle (fp64 math), both rounded once to bf16.
-
-    Allowed per value: one bf16 ulp of the result (<= 2^-7 |r|) plus the fp32
-    error of the rotation before rounding, ~1e-6 * (|y_i| + |y_{i+rot/2}|)
-    with |y| <= ~8 here, taken as an absolute 1e-5.  The second term only
-    matters where the rotation cancels to a value near zero.
-    """
-    g = oracle.bf16_to_f32(got_bits).reshape(got_bits.shape).astype(np.float64)
-    r = oracle.bf16_to_f32(ref_bits).reshape(ref_bits.shape).astype(np.float64)
-    exact = np.mean(got_bits == ref_bits)
-    tol = np.abs(r) * 2.0 ** -7 + 1e-5
-    bad = np.abs(g - r) > tol
-    if bad.any():
-        i = np.unravel_index(np.argmax(np.abs(g - r) - tol), r.shape)
-        raise AssertionError(f"{what}: {int(bad.sum())} values off by more than 1 ulp + 1e-5; "
-                             f"worst at {i}: got {g[i]!r} want {r[i]!r}")
-    assert exact >= 0.99, f"{what}: only {exact:.4f} bit-exact"
 
 
 def _run_gpu(xq, xk, w, rope, rot, device, fused_layout):
@@ -79,8 +59,8 @@ def test_prologue_small(gpu, S, H, rot, fused):
     rope = oracle.rope_table(S, rot) if rot else None
     gq, gk = _run_gpu(x[0], x[1], w, rope, rot, gpu, fused)
     rq, rk = oracle.qk_rmsnorm_rope(x[0][None], x[1][None], rope, w[0], w[1], eps=1e-6, rot_dim=rot)
-    _compare(gq, rq[0], "q")
-    _compare(gk, rk[0], "k")
+    assert_prologue_close(gq, rq[0], "q")
+    assert_prologue_close(gk, rk[0], "k")
 
 
 def test_prologue_s8192_h56_fused_views(gpu):
@@ -91,8 +71,8 @@ def test_prologue_s8192_h56_fused_views(gpu):
     rope = oracle.rope_table(S, 128)
     gq, gk = _run_gpu(x[0], x[1], w, rope, 128, gpu, True)
     rq, rk = oracle.qk_rmsnorm_rope(x[0][None], x[1][None], rope, w[0], w[1], eps=1e-6, rot_dim=128)
-    _compare(gq, rq[0], "q")
-    _compare(gk, rk[0], "k")
+    assert_prologue_close(gq, rq[0], "q")
+    assert_prologue_close(gk, rk[0], "k")
 
 
 def test_prologue_rejects_bad_layout(gpu):

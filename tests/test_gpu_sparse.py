@@ -43,7 +43,8 @@ def test_block_map_to_lut(gpu):
     assert np.array_equal(lut.cpu().numpy(), rl)
 
 
-@pytest.mark.parametrize("blk,S,H", [(128, 1000, 2), (64, 1000, 2), (128, 1160, 1), (64, 777, 3)])
+@pytest.mark.parametrize("blk,S,H", [(128, 1000, 2), (64, 1000, 2), (128, 1160, 1), (64, 777, 3),
+                                     (192, 1000, 2), (256, 1000, 2), (192, 1537, 1), (256, 1300, 3)])
 def test_sparse_vs_masked_oracle(gpu, blk, S, H):
     rng = np.random.default_rng(blk + S)
     q, k, v = (randn_bf16(rng, (1, H, S, 128)) for _ in range(3))
@@ -54,6 +55,36 @@ def test_sparse_vs_masked_oracle(gpu, blk, S, H):
     got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
     ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
     assert_close_absmax(got, ref, what=f"sparse blk={blk}")
+
+
+@pytest.mark.parametrize("blk_q,blk_k,S", [(256, 64, 1000), (64, 256, 1000), (192, 128, 1111),
+                                           (128, 192, 1111), (256, 192, 777), (192, 256, 1500)])
+@pytest.mark.parametrize("split", [True, False])
+def test_sparse_mixed_block_sizes(gpu, blk_q, blk_k, S, split):
+    """Query and key blocks of different sizes from {64, 128, 192, 256}: a LUT row serves
+    blk_q / 64 or blk_q / 128 query sub-blocks, a key block is blk_k / 64 stages."""
+    rng = np.random.default_rng(blk_q * 7 + blk_k + S)
+    H = 2
+    q, k, v = (randn_bf16(rng, (1, H, S, 128)) for _ in range(3))
+    nk = -(-S // blk_k)
+    bmap = oracle.block_map(q, k, blk_q, blk_k, keep=max(1, nk // 3), force_diag=True)
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, blk_q, blk_k,
+                                    split_tail=split)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk_q, blk_k=blk_k)
+    assert_close_absmax(got, ref, what=f"sparse blk_q={blk_q} blk_k={blk_k}")
+
+
+def test_sparse_unsupported_block_sizes_raise(gpu):
+    q = torch.zeros(1, 1, 256, 128, dtype=torch.bfloat16, device=gpu)
+    lut = torch.zeros(1, 1, 8, 1, dtype=torch.int32, device=gpu)
+    cnt = torch.ones(1, 1, 8, dtype=torch.int32, device=gpu)
+    for bq, bk in ((32, 64), (64, 96), (48, 48), (320, 64)):
+        nqb = -(-256 // bq)
+        with pytest.raises(ValueError, match="unsupported"):
+            h3attn.attn_fwd_blocksparse(q, q, q, lut[:, :, :1].expand(1, 1, nqb, 1).contiguous(),
+                                        cnt[:, :, :1].expand(1, 1, nqb).contiguous(), bq, bk)
 
 
 @pytest.mark.parametrize("S,blk_k", [(640, 128), (1300, 64), (131, 128)])
@@ -242,13 +273,16 @@ def test_sparse_lone_dominant_key(gpu):
     assert np.abs(got[0, 0, blk:] - vrow).max() <= 2.0 ** -8 * np.abs(vrow).max()
 
 
-@pytest.mark.parametrize("bad", [-1, 10**6])
-def test_lut_leading_invalid_entry_changes_nothing(gpu, bad):
-    """A LUT row whose first entries name no key block (-1, or a block past the keys)
-    starts with fully masked stages.  The result equals the row without them, bit for
-    bit: the first valid stage sets the reference max exactly either way."""
+@pytest.mark.parametrize("blk", [128, 64])
+@pytest.mark.parametrize("bad", [-1, 10**6, 2**24 + 5, 2**31 - 1, -2**31, 2**31 // 64])
+def test_lut_leading_invalid_entry_changes_nothing(gpu, bad, blk):
+    """A LUT row whose first entries name no key block (negative, or a block past the
+    keys, up to 2^31 - 1, whose first key would overflow a 32-bit multiply) starts with
+    fully masked stages.  The result equals the row without them, bit for bit: the first
+    valid stage sets the reference max exactly either way.  Both sparse kernels (pairs
+    of 128-row blocks, key-split 64-row blocks)."""
     rng = np.random.default_rng(43)
-    S, blk = 1000, 128
+    S = 1000
     q, k, v = (to_dev_bf16(randn_bf16(rng, (1, 2, S, 128)), gpu) for _ in range(3))
     nq = nk = -(-S // blk)
     kept = [sorted(rng.choice(nk, size=3, replace=False).tolist()) for _ in range(2 * nq)]

@@ -195,6 +195,94 @@ def test_sla_override_scope_schedule_and_fallback():
     assert sched.keep_for(None) == sched.default_keep and sched.keep_for(99) == sched.default_keep
 
 
+def test_sla_block_size_checked_at_construction():
+    """Unsupported block sizes fail when the schedule/override is built (as the node fails at
+    patch time, custom_nodes/h3_sla/__init__.py:331), not by silently running dense later."""
+    for blk in (16, 32, 48, 80, 96, 112, 144, 160, 176, 208, 224, 240, 0, 512):
+        with pytest.raises(ValueError, match="block size"):
+            hooks.Schedule("custom", [0.5] * 50, blk=blk)
+        with pytest.raises(ValueError, match="block size"):
+            hooks.make_sla_override(topk=0.5, blk=blk)
+        with pytest.raises(ValueError, match="block size"):
+            sla.sparse_attention(torch.zeros(1, 1, 8, 128), torch.zeros(1, 1, 8, 128),
+                                 torch.zeros(1, 1, 8, 128), 0.5, blk)
+    for blk in sla.SUPPORTED_BLOCKS:
+        assert hooks.Schedule("custom", [0.5] * 50, blk=blk).blk == blk
+        assert callable(hooks.make_sla_override(topk=0.5, blk=blk))
+
+
+def test_schedule_summary_and_format():
+    """schedule_summary / format_summary (custom_nodes/h3_sla/__init__.py:110-136)."""
+    name, keeps = sla.resolve_schedule("balanced")
+    sm = sla.schedule_summary(name, keeps, 128)
+    assert sm["preset"] == "balanced" and sm["research_name"] == "T2" and sm["blk"] == 128
+    assert sm["default_keep"] == 0.15
+    assert sm["layers_by_keep"] == {"SLA25": "31-42,48-49"}
+    assert sm["counts"] == {"15": 36, "25": 14}
+    text = sla.format_summary(sm).splitlines()
+    assert text == ["[h3_sla] SLA preset: balanced (research T2)", "[h3_sla] default keep: 15%",
+                    "[h3_sla] SLA25 layers: 31-42,48-49", "[h3_sla] layer counts: SLA15=36, SLA25=14"]
+    sm = sla.schedule_summary("custom", [0.3, 0.3, 0.2, 0.3, 0.2, 0.2, 0.2])
+    assert sm["default_keep"] == 0.2 and sm["layers_by_keep"] == {"SLA30": "0-1,3"}
+    assert sla._ranges_str([5, 1, 2, 3, 9]) == "1-3,5,9"
+    assert hooks.Schedule(name, keeps, blk=64).summary["layers_by_keep"] == {"SLA25": "31-42,48-49"}
+
+
+def test_schedule_timing_buckets(monkeypatch):
+    """H3_SLA_TIMING: events around each sparse layer, resolved at the step's last layer (h3_sla:199-212)."""
+    monkeypatch.setattr(torch.cuda, "Event", lambda enable_timing=True: _FakeSyncEvent())
+    monkeypatch.setattr(sla, "sparse_attention", lambda q, k, v, keep, blk, **kw: q)
+    monkeypatch.setenv("H3_SLA_TIMING", "1")
+    sched = hooks.Schedule("custom", [0.5, 1.0, 0.5], blk=64)
+    assert sched.timing
+    q = torch.zeros(1, 1, 4, 128)
+    for _ in range(2):  # two steps of three layers
+        for layer in range(3):
+            out = sched.run(layer, q, q, q)
+            assert (out is None) == (layer == 1)
+    assert sched.attn_n == [2, 0, 2] and sched._ev == []
+    ms = sched.attn_ms_per_layer_call()
+    assert ms[1] is None and ms[0] > 0 and ms[2] > 0
+    monkeypatch.setenv("H3_SLA_TIMING", "0")
+    assert not hooks.Schedule("custom", [0.5], blk=64).timing
+
+
+class _FakeSyncEvent:
+    clock = [0]
+
+    def record(self):
+        _FakeSyncEvent.clock[0] += 1
+        self.t = _FakeSyncEvent.clock[0]
+
+    def synchronize(self):
+        pass
+
+    def elapsed_time(self, other):
+        return float(other.t - self.t)
+
+
+def test_installed_optimized_attention_still_calls_the_override():
+    """With hooks.install_optimized_attention in place, a transformer_options override (the
+    h3_sla sparse path) still receives every call first, as ComfyUI's wrapper does."""
+    import types
+    mod = types.SimpleNamespace(optimized_attention=standin_dit.optimized_attention)
+    assert hooks.install_optimized_attention(mod)
+    seen = []
+
+    def override(func, *args, **kwargs):
+        seen.append((func, kwargs.get("mask"), "optimized_attention_override" in kwargs["transformer_options"]))
+        return func(*args, **kwargs)  # fall back, as a gated-off override does
+
+    q, k, v = (torch.randn(1, 2, 6, 128) for _ in range(3))
+    opts = {"optimized_attention_override": override, "other": 1}
+    got = mod.optimized_attention(q, k, v, 2, skip_reshape=True, transformer_options=opts)
+    want = standin_dit.optimized_attention(q, k, v, 2, skip_reshape=True)
+    assert len(seen) == 1 and seen[0][1] is None and seen[0][2]
+    assert torch.equal(got, want)  # CPU tensors: the fallback reaches the original exactly once
+    assert mod.optimized_attention(q, k, v, 2, skip_reshape=True).shape == (1, 6, 256)
+    assert len(seen) == 1
+
+
 # ----------------------------------------------------------------------------- per-component timing
 class _FakeEvent:
     """record() stamps a shared tick counter; elapsed_time is the tick difference."""
