@@ -22,11 +22,55 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "minimaxh3-on-a100-x4_amd"))
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
-# HBM bytes per launch of the dense kernel at this shape, from the rocprofv3
-# FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0) passes recorded in
-# profiles/attn_dense_h56_s42120_counters.txt (scales from a 2048 MiB copy).
-MEASURED_TRAFFIC_BYTES = 9.58e9
+NOMINAL_CLOCK_GHZ = 2.4
+FLOP_PER_CLK = 256 * 4096  # dense bf16 MFMA, whole chip
+# HBM bytes per launch of the dense kernel at this shape come from the rocprofv3
+# FETCH_SIZE (x2.0) and WRITE_SIZE (x1.0) passes summarised in this file (each
+# counter scaled by what it reads for a 2048 MiB device copy); its line
+# "roofline.traffic = <bytes> B" is read at run time.
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_h56_s42120_counters.txt")
 B, H, S, D, LAYERS = 1, 56, 42120, 128, 50
+
+
+def measured_traffic():
+    """(bytes per dense launch, source) from the committed counter summary, or (None, reason)."""
+    import re
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for ln in f:
+                m = re.match(r"\s*roofline\.traffic\s*=\s*([0-9.]+[eE][+]?[0-9]+)\s*B\b", ln)
+                if m:
+                    return float(m.group(1)), os.path.relpath(TRAFFIC_SUMMARY, ROOT)
+    except OSError as e:
+        return None, f"unreadable: {e}"
+    return None, "no roofline.traffic line"
+
+
+def measure_clock(torch, h3attn, dev, heads=H):
+    """Shader clock under this workload, measured in this process: one dense layer of the
+    same shape through the phase-profile build, whose workgroup 0 counts shader-clock
+    ticks (s_memtime) and 100 MHz ticks (s_memrealtime) over its stage loop.  Returns
+    (GHz averaged over the workgroup's 8 waves, note) or (None, reason)."""
+    from h3attn import ops
+    try:
+        if not ops.prof_enabled(profile=True):
+            return None, "profile build records nothing"
+        g = torch.Generator(device=dev).manual_seed(77)
+        q, k, v = (torch.randn(B, heads, S, D, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(3))
+        out = torch.empty_like(q)
+        ops.attn_fwd_profiled(q, k, v, out=out)  # warm: the clock settles under load
+        ops.prof_reset()
+        ops.attn_fwd_profiled(q, k, v, out=out)
+        rows = ops.prof_read()
+        ghz = [r[7] / (r[8] * 10.0) for r in rows if r[8] > 0]
+        del q, k, v, out
+        if not ghz:
+            return None, "no profile rows"
+        return sum(ghz) / len(ghz), (f"s_memtime / s_memrealtime over workgroup 0's stage loop, one profiled "
+                                     f"layer (H={heads}, S={S}) after the timed steps; waves "
+                                     f"{min(ghz):.3f}-{max(ghz):.3f} GHz")
+    except (RuntimeError, ValueError) as e:
+        return None, f"not measured: {e}"
 
 
 def flops_per_layer(h=H, s=S, d=D):
@@ -77,6 +121,30 @@ def cpu_baseline(budget_s: float = 12.0, heads: int = H):
     }
 
 
+def cpu_config1(torch, reps: int = 5):
+    """The CPU-runnable dense case (B=1, H=4, S=2048, D=128, bf16, N(0,1) from a seed) timed
+    with torch SDPA on the host cores: the MATH backend and the default CPU flash backend."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 4, 2048, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    fl = flops_per_layer(h=4, s=2048)
+    out = {"shape": "B=1 H=4 S=2048 D=128 bf16", "cores": torch.get_num_threads()}
+    for name, backends in (("math", [SDPBackend.MATH]), ("flash", [SDPBackend.FLASH_ATTENTION])):
+        try:
+            with sdpa_kernel(backends):
+                torch.nn.functional.scaled_dot_product_attention(q, k, v)
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    torch.nn.functional.scaled_dot_product_attention(q, k, v)
+                dt = (time.perf_counter() - t0) / reps
+            out[f"{name}_ms"] = round(dt * 1e3, 2)
+            out[f"{name}_tflops"] = round(fl / dt / 1e12, 4)
+        except RuntimeError as e:
+            out[f"{name}_ms"] = None
+            out[f"{name}_error"] = str(e)[:120]
+    return out
+
+
 def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,6 +163,8 @@ def _parse():
                     help="sparse: query and key tile size (128: the 128x128 workload; 64: the SLA "
                          "block size default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-clock", action="store_true",
+                    help="dense: skip the shader-clock measurement (one profiled layer after the timed steps)")
     ap.add_argument("--no-split-tail", action="store_true",
                     help="dense: run h3a_attn_fwd (never splits the last round of tiles) instead of "
                          "h3a_attn_fwd_ws")
@@ -174,17 +244,26 @@ def run_dense(args, torch, h3attn, dev, heads=H):
                 {"workload": workload, "B": B, "H": heads, "S": S, "D": D, "layers": L,
                  "segments": "text 512 + cond 256 + audio 2048 + video 39304"})
     res["data"] = "synthetic (seeded device RNG, fresh q/k/v per layer, resident in HBM)"
+    traffic, traffic_src = measured_traffic() if heads == H else (None, "counters taken at H=56 only")
+    ghz, clock_note = measure_clock(torch, h3attn, dev, heads) if not args.no_clock else (None, "skipped")
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic, "traffic_source": traffic_src,
+            "kernel": "attn_fwd_pingpong_kernel (+ split_combine_kernel for the split tail)",
+            "flop_per_launch": fpl, "avg_launch_ms": round(avg_kernel_ms, 3),
+            "clock_ghz_measured": None if ghz is None else round(ghz, 3), "clock_note": clock_note}
+    if ghz:
+        peak_at_clock = FLOP_PER_CLK * ghz * 1e9 / 1e12
+        roof["peak_at_measured_clock"] = round(peak_at_clock, 1)
+        roof["frac_at_measured_clock"] = round(achieved / peak_at_clock, 4)
     res.update({
         "pct_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "ms_per_layer": round(avg_kernel_ms, 3),
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES if heads == H else None,
-                     "kernel": "attn_fwd_pingpong_kernel (+ split_combine_kernel for the split tail)", "flop_per_launch": fpl,
-                     "avg_launch_ms": round(avg_kernel_ms, 3)},
+        "roofline": roof,
     })
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(heads=heads)
+        res["cpu_baseline"]["config1_sdpa_cpu"] = cpu_config1(torch)
     return res
 
 
