@@ -96,6 +96,28 @@ int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o,
                     float scale, void *workspace, size_t workspace_bytes, h3a_stream_t stream);
 
 /*
+ * h3a_attn_fwd_ws without a workspace argument and without any allocation:
+ * the split-tail partials go to a static device array of
+ * H3A_NOALLOC_SCRATCH_BYTES (32.5 MiB) that each GPU the library runs on holds
+ * until the process ends.  No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It calls no hipMalloc/hipFree and no
+ * allocating library routine.  Every call on a GPU shares that GPU's array, so
+ * calls that overlap on one GPU (other streams, other threads) race: the
+ * caller must serialise them.  Every byte the merge reads is written earlier
+ * by the same call, so nothing needs clearing between calls.  A split tail
+ * larger than the array (a device with more than 256 CUs) gives
+ * H3A_ERR_UNSUPPORTED.  Same kernels and split plan as h3a_attn_fwd_ws, so the
+ * results are equal bit for bit; same arguments and errors as h3a_attn_fwd.
+ */
+#define H3A_NOALLOC_SCRATCH_BYTES 34078720u
+int h3a_attn_fwd_noalloc(const void *q, const void *k, const void *v, void *o,
+                         int B, int H, int Sq, int Skv, int D,
+                         const int64_t q_strides[3], const int64_t k_strides[3],
+                         const int64_t v_strides[3], const int64_t o_strides[3],
+                         float scale, h3a_stream_t stream);
+
+/*
  * Block-sparse attention forward (h3_sla path, custom_nodes/h3_sla/__init__.py:226-235).
  * Query block qb of (b,h) attends only to the key blocks listed in
  *   lut[((b*H + h)*nqb + qb)*max_k_blocks + 0 .. counts[(b*H+h)*nqb + qb]-1]

@@ -1,10 +1,12 @@
 // extern "C" entry points of libh3attn (declared in include/h3attn.h):
 // argument validation, error reporting, dispatch to the kernel launchers.
 // Validation runs before any HIP call, so a bad argument never reaches the GPU.
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "h3a_internal.h"
 
@@ -68,6 +70,41 @@ int check_attn(const void *q, const void *k, const void *v, void *o, int B, int 
   return H3A_OK;
 }
 
+// Scratch of the allocation-free dense entry point (h3a_attn_fwd_noalloc): the
+// split-tail partials, (O row, m, l) in fp32 for each of the r * P key ranges
+// of the last round's tiles.  r * P <= CUs (P = CUs / r at most), so on a
+// 256-CU device no plan needs more than 256 * 256 * (128 + 2) floats.  Each GPU
+// holds its own copy until the process ends.  In host code `scratch` only
+// names the symbol; its device address comes from hipGetSymbolAddress, once per
+// device (scratch_ptr).
+constexpr size_t kScratchBytes = H3A_NOALLOC_SCRATCH_BYTES;
+static_assert(kScratchBytes == (size_t)256 * 256 * (128 + 2) * sizeof(float), "256-CU split tail");
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's copy of `scratch`.
+int scratch_ptr(void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(H3A_ERR_HIP, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(H3A_ERR_UNSUPPORTED, "device index %d out of range", dev);
+  void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(H3A_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return H3A_OK;
+}
+
 void fill_attn_args(AttnArgs &a, const void *q, const void *k, const void *v, void *o, int B, int H,
                     int Sq, int Skv, const int64_t *qs, const int64_t *ks, const int64_t *vs,
                     const int64_t *os, float scale) {
@@ -107,6 +144,29 @@ int h3a_attn_fwd(const void *q, const void *k, const void *v, void *o, int B, in
   AttnArgs a;
   fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
   return launch_attn_dense(a, as_stream(stream));
+}
+
+int h3a_attn_fwd_noalloc(const void *q, const void *k, const void *v, void *o, int B, int H, int Sq,
+                         int Skv, int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                         const int64_t v_strides[3], const int64_t o_strides[3], float scale,
+                         h3a_stream_t stream) {
+  clear_error();
+  int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
+  if (rc) return rc;
+  SplitPlan plan;
+  rc = plan_attn_split(B, H, Sq, Skv, &plan);
+  if (rc) return rc;
+  void *ws = nullptr;
+  if (plan.pieces > 1) {
+    if (plan.bytes > kScratchBytes)
+      return fail(H3A_ERR_UNSUPPORTED, "split tail needs %zu bytes of scratch; the static array holds %zu",
+                  plan.bytes, kScratchBytes);
+    rc = scratch_ptr(&ws);
+    if (rc) return rc;
+  }
+  AttnArgs a;
+  fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
+  return launch_attn_dense_split(a, plan, ws, as_stream(stream));
 }
 
 int h3a_attn_fwd_workspace_size(int B, int H, int Sq, int Skv, int D, size_t *bytes) {

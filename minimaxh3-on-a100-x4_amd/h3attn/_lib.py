@@ -44,6 +44,8 @@ SIGNATURES = {
     "h3a_attn_fwd_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(ctypes.c_size_t)]),
     "h3a_attn_fwd_ws": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                              _c_i64_3, _c_i64_3, _c_i64_3, _c_i64_3, _f, _vp, ctypes.c_size_t, _vp]),
+    "h3a_attn_fwd_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                  _c_i64_3, _c_i64_3, _c_i64_3, _c_i64_3, _f, _vp]),
     "h3a_attn_fwd_blocksparse": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                       _c_i64_3, _c_i64_3, _c_i64_3, _c_i64_3,
                                       _vp, _vp, _i, _i, _i, _f, _vp]),
