@@ -27,16 +27,14 @@
 //    a stale reference max and takes a row max only when a stage's p sum
 //    overflows its bound.  A split tail cuts the last, partly filled round of
 //    query tiles into key ranges merged by split_combine_kernel.
-//  * Block-sparse, 128-row query blocks (attn_fwd_pingpong_kernel with
-//    kSparse): the ping-pong over a pair of query blocks, one per group, each
-//    with its own LUT row and K/V stream staged through VGPRs into padded LDS
-//    rows; a group issues its loads right after its matrix cluster and
-//    writes LDS at the end of its softmax slot.  LUT entries are read ahead.
-//  * Block-sparse, 64-row query blocks (attn_fwd_kernel with kSparse and
-//    kKeySplit): 4 waves split each stage's keys between two pairs of waves
-//    and merge the halves at the end; two workgroups per CU, register-staged
-//    K/V, lazy rescale (the running max is refreshed only when a row outgrows
-//    it by 2^8).
+//  * Block-sparse (attn_fwd_pingpong_kernel with kSparse): the ping-pong
+//    over a pair of query blocks, one per group, each with its own LUT row
+//    and K/V stream fetched by LDS DMA into swizzled rows; a group issues its
+//    K fetch at the top of its softmax slot (while the other group's MFMAs
+//    run) and its V fetch right after its matrix cluster.  LUT entries are
+//    read ahead.  128-row blocks: each wave takes 32 rows against all 64 keys
+//    of a stage.  64-row blocks (kKeySplit): a group's 4 waves are 2 query
+//    slices x 2 key halves, merged at the end.
 //  * Every stage's buffer resource is rebased on its first key and covers only
 //    the valid rows, so rows past Skv arrive as zeros and offsets stay
 //    loop-invariant; exp2-based softmax with scale*log2(e) folded into one
@@ -98,10 +96,11 @@ namespace h3a {
 #ifndef H3A_SPARSE_PINGPONG
 #define H3A_SPARSE_PINGPONG 1
 #endif
-// Sparse ping-pong: a group issues its K/V loads right after its matrix
-// cluster (1), at the top of its softmax slot (0), the K loads after the
-// matrix cluster and the V loads at the top of the softmax slot (2), or
-// interleaved with the last 8 MFMAs of the matrix cluster (3).
+// Sparse ping-pong with register staging (H3A_SPARSE_PP_DMA=0): a group
+// issues its K/V loads right after its matrix cluster (1), at the top of its
+// softmax slot (0), the K loads after the matrix cluster and the V loads at
+// the top of the softmax slot (2), or interleaved with the last 8 MFMAs of
+// the matrix cluster (3).
 #ifndef H3A_SPARSE_PP_EARLY
 #define H3A_SPARSE_PP_EARLY 1
 #endif
@@ -109,9 +108,28 @@ namespace h3a {
 #ifndef H3A_SPARSE_REGS
 #define H3A_SPARSE_REGS 1
 #endif
+// Sparse ping-pong (pairs of query blocks): each group fetches its own K/V
+// stages by LDS DMA into swizzled rows (1), or stages them through VGPRs into
+// padded rows (0).  With DMA, KTOP of a wave's 4 K loads and VTOP of its 4 V
+// loads per stage go at the top of its softmax slot, the rest right after its
+// matrix cluster.
+#ifndef H3A_SPARSE_PP_DMA
+#define H3A_SPARSE_PP_DMA 1
+#endif
+#ifndef H3A_SPARSE_PP_KTOP
+#define H3A_SPARSE_PP_KTOP 4
+#endif
+#ifndef H3A_SPARSE_PP_VTOP
+#define H3A_SPARSE_PP_VTOP 0
+#endif
 // 64-row query blocks: 4-wave key-split workgroups (1) or 2-wave workgroups (0).
 #ifndef H3A_SPARSE64_KEYSPLIT
 #define H3A_SPARSE64_KEYSPLIT 1
+#endif
+// 64-row query blocks: the ping-pong kernel over pairs of blocks, each group
+// key-split over its block (1), or the single-group kernel above (0).
+#ifndef H3A_SPARSE64_PINGPONG
+#define H3A_SPARSE64_PINGPONG 1
 #endif
 // LDS operand reads issued ahead of the first MFMA of a ping-pong matrix
 // cluster (0: leave the order to the scheduler).
@@ -147,6 +165,11 @@ namespace h3a {
 // LDS operand reads issued after each MFMA of a ping-pong matrix cluster.
 #ifndef H3A_PP_READS_PER_MFMA
 #define H3A_PP_READS_PER_MFMA 2
+#endif
+// Ping-pong matrix cluster with the score and PV MFMAs alternating
+// (qk_pv_interleaved) instead of all score MFMAs first.
+#ifndef H3A_PP_INTERLEAVE
+#define H3A_PP_INTERLEAVE 0
 #endif
 // Row sum from the bf16-rounded P (v_dot2, 16 ops) instead of the unrounded
 // p (32 adds).  Off by default: the reference sums unrounded p.
@@ -461,6 +484,32 @@ __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[
       const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * L::kVRow));
       o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[ks], o[dt]);
     }
+  }
+}
+
+// S^T(j+1) = K(j+1) Q^T and O^T += V^T(j) P^T(j) for two 32-key score
+// sub-tiles, with the two products' MFMAs alternating: score MFMA i (k-step
+// i/2, sub-tile i%2) then PV MFMA i (key step i/4, dim tile i%4).  A score
+// accumulator is then reused every 4th MFMA and a PV one every 8th, instead
+// of every 2nd (score_tile) and every 4th (pv_tile).
+template <class L>
+__device__ __forceinline__ void qk_pv_interleaved(const uint16_t *kbuf, const uint16_t *vbuf,
+                                                  const u32x4 (&qf)[8], int k_rd, int v_rd,
+                                                  f32x16 (&s)[2], const u32x4 (&pf)[4], f32x16 (&o)[4]) {
+  s[0] = f32x16{0.f};
+  s[1] = f32x16{0.f};
+  const char *kb = reinterpret_cast<const char *>(kbuf);
+  const char *vb = reinterpret_cast<const char *>(vbuf);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int ks = i >> 1, u = i & 1;
+    const u32x4 a = *(const u32x4 *)(kb + L::k_off(k_rd, ks) + 32 * u * L::kKRow);
+    s[u] = mfma_32x32x16(a, qf[ks], s[u]);
+    const int kv = i >> 2, dt = i & 3;
+    const char *p = vb + L::v_off(v_rd, dt) + 16 * kv * L::kVRow;
+    const u32x2 lo = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p));
+    const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * L::kVRow));
+    o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[kv], o[dt]);
   }
 }
 
@@ -849,8 +898,12 @@ __device__ __forceinline__ void exp_pack_sum(const f32x16 (&s)[NSUB], float sl2,
         p1[u] = fast_exp2(fmaf(s[u][r + 1], sl2, -m));
         pf[2 * u + h][w] = pack_bf16x2(p0[u], p1[u]);
       }
-      a[r] = p0[0] + p0[1];
-      a[r + 1] = p1[0] + p1[1];
+      a[r] = p0[0];
+      a[r + 1] = p1[0];
+      if constexpr (NSUB >= 2) {
+        a[r] += p0[1];
+        a[r + 1] += p1[1];
+      }
       if constexpr (NSUB == 4) {
         a[r] += p0[2] + p0[3];
         a[r + 1] += p1[2] + p1[3];
@@ -996,31 +1049,46 @@ __device__ __forceinline__ void mid_barrier() {
 // from slot 2j+3 on, after every wave waited for its share of the DMA at the
 // end of slot 2j+2.
 //
-// kSparse: block-sparse attention over pairs of 128-row query blocks, in
-// PadLayout.  Group A takes query block 2p and group B block 2p+1 of pair p,
-// each with its own LUT row and its own double-buffered K/V stages in LDS;
-// both step through the longer of the two stage lists (the shorter one's
-// extra stages load nothing and are fully masked).  A group stages its K/V
-// through VGPRs in its softmax slot: the global loads at the top, the LDS
-// writes at the end, so the registers are free again in its matrix slot.
-//   slot 2j+1:  A: MFMA(j)                    B: load K(j+2) V(j+1), SOFT(j-1), write
-//   slot 2j+2:  A: load K(j+2) V(j+1), SOFT(j), write     B: MFMA(j)
-// A group writes kbuf[j&1] and vbuf[(j+1)&1], last read by its own MFMA(j-1)
-// in an earlier slot, and reads them in MFMA(j+1), after the slot's barrier.
-template <class L, int NSUB, bool kSparse = false>
+// kSparse: block-sparse attention over pairs of query blocks.  Group A takes
+// query block 2p and group B block 2p+1 of pair p, each with its own LUT row
+// and its own double-buffered K/V stages in LDS; both step through the longer
+// of the two stage lists (the shorter one's extra stages load nothing and are
+// fully masked).  By default (H3A_SPARSE_PP_DMA) a group fetches its stages
+// by LDS DMA into SwzLayout rows, K(j+2) at the top of its softmax slot and
+// V(j+1) right after its MFMA(j):
+//   slot 2j+1:  A: MFMA(j), DMA V(j+1)        B: DMA K(j+2), SOFT(j-1)
+//   slot 2j+2:  A: DMA K(j+2), SOFT(j)        B: MFMA(j), DMA V(j+1)
+// Both go to kbuf[j&1] and vbuf[(j+1)&1], last read by the group's own
+// MFMA(j-1) before an earlier barrier; a wave waits for its own DMA before
+// the barrier that precedes the group's MFMA(j+1) (group B lets the loads
+// issued at the top of the current stage stay in flight: vmcnt(kDmaTop)).
+// With register staging (H3A_SPARSE_PP_DMA=0, PadLayout) a group loads
+// through VGPRs in one slot and writes LDS at the end of its softmax slot.
+//
+// kKeySplit (with kSparse): pairs of 64-row query blocks.  Each group's 4
+// waves are 2 query slices (32 rows) x 2 key halves: wave (rq, kh) scores its
+// 32 rows against keys 32*kh .. 32*kh+31 of every 64-key stage (one 32-key
+// score sub-tile, 16 MFMAs per stage) with its own running max, row sum and
+// O; after the loop the key-half-1 wave hands (O, m, l) to its partner
+// through LDS, which merges them as the split-tail combine does.
+template <class L, int NSUB, bool kSparse = false, bool kKeySplit = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   constexpr int NW = 8;
   constexpr int BN = 32 * NSUB;  // keys per stage
+  constexpr int WS = kKeySplit ? 1 : NSUB;  // 32-key score sub-tiles per wave and stage
+  constexpr int QB = kKeySplit ? 64 : 128;  // sparse: query rows per group
   constexpr int kKE = StageBytes<L, BN>::kK / 2, kVE = StageBytes<L, BN>::kV / 2;  // elements
   constexpr int NG = kSparse ? 2 : 1;  // K/V streams: one per group (sparse)
   static_assert(!kSparse || BN == kBN, "block-sparse stages are 64 keys");
-  static_assert(!kSparse || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
+  static_assert(!kKeySplit || (kSparse && NSUB == 2), "key-split pairs are block-sparse, 64-key stages");
+  constexpr bool kSpDma = kSparse && H3A_SPARSE_PP_DMA;  // sparse stages fetched by LDS DMA
+  static_assert(!kSparse || kSpDma || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
   __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[NG][2][kKE];
   __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[NG][2][kVE];
 
   PhaseClock pc;
-  pc.begin(!kSparse && blockIdx.x == 0);
+  pc.begin(blockIdx.x == 0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -1054,7 +1122,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     j0 = (int)((int64_t)nstages * p / a.split_pieces);
     niter = (int)((int64_t)nstages * (p + 1) / a.split_pieces) - j0;  // >= 1
   }
-  // Sparse: a.nqt counts 128-row query blocks and w runs over (b, h, pair).
+  // Sparse: a.nqt counts query sub-blocks of QB rows and w runs over (b, h, pair).
   const int nw_bh = kSparse ? (a.nqt + 1) / 2 : a.nqt;
   const int qt = w % nw_bh, bh = w / nw_bh;
   const int h = bh % a.H, b = bh / a.H;
@@ -1062,15 +1130,19 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
   const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
   uint16_t *Ob = a.o + b * a.osb + h * a.osh;
-  const int qrow = kSparse ? (2 * qt + grp) * 128 + (wave_u & 3) * 32 + l32 : qt * 256 + wave * 32 + l32;
+  // Key-split: wave (rq, kh) of its group (see above); otherwise rq is the
+  // wave's 32-row slice of the group's block and kh = 0.
+  const int rq = kKeySplit ? (wave_u & 1) : (wave_u & 3);
+  const int kh = kKeySplit ? ((wave_u >> 1) & 1) : 0;
+  const int qrow = kSparse ? (2 * qt + grp) * QB + rq * 32 + l32 : qt * 256 + wave * 32 + l32;
   // Sparse: this group's stage count and LUT row; both groups run the longer
   // of the two lists.  A piece of a split pair runs stages [gj0, gj0 + ngrp)
   // of the group's list.
   int ngrp = niter, gj0 = 0;
   const int32_t *lut_row = nullptr;
   if constexpr (kSparse) {
-    // 128-row query sub-block qb reads LUT row qb / a.qmul (blk_q = 256: the
-    // two blocks of a pair share one row).
+    // Query sub-block qb reads LUT row qb / a.qmul (blk_q = 256: the two
+    // 128-row blocks of a pair share one row; blk_q = 192: three 64-row ones).
     auto stages_of = [&](int qb) __attribute__((always_inline)) -> int {
       if (qb >= a.nqt) return 0;
       const int cnt = a.counts[(int64_t)bh * a.nqb + qb / a.qmul];
@@ -1127,7 +1199,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       }
       return;
     }
-    if (qrow < a.Sq) {
+    if (qrow < a.Sq && kh == 0) {
       uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
 #pragma unroll
       for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
@@ -1149,8 +1221,10 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
   float m = kNegInf;  // running row max, in scale*log2(e) units
   float lsum = 0.f;   // this lane's share of the running row sum
-  const int k_rd = L::k_base(l32, g);
-  const int v_rd = L::v_base(lane);
+  // Key half kh starts 32 rows into the stage (an offset that neither layout's
+  // per-step offsets interact with).
+  const int k_rd = L::k_base(l32, g) + kh * 32 * L::kKRow;
+  const int v_rd = L::v_base(lane) + kh * 32 * L::kVRow;
 
   // Dense: each K/V stage is fetched by LDS DMA (all 8 waves, or split
   // between the groups as the knobs say).  Sparse: each group stages its own
@@ -1231,7 +1305,12 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   vst.init(a.vss, tid & 255);
 
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
-  if constexpr (kSparse) {
+  if constexpr (kSpDma) {
+    kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
+    vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+    kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+    wait_vmem_all();
+  } else if constexpr (kSparse) {
     kst.start(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
     vst.start(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
     kst.finish(kbuf[0]);
@@ -1245,10 +1324,10 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     wait_vmem_all();
   }
   __syncthreads();
-  f32x16 s[NSUB];
-  u32x4 pf[2 * NSUB];
-  score_tile<L, NSUB>(kbuf[0], qf, k_rd, s);
-  softmax_stage<NSUB>(s, key_base(0), a.Skv, g, a.sl2, m, lsum, o, pf);
+  f32x16 s[WS];
+  u32x4 pf[2 * WS];
+  score_tile<L, WS>(kbuf[0], qf, k_rd, s);
+  softmax_stage<WS>(s, key_base(0) + 32 * kh, a.Skv, g, a.sl2, m, lsum, o, pf);
   __syncthreads();  // kbuf[0] is free for K(2)
 
   auto dma = [&](auto par, int j) __attribute__((always_inline)) {
@@ -1297,6 +1376,35 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     kst.finish(kbuf[P]);
     vst.finish(vbuf[P ^ 1]);
   };
+  // Sparse with LDS DMA: stage j's fetch of K(j+2) into kbuf[j&1] and V(j+1)
+  // into vbuf[(j+1)&1], buffers the group last read in MFMA(j-1).  Issued
+  // right after the group's MFMA(j); the group waits for it before the
+  // barrier that precedes its MFMA(j+1).
+  // Where a group issues stage j's fetch: right after its MFMA(j), or at the
+  // top of its softmax slot while the other group's MFMAs run.  Of each
+  // wave's kInst loads of K (and of V), the first H3A_SPARSE_PP_KTOP
+  // (H3A_SPARSE_PP_VTOP) go at the top, the rest after the MFMAs.
+  constexpr int kKTop = kSpDma ? H3A_SPARSE_PP_KTOP : 0;
+  constexpr int kVTop = kSpDma ? H3A_SPARSE_PP_VTOP : 0;
+  static_assert(!kSpDma || (decltype(kdma)::kInstTotal % (NW / 2) == 0 &&
+                            decltype(vdma)::kInstTotal % (NW / 2) == 0),
+                "every wave issues the same number of DMA loads per stage");
+  static_assert(kKTop <= decltype(kdma)::kInst && kVTop <= decltype(vdma)::kInst, "placement split");
+  // Loads a group-B wave issues at the top of a stage (waited one stage later).
+  constexpr int kDmaTop = kKTop + kVTop;
+  // top = true: the loads that go at the top of the softmax slot.
+  auto dma_k = [&](auto top, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    constexpr int I0 = decltype(top)::value ? 0 : kKTop;
+    constexpr int I1 = decltype(top)::value ? kKTop : decltype(kdma)::kInst;
+    kdma.template issue_range<I0, I1>(Kb, a.kss, key_k, a.Skv, kbuf[P]);
+  };
+  auto dma_v = [&](auto top, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    constexpr int I0 = decltype(top)::value ? 0 : kVTop;
+    constexpr int I1 = decltype(top)::value ? kVTop : decltype(vdma)::kInst;
+    vdma.template issue_range<I0, I1>(Vb, a.vss, key_v, a.Skv, vbuf[P ^ 1]);
+  };
   constexpr bool kALate = kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
@@ -1306,11 +1414,15 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     constexpr int P = decltype(par)::value;
     if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(1);
 #if H3A_PP_PV_FIRST
-    pv_tile<L, 2 * NSUB>(vbuf[P], pf, v_rd, o);
-    score_tile<L, NSUB>(kbuf[P ^ 1], qf, k_rd, s);
+    pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o);
+    score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s);
 #else
-    score_tile<L, NSUB>(kbuf[P ^ 1], qf, k_rd, s);
-    pv_tile<L, 2 * NSUB>(vbuf[P], pf, v_rd, o);
+    if constexpr (H3A_PP_INTERLEAVE && WS == 2) {
+      qk_pv_interleaved<L>(kbuf[P ^ 1], vbuf[P], qf, k_rd, v_rd, s, pf, o);
+    } else {
+      score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s);
+      pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o);
+    }
 #endif
     constexpr bool kLoadsIn = kSparse && kEarly == 3;
     if constexpr (kLoadsIn) {
@@ -1322,25 +1434,25 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
 #if H3A_PP_READ_AHEAD
     __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
 #pragma unroll
-    for (int i = 0; i < 16 * NSUB; ++i) {
+    for (int i = 0; i < 16 * WS; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
-      if (kLoadsIn && i >= 16 * NSUB - 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (kLoadsIn && i >= 16 * WS - 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
 #endif
     if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(0);
   };
   auto soft = [&](int j) __attribute__((always_inline)) {
     if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(1);
-    const int key0 = kSparse ? soft_key : key_base(j + 1);
+    const int key0 = (kSparse ? soft_key : key_base(j + 1)) + 32 * kh;
 #if H3A_PP_STALE_MAX
-    softmax_stage_stale<NSUB, kSparse>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
+    softmax_stage_stale<WS, kSparse>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
 #else
-    softmax_stage<NSUB>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
+    softmax_stage<WS>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
 #endif
 #if H3A_PP_PIN_SOFTMAX
 #pragma unroll
-    for (int i = 0; i < 2 * NSUB; ++i) pin(pf[i]);
+    for (int i = 0; i < 2 * WS; ++i) pin(pf[i]);
     pin(lsum);
     pin(m);
 #endif
@@ -1350,15 +1462,39 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   pc.loop_begin();
   if (lead) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
-      if constexpr (kSparse) {
+      if constexpr (kSpDma) {
+        pc.mark(0);
+        mfma(par);
+        pc.mark(1);
+        stage_keys(j);
+        dma_k(std::false_type{}, par);
+        dma_v(std::false_type{}, par);
+        pc.mark(0);
+        mid_barrier();
+        pc.mark(2);
+        dma_k(std::true_type{}, par);
+        dma_v(std::true_type{}, par);
+        lut_next(j);
+        if (j + 1 < niter) soft(j);        pc.mark(3);
+        wait_vmem_all();
+        pc.mark(4);
+        slot_barrier();
+        pc.mark(5);
+        pc.stage_done();
+        return;
+      } else if constexpr (kSparse) {
+        pc.mark(0);
         if constexpr (kEarly == 3) stage_keys(j);
         mfma(par);
+        pc.mark(1);
         if constexpr (kEarly == 1 || kEarly == 2) {
           stage_keys(j);
           load_k();
           if constexpr (kEarly == 1) load_v();
         }
+        pc.mark(0);
         mid_barrier();
+        pc.mark(2);
         if constexpr (kEarly == 0) {
           stage_keys(j);
           load_k();
@@ -1366,8 +1502,12 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         if constexpr (kEarly == 0 || kEarly == 2) load_v();
         lut_next(j);
         if (j + 1 < niter) soft(j);
+        pc.mark(3);
         stage_out(par);
+        pc.mark(4);
         slot_barrier();
+        pc.mark(5);
+        pc.stage_done();
         return;
       }
       if constexpr (!kALate) dma(par, j);
@@ -1396,7 +1536,31 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     // kFirst: stage 0, which has no softmax before its matrix cluster (P(0)
     // came from the prologue); peeled off so that the loop body has no branch.
     auto stage = [&](auto par, int j, auto first) __attribute__((always_inline)) {
-      if constexpr (kSparse) {
+      if constexpr (kSpDma) {
+        pc.mark(0);
+        stage_keys(j);  // also sets the key SOFT(j-1) masks with: stage j's first
+        dma_k(std::true_type{}, par);
+        dma_v(std::true_type{}, par);
+        lut_next(j);
+        if constexpr (!decltype(first)::value) soft(j - 1);
+        pc.mark(1);
+        // This wave's fetch of K(j+1) and V(j), issued in stage j-1; what it
+        // issued at the top of this stage may stay in flight.
+        wait_vmem_le<kDmaTop>();
+        pc.mark(4);
+        mid_barrier();
+        pc.mark(2);
+        mfma(par);
+        pc.mark(3);
+        dma_k(std::false_type{}, par);
+        dma_v(std::false_type{}, par);
+        pc.mark(0);
+        slot_barrier();
+        pc.mark(5);
+        pc.stage_done();
+        return;
+      } else if constexpr (kSparse) {
+        pc.mark(0);
         if constexpr (kEarly == 0) {
           stage_keys(j);
           load_k();
@@ -1404,18 +1568,25 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         if constexpr (kEarly == 0 || kEarly == 2) load_v();
         lut_next(j);
         if constexpr (!decltype(first)::value) soft(j - 1);
+        pc.mark(1);
         stage_out(par);
+        pc.mark(4);
         mid_barrier();
+        pc.mark(2);
         // kEarly == 3: the loads for stage j+1 go inside the matrix cluster,
         // also after the last stage (keys past the list: nothing is read).
         if constexpr (kEarly == 3) stage_keys(j + 1);
         mfma(par);
+        pc.mark(3);
         if ((kEarly == 1 || kEarly == 2) && j + 1 < niter) {
           stage_keys(j + 1);
           load_k();
           if constexpr (kEarly == 1) load_v();
         }
+        pc.mark(0);
         slot_barrier();
+        pc.mark(5);
+        pc.stage_done();
         return;
       }
       dma(par, j);
@@ -1434,7 +1605,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
-    if constexpr (kSparse && kEarly > 0) {
+    if constexpr (kSparse && !kSpDma && kEarly > 0) {
       stage_keys(0);
       load_k();
       if constexpr (kEarly != 2) load_v();
@@ -1449,6 +1620,39 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   // Sparse, loads inside the matrix cluster: group B's last stage issued
   // loads (of nothing: keys past its list) that no stage writes out.
   if constexpr (kSparse) wait_vmem_all();
+
+  if constexpr (kKeySplit) {
+    // The loop ended on a barrier after every LDS read and write of the
+    // stages, so a group's own K/V buffers hold the exchange: O of each
+    // slice's key-half-1 wave in the K buffers (lane-major: 64 consecutive
+    // floats per register), its m and l in the V buffers.
+    static_assert(sizeof(kbuf_all[0]) >= 2 * 64 * 64 * sizeof(float), "O exchange fits a group's K buffers");
+    static_assert(sizeof(vbuf_all[0]) >= 2 * 2 * 64 * sizeof(float), "m/l exchange fits a group's V buffers");
+    float *xo = reinterpret_cast<float *>(&kbuf[0][0]) + rq * 64 * 64;
+    float *xm = reinterpret_cast<float *>(&vbuf[0][0]) + rq * 2 * 64;
+    if (kh == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(16 * dt + r) * 64 + lane] = o[dt][r];
+      xm[lane] = m;
+      xm[64 + lane] = lsum;
+    }
+    __syncthreads();
+    if (kh == 1) {  // no barrier follows
+      pc.finish(wave, lane);
+      return;
+    }
+    const float m2 = xm[lane], l2 = xm[64 + lane];
+    const float mn = fmaxf(m, m2);
+    const float a1 = m == kNegInf ? 0.f : fast_exp2(m - mn);
+    const float a2 = m2 == kNegInf ? 0.f : fast_exp2(m2 - mn);
+    lsum = lsum * a1 + l2 * a2;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a1 + xo[(16 * dt + r) * 64 + lane] * a2;
+  }
 
   const float ltot = half_swap_sum(lsum);
   if (piece >= 0) {
@@ -1596,6 +1800,9 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 
 // ---------------------------------------------------------------------------
 using DenseLayout = std::conditional_t<H3A_DENSE_LAYOUT == 1, PadLayout, SwzLayout>;
+// Stage layout of the sparse ping-pong kernels: swizzled rows filled by LDS DMA,
+// or padded rows filled from VGPRs.
+using SparseLayout = std::conditional_t<H3A_SPARSE_PP_DMA != 0, SwzLayout, PadLayout>;
 constexpr int kDenseSub = H3A_DENSE_BN / 32;
 // 128-key dense stages (H3A_DENSE_BN=128) measured 22 % slower, and one
 // build of them gave wrong output when the compiler made the softmax lambda an
@@ -1705,7 +1912,7 @@ int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan
   const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
   p.total = (int)total;
-  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<PadLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
+  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SparseLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
   int rc = check_launch("attn_fwd_pingpong_kernel<sparse, split>");
   if (rc) return rc;
   const int64_t rows = (int64_t)(plan.tiles - plan.first) * 256;
@@ -1715,12 +1922,15 @@ int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   const int rows = sparse_sub_block_rows(blk_q);
-  if (H3A_SPARSE_PINGPONG && rows == 128) {
+  if ((H3A_SPARSE_PINGPONG && rows == 128) || (H3A_SPARSE64_PINGPONG && rows == 64)) {
     AttnArgs p = a;
     const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
     if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
     p.total = (int)pairs;
-    hipLaunchKernelGGL((attn_fwd_pingpong_kernel<PadLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
+    if (rows == 128)
+      hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SparseLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
+    else
+      hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SparseLayout, 2, true, true>), dim3(p.total), dim3(512), 0, s, p);
     return check_launch("attn_fwd_pingpong_kernel<sparse>");
   }
   if (rows == 128) {
@@ -1801,12 +2011,14 @@ int attn_kernel_attrs(int which, double out[6]) {
 #endif
     case H3A_KERNEL_ATTN_SPARSE_128:
 #if H3A_SPARSE_PINGPONG
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<PadLayout, 2, true>), 512, out);
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SparseLayout, 2, true>), 512, out);
 #else
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), 256, out);
 #endif
     case H3A_KERNEL_ATTN_SPARSE_64:
-#if H3A_SPARSE64_KEYSPLIT
+#if H3A_SPARSE64_PINGPONG
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SparseLayout, 2, true, true>), 512, out);
+#elif H3A_SPARSE64_KEYSPLIT
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true, true>),
                         256, out);
 #else

@@ -134,6 +134,25 @@ def attn_fwd_profiled(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: 
     return out
 
 
+def attn_fwd_blocksparse_profiled(q, k, v, lut, counts, blk_q: int, blk_k: int, scale: float | None = None,
+                                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """attn_fwd_blocksparse through the phase-profile build, unsplit (h3a_attn_fwd_blocksparse).
+
+    The ping-pong sparse kernels (pairs of query blocks) record workgroup 0's
+    per-wave phases like the dense kernel; read them with prof_read().
+    """
+    q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
+    lut, counts = lut.contiguous(), counts.contiguous()
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    L = lib(profile=True)
+    with torch.cuda.device(q.device):
+        rc = L.h3a_attn_fwd_blocksparse(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Skv,
+                                        D, _bhs(q), _bhs(k), _bhs(v), _bhs(out), lut.data_ptr(), counts.data_ptr(),
+                                        int(blk_q), int(blk_k), int(lut.shape[3]), sc, _stream(q))
+    check("h3a_attn_fwd_blocksparse (profile build)", rc, L)
+    return out
+
+
 def prof_enabled(profile: bool = True) -> bool:
     """Whether the library (profile=True: the profile build) records phases."""
     return bool(lib(profile=profile).h3a_prof_enabled())

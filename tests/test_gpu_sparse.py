@@ -87,29 +87,31 @@ def test_sparse_unsupported_block_sizes_raise(gpu):
                                         cnt[:, :, :1].expand(1, 1, nqb).contiguous(), bq, bk)
 
 
-@pytest.mark.parametrize("S,blk_k", [(640, 128), (1300, 64), (131, 128)])
-def test_sparse_pairs_uneven_lists(gpu, S, blk_k):
-    """128-row query blocks run in pairs (blocks 2p and 2p+1 share a workgroup and step
-    through the longer of their two LUT lists).  Random keep counts from 0 to all key
-    blocks per row, so partners differ in length, some rows are empty (O = 0) and, with
-    an odd block count, the last block has no partner."""
-    rng = np.random.default_rng(7000 + S + blk_k)
+@pytest.mark.parametrize("S,blk_k,blk_q", [(640, 128, 128), (1300, 64, 128), (131, 128, 128),
+                                           (640, 64, 64), (1300, 128, 64), (131, 64, 64), (700, 256, 64)])
+def test_sparse_pairs_uneven_lists(gpu, S, blk_k, blk_q):
+    """Query blocks run in pairs (blocks 2p and 2p+1 share a workgroup and step through
+    the longer of their two LUT lists; 64-row blocks with each group's waves split over
+    the two key halves of a stage).  Random keep counts from 0 to all key blocks per row,
+    so partners differ in length, some rows are empty (O = 0) and, with an odd block
+    count, the last block has no partner."""
+    rng = np.random.default_rng(7000 + S + blk_k + blk_q)
     q, k, v = (randn_bf16(rng, (1, 2, S, 128)) for _ in range(3))
-    nq, nk = -(-S // 128), -(-S // blk_k)
+    nq, nk = -(-S // blk_q), -(-S // blk_k)
     bmap = np.zeros((1, 2, nq, nk), np.uint8)
     for h in range(2):
         for i in range(nq):
             n = int(rng.integers(0, nk + 1)) if i % 3 else 0
             bmap[0, h, i, rng.choice(nk, size=n, replace=False)] = 1
     lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
-    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, 128, blk_k)
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, blk_q, blk_k)
     got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
-    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=128, blk_k=blk_k)
-    assert_close_absmax(got, ref, what=f"sparse pairs S={S} blk_k={blk_k}")
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk_q, blk_k=blk_k)
+    assert_close_absmax(got, ref, what=f"sparse pairs S={S} blk_q={blk_q} blk_k={blk_k}")
     for h in range(2):
         for i in range(nq):
             if not bmap[0, h, i].any():
-                assert not got[0, h, 128 * i:128 * (i + 1)].any(), f"empty row h={h} block={i}"
+                assert not got[0, h, blk_q * i:blk_q * (i + 1)].any(), f"empty row h={h} block={i}"
 
 
 @pytest.mark.parametrize("S,blk_k", [(1300, 128), (2000, 64), (640, 64)])
