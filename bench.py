@@ -46,6 +46,35 @@ def measured_traffic():
     return None, "no roofline.traffic line"
 
 
+def _clock_from_rows(rows):
+    ghz = [r[7] / (r[8] * 10.0) for r in rows if r[8] > 0]
+    return (sum(ghz) / len(ghz), min(ghz), max(ghz)) if ghz else None
+
+
+def measure_clock_sparse(item, blk):
+    """As measure_clock, for the block-sparse kernel: one profiled launch of the first
+    layer's inputs (the ping-pong sparse kernels record workgroup 0's phases)."""
+    from h3attn import ops
+    try:
+        q, k, v, lut, cnt, _ = item
+        out = torch_empty_like(q)
+        ops.attn_fwd_blocksparse_profiled(q, k, v, lut, cnt, blk, blk, out=out)
+        ops.prof_reset()
+        ops.attn_fwd_blocksparse_profiled(q, k, v, lut, cnt, blk, blk, out=out)
+        c = _clock_from_rows(ops.prof_read())
+        if c is None:
+            return None, "no profile rows"
+        return c[0], (f"s_memtime / s_memrealtime over workgroup 0's stage loop, one profiled layer after the "
+                      f"timed steps; waves {c[1]:.3f}-{c[2]:.3f} GHz")
+    except (RuntimeError, ValueError) as e:
+        return None, f"not measured: {e}"
+
+
+def torch_empty_like(t):
+    import torch
+    return torch.empty_like(t)
+
+
 def measure_clock(torch, h3attn, dev, heads=H):
     """Shader clock under this workload, measured in this process: one dense layer of the
     same shape through the phase-profile build, whose workgroup 0 counts shader-clock
@@ -61,14 +90,12 @@ def measure_clock(torch, h3attn, dev, heads=H):
         ops.attn_fwd_profiled(q, k, v, out=out)  # warm: the clock settles under load
         ops.prof_reset()
         ops.attn_fwd_profiled(q, k, v, out=out)
-        rows = ops.prof_read()
-        ghz = [r[7] / (r[8] * 10.0) for r in rows if r[8] > 0]
+        c = _clock_from_rows(ops.prof_read())
         del q, k, v, out
-        if not ghz:
+        if c is None:
             return None, "no profile rows"
-        return sum(ghz) / len(ghz), (f"s_memtime / s_memrealtime over workgroup 0's stage loop, one profiled "
-                                     f"layer (H={heads}, S={S}) after the timed steps; waves "
-                                     f"{min(ghz):.3f}-{max(ghz):.3f} GHz")
+        return c[0], (f"s_memtime / s_memrealtime over workgroup 0's stage loop, one profiled "
+                      f"layer (H={heads}, S={S}) after the timed steps; waves {c[1]:.3f}-{c[2]:.3f} GHz")
     except (RuntimeError, ValueError) as e:
         return None, f"not measured: {e}"
 
@@ -159,7 +186,7 @@ def _parse():
                          "prologue + attention on the fused QKV layout at S=8192, H=56; graph: "
                          "--layers layers of prologue + attention at S=2048, H=4, eager vs one "
                          "HIP-graph replay (launch overhead)")
-    ap.add_argument("--blk", type=int, default=128, choices=[64, 128],
+    ap.add_argument("--blk", type=int, default=128, choices=[64, 128, 192, 256],
                     help="sparse: query and key tile size (128: the 128x128 workload; 64: the SLA "
                          "block size default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -305,6 +332,7 @@ def run_sparse(args, torch, h3attn, dev):
                 events[i][1].record(stream)
 
     wall, avg_kernel_ms = _timed(step, args.steps, args.warmup, L, torch, stream)
+    ghz, clock_note = measure_clock_sparse(items[0], blk) if not args.no_clock else (None, "skipped")
     flops = sum(it[5] for it in items) / L
     value = flops * L * args.steps / wall / 1e12
     achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
@@ -320,11 +348,17 @@ def run_sparse(args, torch, h3attn, dev):
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": ("attn_fwd_pingpong_kernel<PadLayout,2,sparse> (pairs of query blocks; "
-                                "+ split_combine_kernel for the split tail)" if blk == 128
-                                else "attn_fwd_kernel<4,PadLayout,regs,sparse,key-split>"), "flop_per_launch": flops,
-                     "avg_launch_ms": round(avg_kernel_ms, 3)},
+                     "kernel": ("attn_fwd_pingpong_kernel<SwzLayout,2,sparse> (pairs of 128-row query blocks; "
+                                "+ split_combine_kernel for the split tail)" if blk % 128 == 0
+                                else "attn_fwd_pingpong_kernel<SwzLayout,2,sparse,key-split> (pairs of 64-row "
+                                     "query blocks)"), "flop_per_launch": flops,
+                     "avg_launch_ms": round(avg_kernel_ms, 3),
+                     "clock_ghz_measured": None if ghz is None else round(ghz, 3), "clock_note": clock_note},
     })
+    if ghz:
+        peak_at_clock = FLOP_PER_CLK * ghz * 1e9 / 1e12
+        res["roofline"]["peak_at_measured_clock"] = round(peak_at_clock, 1)
+        res["roofline"]["frac_at_measured_clock"] = round(achieved / peak_at_clock, 4)
     return res
 
 
