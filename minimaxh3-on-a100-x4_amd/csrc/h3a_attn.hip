@@ -139,18 +139,25 @@ namespace h3a {
 // Dense ping-pong fetch split: instructions of each K and V stage (4 per wave
 // column: waves w and w+4 of the two groups) that the group-A wave issues
 // (H3A_PP_A_KINST of K, H3A_PP_A_VINST of V); the group-B wave issues the
-// rest.  -1: every wave issues 2 + 2 over an 8-wave layout.  Default: group B
-// fetches everything, at the top of its softmax cluster.
+// rest, at the top of its softmax cluster.  -1: every wave issues 2 + 2 over
+// an 8-wave layout.  Default: group B fetches K, group A fetches V at the top
+// of its own softmax cluster (H3A_PP_A_SOFT), so each softmax slot carries
+// half of the fetch.
 #ifndef H3A_PP_A_KINST
 #define H3A_PP_A_KINST 0
 #endif
 #ifndef H3A_PP_A_VINST
-#define H3A_PP_A_VINST 0
+#define H3A_PP_A_VINST 4
 #endif
 // 1: group A issues its share of the fetch after its matrix cluster (while
 // the last MFMAs drain) instead of before it.
 #ifndef H3A_PP_A_LATE
 #define H3A_PP_A_LATE 0
+#endif
+// 1: group A issues its share of the fetch at the top of its softmax slot
+// (after the mid-stage barrier, while group B's MFMAs run) instead.
+#ifndef H3A_PP_A_SOFT
+#define H3A_PP_A_SOFT 1
 #endif
 // Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
 // during the softmax cluster (2), or never (0).
@@ -158,9 +165,12 @@ namespace h3a {
 #define H3A_PP_PRIO 1
 #endif
 // Workgroup barrier between the two clusters of a ping-pong stage (1), or
-// only the one at the end of the stage (0), which the LDS buffers need.
+// only the one at the end of the stage (0), which the LDS buffers need.  The
+// end barrier alone keeps the groups one cluster apart once each softmax slot
+// carries half of the fetch; with group B fetching everything the mid barrier
+// paid for itself.
 #ifndef H3A_PP_MID_BARRIER
-#define H3A_PP_MID_BARRIER 1
+#define H3A_PP_MID_BARRIER 0
 #endif
 // LDS operand reads issued after each MFMA of a ping-pong matrix cluster.
 #ifndef H3A_PP_READS_PER_MFMA
@@ -1022,32 +1032,40 @@ __device__ __forceinline__ void slot_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// The boundary between the two clusters of a ping-pong stage.
+// The boundary between the two clusters of a ping-pong stage: a workgroup
+// barrier when kNeeded (the block-sparse kernels: there group B waits for its
+// own fetch right before it, and the barrier is what makes every wave's fetch
+// visible to the group's next matrix cluster) or when H3A_PP_MID_BARRIER asks
+// for one; otherwise only a scheduling fence.
+template <bool kNeeded>
 __device__ __forceinline__ void mid_barrier() {
-#if H3A_PP_MID_BARRIER
-  slot_barrier();
-#else
-  __builtin_amdgcn_sched_barrier(0);
-#endif
+  if constexpr (kNeeded || H3A_PP_MID_BARRIER) {
+    slot_barrier();
+  } else {
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // Dense ping-pong kernel: 8 waves x 32 query rows (one 256-row query tile per
 // workgroup); waves 0-3 (group A) and 4-7 (group B) sit one of each per SIMD.
 // Every stage of BN = 32*NSUB keys is split into a matrix-core cluster,
 // MFMA(j): S(j+1) = K(j+1) Q^T and O += V(j) P(j), and a softmax cluster,
-// SOFT(j): S(j+1) -> P(j+1), with a workgroup barrier after each.  Group B
-// runs one cluster behind group A, so on every SIMD one wave issues MFMAs
-// while the other issues the softmax's VALU work and the two pipes overlap.
+// SOFT(j): S(j+1) -> P(j+1).  Group B runs one cluster behind group A, so on
+// every SIMD one wave issues MFMAs while the other issues the softmax's VALU
+// work and the two pipes overlap.  A workgroup barrier ends every stage (and,
+// in the block-sparse kernels or with H3A_PP_MID_BARRIER, also separates its
+// two clusters).
 //
-// Barrier slots after the prologue (both groups pass the same barriers):
-//   slot 2j+1:  A: MFMA(j)                    B: DMA(j), SOFT(j-1)
-//   slot 2j+2:  A: SOFT(j)                    B: MFMA(j), wait for DMA(j)
-// DMA(j) fetches K(j+2) into kbuf[j&1] and V(j+1) into vbuf[(j+1)&1]; the 4
-// waves of group B split each tile (H3A_PP_A_KINST / H3A_PP_A_VINST give part
-// of it to group A instead).  Those buffers were last read by MFMA(j-1), which
-// both groups finished by the end of slot 2j; the data is read by MFMA(j+1)
-// from slot 2j+3 on, after every wave waited for its share of the DMA at the
-// end of slot 2j+2.
+// Slots of stage j after the prologue:
+//   slot 2j+1:  A: MFMA(j)                        B: DMA K(j+2), SOFT(j-1)
+//   slot 2j+2:  A: DMA V(j+1), SOFT(j), wait      B: MFMA(j), wait
+// K(j+2) goes to kbuf[j&1] and V(j+1) to vbuf[(j+1)&1] (by default group B
+// fetches K and group A fetches V, each at the top of its softmax cluster;
+// H3A_PP_A_KINST / H3A_PP_A_VINST / H3A_PP_A_SOFT move the split).  Those
+// buffers were last read by MFMA(j-1), which both groups finished before the
+// barrier that ended stage j-1; the data is read by MFMA(j+1) in stage j+1,
+// after every wave waited for its share of the fetch before the barrier that
+// ends stage j.
 //
 // kSparse: block-sparse attention over pairs of query blocks.  Group A takes
 // query block 2p and group B block 2p+1 of pair p, each with its own LUT row
@@ -1406,6 +1424,10 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     vdma.template issue_range<I0, I1>(Vb, a.vss, key_v, a.Skv, vbuf[P ^ 1]);
   };
   constexpr bool kALate = kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
+  // Group A's share at the top of its softmax slot: the buffers it fills were
+  // last read in MFMA(j-1), and it waits for the share before the barrier
+  // that ends the slot, as for any share.
+  constexpr bool kASoft = kSplitDma && !kALate && H3A_PP_A_SOFT && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
   // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
@@ -1470,7 +1492,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         dma_k(std::false_type{}, par);
         dma_v(std::false_type{}, par);
         pc.mark(0);
-        mid_barrier();
+        mid_barrier<kSparse>();
         pc.mark(2);
         dma_k(std::true_type{}, par);
         dma_v(std::true_type{}, par);
@@ -1493,7 +1515,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
           if constexpr (kEarly == 1) load_v();
         }
         pc.mark(0);
-        mid_barrier();
+        mid_barrier<kSparse>();
         pc.mark(2);
         if constexpr (kEarly == 0) {
           stage_keys(j);
@@ -1510,7 +1532,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         pc.stage_done();
         return;
       }
-      if constexpr (!kALate) dma(par, j);
+      if constexpr (!kALate && !kASoft) dma(par, j);
       pc.mark(0);
       mfma(par);
       if constexpr (kALate) {
@@ -1518,8 +1540,12 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         dma(par, j);
       }
       pc.mark(1);
-      mid_barrier();
+      mid_barrier<kSparse>();
       pc.mark(2);
+      if constexpr (kASoft) {
+        dma(par, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (j + 1 < niter) soft(j);
       pc.mark(3);
       wait_vmem_all();
@@ -1548,7 +1574,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         // issued at the top of this stage may stay in flight.
         wait_vmem_le<kDmaTop>();
         pc.mark(4);
-        mid_barrier();
+        mid_barrier<kSparse>();
         pc.mark(2);
         mfma(par);
         pc.mark(3);
@@ -1571,7 +1597,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
         pc.mark(1);
         stage_out(par);
         pc.mark(4);
-        mid_barrier();
+        mid_barrier<kSparse>();
         pc.mark(2);
         // kEarly == 3: the loads for stage j+1 go inside the matrix cluster,
         // also after the last stage (keys past the list: nothing is read).
@@ -1593,7 +1619,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       pc.mark(0);
       if constexpr (!decltype(first)::value) soft(j - 1);
       pc.mark(1);
-      mid_barrier();
+      mid_barrier<kSparse>();
       pc.mark(2);
       mfma(par);
       pc.mark(3);
