@@ -79,9 +79,12 @@ int h3a_attn_fwd(const void *q, const void *k, const void *v, void *o,
  * library).  With it, the query tiles of the last, partly filled round of
  * workgroups are split into key ranges that run side by side and are merged
  * by a second kernel on the same stream; results equal h3a_attn_fwd's within
- * floating-point rounding.  h3a_attn_fwd_workspace_size gives the bytes
- * needed for a problem on the current device (0: nothing is split, and
- * workspace may be NULL).  The workspace must stay untouched until the call's
+ * floating-point rounding.  Problems of four or more rounds of tiles also
+ * run on a persistent grid whose workgroups take tiles from per-XCD work
+ * queues (1 KiB of counters in the workspace, cleared by the call itself
+ * with a kernel before the attention launch).  h3a_attn_fwd_workspace_size
+ * gives the bytes needed for a problem on the current device (0: nothing is
+ * split or queued, and workspace may be NULL).  The workspace must stay untouched until the call's
  * work on `stream` has completed, and two calls in flight at once need two
  * workspaces.  Same arguments and errors as h3a_attn_fwd, plus
  * H3A_ERR_INVALID_ARG for a missing or short workspace.  This entry point has
@@ -97,20 +100,21 @@ int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o,
 
 /*
  * h3a_attn_fwd_ws without a workspace argument and without any allocation:
- * the split-tail partials go to a static device array of
- * H3A_NOALLOC_SCRATCH_BYTES (32.5 MiB) that each GPU the library runs on holds
+ * the split-tail partials and the work queues' counters go to a static device
+ * array of H3A_NOALLOC_SCRATCH_BYTES (32.5 MiB + 1 KiB) that each GPU the library runs on holds
  * until the process ends.  No counterpart in the reference: it is for callers
  * that cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It calls no hipMalloc/hipFree and no
  * allocating library routine.  Every call on a GPU shares that GPU's array, so
  * calls that overlap on one GPU (other streams, other threads) race: the
  * caller must serialise them.  Every byte the merge reads is written earlier
- * by the same call, so nothing needs clearing between calls.  A split tail
+ * by the same call, and the call clears the queue counters itself (with a
+ * kernel, not a memset), so nothing needs clearing between calls.  A split tail
  * larger than the array (a device with more than 256 CUs) gives
  * H3A_ERR_UNSUPPORTED.  Same kernels and split plan as h3a_attn_fwd_ws, so the
  * results are equal bit for bit; same arguments and errors as h3a_attn_fwd.
  */
-#define H3A_NOALLOC_SCRATCH_BYTES 34078720u
+#define H3A_NOALLOC_SCRATCH_BYTES 34079744u
 int h3a_attn_fwd_noalloc(const void *q, const void *k, const void *v, void *o,
                          int B, int H, int Sq, int Skv, int D,
                          const int64_t q_strides[3], const int64_t k_strides[3],

@@ -72,13 +72,15 @@ int check_attn(const void *q, const void *k, const void *v, void *o, int B, int 
 
 // Scratch of the allocation-free dense entry point (h3a_attn_fwd_noalloc): the
 // split-tail partials, (O row, m, l) in fp32 for each of the r * P key ranges
-// of the last round's tiles.  r * P <= CUs (P = CUs / r at most), so on a
-// 256-CU device no plan needs more than 256 * 256 * (128 + 2) floats.  Each GPU
+// of the last round's tiles, then 1 KiB of work-queue counters.  r * P <= CUs
+// (P = CUs / r at most), so on a 256-CU device no plan needs more than
+// 256 * 256 * (128 + 2) floats + 1 KiB.  Each GPU
 // holds its own copy until the process ends.  In host code `scratch` only
 // names the symbol; its device address comes from hipGetSymbolAddress, once per
 // device (scratch_ptr).
 constexpr size_t kScratchBytes = H3A_NOALLOC_SCRATCH_BYTES;
-static_assert(kScratchBytes == (size_t)256 * 256 * (128 + 2) * sizeof(float), "256-CU split tail");
+static_assert(kScratchBytes == (size_t)256 * 256 * (128 + 2) * sizeof(float) + 1024,
+              "256-CU split tail, then the dense work queues' counters");
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 constexpr int kMaxDevices = 64;
@@ -120,7 +122,7 @@ void fill_attn_args(AttnArgs &a, const void *q, const void *k, const void *v, vo
   a.sl2 = scale * 1.4426950408889634f;
   a.lut = nullptr; a.counts = nullptr; a.lut_stride = 0; a.sub = 1; a.blk_k = 64;
   a.nkb = 0; a.nqb = 0; a.qmul = 1;
-  a.split_first = INT_MAX; a.split_pieces = 1; a.ws = nullptr;
+  a.split_first = INT_MAX; a.split_pieces = 1; a.ws = nullptr; a.sched = nullptr;
 }
 
 }  // namespace
@@ -157,9 +159,9 @@ int h3a_attn_fwd_noalloc(const void *q, const void *k, const void *v, void *o, i
   rc = plan_attn_split(B, H, Sq, Skv, &plan);
   if (rc) return rc;
   void *ws = nullptr;
-  if (plan.pieces > 1) {
+  if (plan.bytes > 0) {
     if (plan.bytes > kScratchBytes)
-      return fail(H3A_ERR_UNSUPPORTED, "split tail needs %zu bytes of scratch; the static array holds %zu",
+      return fail(H3A_ERR_UNSUPPORTED, "split tail and queues need %zu bytes of scratch; the static array holds %zu",
                   plan.bytes, kScratchBytes);
     rc = scratch_ptr(&ws);
     if (rc) return rc;
@@ -192,7 +194,7 @@ int h3a_attn_fwd_ws(const void *q, const void *k, const void *v, void *o, int B,
   SplitPlan plan;
   rc = plan_attn_split(B, H, Sq, Skv, &plan);
   if (rc) return rc;
-  if (plan.pieces > 1) {
+  if (plan.bytes > 0) {
     if (!workspace || workspace_bytes < plan.bytes)
       return fail(H3A_ERR_INVALID_ARG, "workspace of %zu bytes needed, %zu given", plan.bytes,
                   workspace ? workspace_bytes : (size_t)0);

@@ -55,6 +55,11 @@ namespace h3a {
 #ifndef H3A_XCD_REMAP
 #define H3A_XCD_REMAP 1
 #endif
+// Dense problems of several rounds of tiles on a persistent grid fed by
+// per-XCD work queues (1), or one tile per workgroup (0).
+#ifndef H3A_DENSE_QUEUES
+#define H3A_DENSE_QUEUES 1
+#endif
 // Scheduling-group hints interleaving MFMA / LDS reads / VALU in the stage body.
 #ifndef H3A_SCHED_HINTS
 #define H3A_SCHED_HINTS 0
@@ -191,6 +196,12 @@ namespace h3a {
 // the shader clock at its cluster boundaries (see PhaseClock).
 #ifndef H3A_PROFILE
 #define H3A_PROFILE 0
+#endif
+// Tuning builds only: every workgroup records its start and end
+// (s_memrealtime) and its XCC / hardware ids in g_timeline, read back with
+// h3a_timeline_read (exported only by such builds).
+#ifndef H3A_TIMELINE
+#define H3A_TIMELINE 0
 #endif
 
 constexpr int kD = 128;
@@ -952,13 +963,14 @@ __device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0,
 // Phase profile of the dense ping-pong kernel (H3A_PROFILE builds; every
 // method compiles to nothing otherwise).  Workgroup 0's 8 waves each sum
 // s_memtime ticks (the shader clock) per phase of their stage loop, in
-// registers, and store them once after the loop, one row per wave:
+// registers, and store them once after the loop, one row per wave (with
+// dynamic dispatch, for the last work item workgroup 0 ran):
 //   [0] DMA issue, and the loop's own branch   [1] first cluster
 //   [2] mid-stage barrier                       [3] second cluster
 //   [4] wait for the DMA (vmcnt)                [5] end-of-stage barrier
 //   [6] stages run                              [7] loop, s_memtime ticks
 //   [8] loop, s_memrealtime ticks (100 MHz)     [9] epilogue (normalise, store)
-//   [10] prologue (kernel start to loop start)
+//   [10] prologue (work item start to loop start)
 // Group A's first cluster is its matrix cluster (QK^T and PV MFMAs, which are
 // interleaved and cannot be timed apart) and its second the softmax; group B
 // the other way round.  Phases [0]-[5] tile the loop: their sum is [7].
@@ -966,11 +978,22 @@ constexpr int kProfSlots = H3A_PROF_SLOTS;
 static_assert(H3A_PROF_WAVES == 8, "one row per wave of the dense workgroup");
 __device__ unsigned long long g_prof[H3A_PROF_WAVES][kProfSlots];
 
+constexpr int kTimelineMax = 1 << 16;
+#if H3A_TIMELINE
+__device__ unsigned long long g_timeline[kTimelineMax][4];
+#endif
+
 struct PhaseClock {
   uint32_t ph[kProfSlots];  // a phase sums < 2^32 ticks for any stage count here
-  uint64_t last, t_loop, rt_loop;
+  uint64_t last, t_loop, rt_loop, t_start, c_start;
+  int index;  // work item (timeline builds)
   bool on;
-  __device__ __forceinline__ void begin(bool enabled) {
+  __device__ __forceinline__ void begin(bool enabled, int item) {
+    if constexpr (H3A_TIMELINE) {
+      t_start = __builtin_amdgcn_s_memrealtime();
+      c_start = __builtin_amdgcn_s_memtime();
+      index = item;
+    }
     if constexpr (H3A_PROFILE) {
       on = enabled;
 #pragma unroll
@@ -1006,6 +1029,18 @@ struct PhaseClock {
   }
   // After the epilogue's stores: phase 9, then one row per wave to g_prof.
   __device__ __forceinline__ void finish(int wave, int lane) {
+#if H3A_TIMELINE
+    if (wave == 0 && lane == 0 && index < kTimelineMax) {
+      const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
+      const uint64_t c_end = __builtin_amdgcn_s_memtime();
+      const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_ID
+      const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // XCC_ID
+      g_timeline[index][0] = t_start;
+      g_timeline[index][1] = t_end;
+      g_timeline[index][2] = ((uint64_t)xcc << 32) | hw;
+      g_timeline[index][3] = c_end - c_start;
+    }
+#endif
     if constexpr (H3A_PROFILE) {
       if (on) {
         ph[9] = (uint32_t)(__builtin_amdgcn_s_memtime() - last);
@@ -1089,24 +1124,69 @@ __device__ __forceinline__ void mid_barrier() {
 // score sub-tile, 16 MFMAs per stage) with its own running max, row sum and
 // O; after the loop the key-half-1 wave hands (O, m, l) to its partner
 // through LDS, which merges them as the split-tail combine does.
-template <class L, int NSUB, bool kSparse = false, bool kKeySplit = false>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-attn_fwd_pingpong_kernel(AttnArgs a) {
+// Dynamic dispatch of the ping-pong kernel: kQueues queues, one per XCD.
+// Queue x holds XCD x's share of the whole work items (the contiguous range
+// xcd_remap deals it: consecutive query tiles of the same heads, whose K/V
+// the XCD's L2 then shares) followed by its share of the split pieces.  A
+// workgroup takes items from its own XCD's queue and, once that is empty,
+// from the others in turn, so XCDs that run at a higher clock finish the
+// slower ones' work instead of idling.  Each queue is a counter (one 128-byte
+// line each) that sched_clear_kernel zeroes before the launch.
+constexpr int kQueues = 8;
+constexpr int kQueueStride = 32;  // ints
+constexpr size_t kSchedBytes = (size_t)kQueues * kQueueStride * sizeof(int);
+
+struct QueueShare {
+  int first, len;
+};
+__device__ __forceinline__ QueueShare queue_share(int n, int x) {
+  const int per = n / kQueues, rem = n % kQueues;
+  return {x * per + (x < rem ? x : rem), per + (x < rem ? 1 : 0)};
+}
+
+// The next work item for a workgroup on XCD xcc (items 0..whole-1 are whole
+// tiles, whole + p is split piece p), or -1 when every queue is empty.
+__device__ __forceinline__ int take_item(int *sched, int whole, int pieces, int xcc) {
+  for (int t = 0; t < kQueues; ++t) {
+    const int x = (xcc + t) & (kQueues - 1);
+    const QueueShare sw = queue_share(whole, x), sp = queue_share(pieces, x);
+    const int len = sw.len + sp.len;
+    int *ctr = sched + x * kQueueStride;
+    if (t > 0 && __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= len) continue;
+    const int i = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (i < len) return i < sw.len ? sw.first + i : whole + sp.first + (i - sw.len);
+  }
+  return -1;
+}
+
+template <class L, int NSUB, bool kSparse>
+struct PingPongLds {
+  static constexpr int kKE = StageBytes<L, 32 * NSUB>::kK / 2;  // elements
+  static constexpr int kVE = StageBytes<L, 32 * NSUB>::kV / 2;
+  static constexpr int NG = kSparse ? 2 : 1;  // K/V streams: one per group (sparse)
+  uint16_t k[NG][2][kKE];
+  uint16_t v[NG][2][kVE];
+};
+
+// One work item of attn_fwd_pingpong_kernel: a 256-row query tile, a key
+// range of a split tile, or (sparse) a pair of query blocks or a piece of one.
+// `remapped`: the item number is already XCD-aware (taken from the queues),
+// so whole tiles are not remapped.
+template <class L, int NSUB, bool kSparse, bool kKeySplit>
+__device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item, const bool remapped,
+                                              PingPongLds<L, NSUB, kSparse> &lds, PhaseClock &pc) {
   constexpr int NW = 8;
   constexpr int BN = 32 * NSUB;  // keys per stage
   constexpr int WS = kKeySplit ? 1 : NSUB;  // 32-key score sub-tiles per wave and stage
   constexpr int QB = kKeySplit ? 64 : 128;  // sparse: query rows per group
-  constexpr int kKE = StageBytes<L, BN>::kK / 2, kVE = StageBytes<L, BN>::kV / 2;  // elements
-  constexpr int NG = kSparse ? 2 : 1;  // K/V streams: one per group (sparse)
+  constexpr int kKE = PingPongLds<L, NSUB, kSparse>::kKE, kVE = PingPongLds<L, NSUB, kSparse>::kVE;
   static_assert(!kSparse || BN == kBN, "block-sparse stages are 64 keys");
   static_assert(!kKeySplit || (kSparse && NSUB == 2), "key-split pairs are block-sparse, 64-key stages");
   constexpr bool kSpDma = kSparse && H3A_SPARSE_PP_DMA;  // sparse stages fetched by LDS DMA
   static_assert(!kSparse || kSpDma || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf_all[NG][2][kKE];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf_all[NG][2][kVE];
+  auto &kbuf_all = lds.k;
+  auto &vbuf_all = lds.v;
 
-  PhaseClock pc;
-  pc.begin(blockIdx.x == 0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -1122,19 +1202,21 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   // Sparse pairs split the same way, each piece taking the same fraction of
   // each group's own stage list (split_part).
   int w, piece = -1, j0 = 0, niter = nstages, split_part = -1;
-  if (kSparse && (int)blockIdx.x >= a.split_first) {
-    piece = blockIdx.x - a.split_first;
+  if (kSparse && item >= a.split_first) {
+    piece = item - a.split_first;
     w = a.split_first + piece / a.split_pieces;
     split_part = piece % a.split_pieces;
-  } else if (kSparse || (int)blockIdx.x < a.split_first) {
+  } else if (kSparse || item < a.split_first) {
     const int whole = a.split_first < a.total ? a.split_first : a.total;
 #if H3A_XCD_REMAP
-    w = xcd_remap(blockIdx.x, whole);
+    w = remapped ? item : xcd_remap(item, whole);
 #else
-    w = blockIdx.x;
+    w = item;
+    (void)whole;
+    (void)remapped;
 #endif
   } else {
-    piece = blockIdx.x - a.split_first;
+    piece = item - a.split_first;
     w = a.split_first + piece / a.split_pieces;
     const int p = piece % a.split_pieces;
     j0 = (int)((int64_t)nstages * p / a.split_pieces);
@@ -1716,6 +1798,62 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   pc.finish(wave, lane);
 }
 
+template <class L, int NSUB, bool kSparse = false, bool kKeySplit = false>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+attn_fwd_pingpong_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) PingPongLds<L, NSUB, kSparse> lds;
+  __shared__ int next_item;
+  PhaseClock pc;
+  // Static dispatch (a.sched null): work item blockIdx.x.  Dynamic dispatch:
+  // a persistent grid whose workgroups take items from the queues until all
+  // are empty; the barriers around the take keep every wave of the previous
+  // item clear of the LDS before the next item's first fetch lands there.
+  // Each item reads the arguments afresh from the kernarg segment, through a
+  // pointer the compiler cannot follow across iterations: kept in SGPRs over
+  // the whole loop instead, they push the stage loop's register allocation
+  // into waiting for every LDS operand read (lgkmcnt(0) before each MFMA).
+  // The block-sparse kernels run one item per workgroup.
+  if constexpr (kSparse) {
+    pc.begin(blockIdx.x == 0, blockIdx.x);
+    pingpong_item<L, NSUB, kSparse, kKeySplit>(a, blockIdx.x, false, lds, pc);
+    return;
+  }
+  typedef const __attribute__((address_space(4))) AttnArgs *KernargPtr;
+  for (int item = blockIdx.x;;) {
+    KernargPtr kp = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kp));
+    static_assert(sizeof(AttnArgs) % 4 == 0, "kernel arguments copied as words");
+    typedef const __attribute__((address_space(4))) uint32_t *KernargWords;
+    uint32_t words[sizeof(AttnArgs) / 4];
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(AttnArgs) / 4); ++i) words[i] = ((KernargWords)kp)[i];
+    AttnArgs args;
+    __builtin_memcpy(&args, words, sizeof(args));
+    if (args.sched) {
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const int xcc = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & (kQueues - 1));  // XCC_ID
+        const int whole = args.split_first < args.total ? args.split_first : args.total;
+        next_item = take_item(args.sched, whole, args.total - whole, xcc);
+      }
+      __syncthreads();
+      item = __builtin_amdgcn_readfirstlane(next_item);
+      if (item < 0) break;
+    }
+    pc.begin(blockIdx.x == 0, item);
+    pingpong_item<L, NSUB, kSparse, kKeySplit>(args, item, args.sched != nullptr, lds, pc);
+    KernargPtr kq = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kq));
+    if (!kq->sched) break;
+  }
+}
+
+// Clears the dispatch queues' counters before a dynamic launch (a kernel, not
+// a memset, so the pair can be captured in a graph).
+__global__ void __launch_bounds__(256) sched_clear_kernel(int *sched) {
+  if (threadIdx.x < kQueues * kQueueStride) sched[threadIdx.x] = 0;
+}
+
 // Merge the key-range pieces of the split tiles:
 //   O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p,  M = max_p m_p.
 // One thread per (split tile, row, 4 dims); 8 rows per 256-thread block.
@@ -1874,9 +2012,13 @@ static int device_cu_count(int *cus_out) {
 }
 
 // `tiles` 256-row work items of up to `stages` stages each, split when
-// `splittable`.
-static int plan_tiles(int64_t tiles, int stages, bool splittable, SplitPlan *plan) {
+// `splittable`.  With `queued`, problems of at least kQueuedRounds rounds of
+// tiles run on a persistent grid fed by the per-XCD queues (take_item): the
+// XCDs' clocks differ under full load by up to ~5 %, and with a static
+// deal the fastest XCD idles while the slowest finishes its share.
+static int plan_tiles(int64_t tiles, int stages, bool splittable, bool queued, SplitPlan *plan) {
   constexpr int kMinSplitStages = 4;
+  constexpr int64_t kQueuedRounds = 4;
   int cus = 0;
   const int rc = device_cu_count(&cus);
   if (rc) return rc;
@@ -1886,20 +2028,25 @@ static int plan_tiles(int64_t tiles, int stages, bool splittable, SplitPlan *pla
     const int64_t by_cus = cus / r, by_len = stages / kMinSplitStages;
     pieces = (int)(by_cus < by_len ? by_cus : by_len);
   }
-  if (tiles > INT_MAX || pieces < 2) {
-    *plan = SplitPlan{(int)(tiles > INT_MAX ? INT_MAX : tiles), (int)(tiles > INT_MAX ? INT_MAX : tiles), 1, 0};
-    return H3A_OK;
+  const int clamped = (int)(tiles > INT_MAX ? INT_MAX : tiles);
+  *plan = SplitPlan{clamped, clamped, 1, 0, false, 0};
+  if (tiles > INT_MAX) return H3A_OK;
+  if (pieces >= 2) {
+    plan->first = (int)(tiles - r);
+    plan->pieces = pieces;
+    plan->bytes = (size_t)r * pieces * 256 * (kD + 2) * sizeof(float);
   }
-  plan->tiles = (int)tiles;
-  plan->first = (int)(tiles - r);
-  plan->pieces = pieces;
-  plan->bytes = (size_t)r * pieces * 256 * (kD + 2) * sizeof(float);
+  if (queued && tiles >= kQueuedRounds * cus) {
+    plan->dynamic = true;
+    plan->sched_off = (plan->bytes + 255) & ~(size_t)255;
+    plan->bytes = plan->sched_off + kSchedBytes;
+  }
   return H3A_OK;
 }
 
 int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
   return plan_tiles((int64_t)B * H * ((Sq + 255) / 256), (Skv + H3A_DENSE_BN - 1) / H3A_DENSE_BN,
-                    H3A_DENSE_PINGPONG, plan);
+                    H3A_DENSE_PINGPONG, H3A_DENSE_PINGPONG && H3A_DENSE_QUEUES, plan);
 }
 
 // The longest list a query block can hold (max_k_blocks key blocks) stands in
@@ -1908,21 +2055,54 @@ int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k
   const int rows = sparse_sub_block_rows(blk_q);
   const int64_t nsub = (Sq + rows - 1) / rows;
   return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_k_blocks * (blk_k / 64),
-                    H3A_SPARSE_PINGPONG && rows == 128, plan);
+                    H3A_SPARSE_PINGPONG && rows == 128, false, plan);
+}
+
+// Workgroups of a persistent launch of `kernel` (512 threads): every CU
+// filled to its occupancy, cached per device.
+static int persistent_grid(const void *kernel, int *grid) {
+  static std::atomic<int> grid_cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(H3A_ERR_HIP, "hipGetDevice failed");
+  int n = (dev >= 0 && dev < 64) ? grid_cache[dev].load(std::memory_order_relaxed) : 0;
+  if (n <= 0) {
+    int cus = 0, per_cu = 0;
+    const int rc = device_cu_count(&cus);
+    if (rc) return rc;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 512, 0) != hipSuccess || per_cu <= 0)
+      return fail(H3A_ERR_HIP, "hipOccupancyMaxActiveBlocksPerMultiprocessor failed");
+    n = cus * per_cu;
+    if (dev >= 0 && dev < 64) grid_cache[dev].store(n, std::memory_order_relaxed);
+  }
+  *grid = n;
+  return H3A_OK;
 }
 
 int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s) {
-  if (plan.pieces < 2) return launch_attn_dense(a, s);
+  if (plan.pieces < 2 && !plan.dynamic) return launch_attn_dense(a, s);
   a.nqt = (a.Sq + 255) / 256;
-  a.split_first = plan.first;
-  a.split_pieces = plan.pieces;
-  a.ws = static_cast<float *>(ws);
+  if (plan.pieces >= 2) {
+    a.split_first = plan.first;
+    a.split_pieces = plan.pieces;
+    a.ws = static_cast<float *>(ws);
+  }
   const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
   a.total = (int)total;
-  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>), dim3(a.total), dim3(512), 0, s, a);
-  int rc = check_launch("attn_fwd_pingpong_kernel<split>");
-  if (rc) return rc;
+  auto kernel = attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>;
+  int grid = a.total, rc;
+  if (plan.dynamic) {
+    rc = persistent_grid(reinterpret_cast<const void *>(kernel), &grid);
+    if (rc) return rc;
+    if (grid > a.total) grid = a.total;
+    a.sched = reinterpret_cast<int *>(static_cast<char *>(ws) + plan.sched_off);
+    hipLaunchKernelGGL(sched_clear_kernel, dim3(1), dim3(256), 0, s, a.sched);
+    rc = check_launch("sched_clear_kernel");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(512), 0, s, a);
+  rc = check_launch("attn_fwd_pingpong_kernel<split>");
+  if (rc || plan.pieces < 2) return rc;
   const int64_t rows = (int64_t)(plan.tiles - plan.first) * 256;
   hipLaunchKernelGGL(split_combine_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, a);
   return check_launch("split_combine_kernel");
@@ -2017,6 +2197,15 @@ int attn_prof_read(uint64_t *out) {
     return fail(H3A_ERR_HIP, "hipMemcpyFromSymbol(g_prof) failed");
   return H3A_OK;
 }
+
+#if H3A_TIMELINE
+extern "C" int h3a_timeline_read(unsigned long long *out, int n) {
+  if (hipDeviceSynchronize() != hipSuccess) return H3A_ERR_HIP;
+  const size_t bytes = sizeof(unsigned long long) * 4 * (size_t)(n < kTimelineMax ? n : kTimelineMax);
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_timeline), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess
+             ? H3A_OK : H3A_ERR_HIP;
+}
+#endif
 
 int attn_prof_reset() {
   static const unsigned long long zeros[H3A_PROF_WAVES][kProfSlots] = {};

@@ -45,6 +45,9 @@ struct AttnArgs {
   int split_first;
   int split_pieces;
   float *ws;
+  // dynamic dispatch (persistent grid, per-XCD work queues): the queues'
+  // counters, zeroed before the launch; null for one work item per workgroup
+  int *sched;
 };
 
 // Block sizes of the block-sparse path: multiples of the 64-key stage up to
@@ -59,7 +62,9 @@ struct SplitPlan {
   int tiles;    // B*H*query tiles
   int first;    // tiles run whole (the rest are split)
   int pieces;   // key ranges per split tile (1: no split)
-  size_t bytes; // workspace bytes
+  size_t bytes; // workspace bytes (split partials, then the queue counters)
+  bool dynamic; // persistent grid with per-XCD work queues
+  size_t sched_off;  // byte offset of the queue counters in the workspace
 };
 
 // Launchers implemented in h3a_attn.hip / h3a_prologue.hip.

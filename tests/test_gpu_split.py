@@ -79,3 +79,58 @@ def test_split_full_h3_shape_matches_unsplit(gpu):
     assert d.max().item() <= 1e-2 * ref and d.mean().item() <= 1e-4 * ref
     # the split tiles are the last ones of the last head: they must be the only ones that differ
     assert torch.equal(o_split[0, :H - 1], o_whole[0, :H - 1])
+
+
+def _ws_call(q, k, v, o, ws):
+    L = h3attn._lib.lib()
+    S3 = h3attn._lib.strides3
+    B, H, Sq, D = q.shape
+    st = [S3(*t.stride()[:3]) for t in (q, k, v, o)]
+    stream = h3attn.ops._stream(q)
+    rc = L.h3a_attn_fwd_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B, H, Sq, k.shape[2], D,
+                           *st, 1.0 / np.sqrt(D), ws.data_ptr(), ws.numel(), stream)
+    h3attn._lib.check("h3a_attn_fwd_ws", rc)
+
+
+def test_queued_dispatch_matches_one_tile_per_workgroup(gpu):
+    """Four rounds of tiles and more run on a persistent grid that takes tiles from per-XCD
+    queues (1 KiB of counters in the workspace).  Each tile's arithmetic is that of the
+    one-workgroup-per-tile launch, so without a split tail the outputs are equal bit for
+    bit, also when the workspace starts out holding garbage (the call clears the counters),
+    and on a second call over the first call's counters."""
+    cus = _cus()
+    B, H, Sq, Skv = 4, max(cus // 4, 1), 1024, 640  # 4 tiles per head: 4 * CUs tiles, no remainder
+    assert ops.attn_workspace_bytes(B, H, Sq, Skv) == 1024
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q, k, v = (torch.randn(B, H, n, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+               for n in (Sq, Skv, Skv))
+    want = ops.attn_fwd(q, k, v, split_tail=False)  # h3a_attn_fwd: one workgroup per tile
+    ws = torch.full((1024,), 0x7F, dtype=torch.uint8, device=gpu)
+    for call in range(2):
+        got = torch.full_like(q, float("nan"))
+        _ws_call(q, k, v, got, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"call {call}: queued dispatch differs from one tile per workgroup"
+
+
+def test_queued_dispatch_with_split_tail(gpu):
+    """Queues and a split tail together: the whole tiles match the unsplit kernel bit for
+    bit, the split ones (the last two heads) match it and the oracle at the attention
+    tolerance."""
+    cus = _cus()
+    H, Sq, Skv = cus // 4 + 2, 4000, 1024  # 16 tiles per head: 4 * CUs + 32 tiles
+    nbytes = ops.attn_workspace_bytes(1, H, Sq, Skv)
+    assert nbytes > 1024, "meant to split and queue"
+    rng = np.random.default_rng(17)
+    q = randn_bf16(rng, (1, H, Sq, 128))
+    k, v = randn_bf16(rng, (1, H, Skv, 128)), randn_bf16(rng, (1, H, Skv, 128))
+    qd, kd, vd = (to_dev_bf16(x, gpu) for x in (q, k, v))
+    o_split = ops.attn_fwd(qd, kd, vd)
+    o_whole = ops.attn_fwd(qd, kd, vd, split_tail=False)
+    torch.cuda.synchronize()
+    assert torch.equal(o_split[0, :H - 2], o_whole[0, :H - 2])
+    got = oracle.bf16_to_f32(from_dev_bf16(o_split[:, H - 2:].contiguous())).reshape(1, 2, Sq, 128)
+    assert_close_absmax(got, oracle.attn_fwd(q[:, H - 2:], k[:, H - 2:], v[:, H - 2:]),
+                        what="queued split heads vs oracle")
+    whole = oracle.bf16_to_f32(from_dev_bf16(o_whole[:, H - 2:].contiguous())).reshape(1, 2, Sq, 128)
+    assert_close_absmax(got, whole, what="queued split vs unsplit")

@@ -42,7 +42,7 @@ def test_noalloc_matches_workspace_entry_point(gpu):
         g = torch.Generator(device=gpu).manual_seed(seed)
         q, k, v = (torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
         nbytes = ops.attn_workspace_bytes(1, H, S, S)
-        assert 0 < nbytes <= 34078720, nbytes  # the split tail runs, within the static array
+        assert 0 < nbytes <= 34079744, nbytes  # the split tail runs, within the static array
         want = h3attn.attn_fwd(q, k, v, split_tail=True)  # h3a_attn_fwd_ws
         got = torch.full_like(q, float("nan"))
         torch.cuda.synchronize()
