@@ -147,9 +147,12 @@ int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *
  * blocks in the last, partly filled round of workgroups are each split into
  * ranges of their kept-block lists that run side by side, merged by a second
  * kernel on the same stream (results equal h3a_attn_fwd_blocksparse's within
- * floating-point rounding).  h3a_attn_fwd_blocksparse_workspace_size gives the
- * bytes needed on the current device (0: nothing is split, and workspace may
- * be NULL); the workspace rules are those of h3a_attn_fwd_ws.  This entry
+ * floating-point rounding).  Problems of four or more rounds of pairs run on
+ * a persistent grid fed by per-XCD work queues, as in h3a_attn_fwd_ws (1 KiB
+ * of counters in the workspace, cleared by the call).
+ * h3a_attn_fwd_blocksparse_workspace_size gives the bytes needed on the
+ * current device (0: nothing is split or queued, and workspace may be NULL);
+ * the workspace rules are those of h3a_attn_fwd_ws.  This entry
  * point has no counterpart in the reference; h3a_attn_fwd_blocksparse is the
  * drop-in for the h3_sla path.
  */

@@ -293,7 +293,7 @@ int h3a_attn_fwd_blocksparse_ws(const void *q, const void *k, const void *v, voi
   SplitPlan plan;
   rc = plan_attn_sparse_split(B, H, Sq, blk_q, blk_k, max_k_blocks, &plan);
   if (rc) return rc;
-  if (plan.pieces > 1) {
+  if (plan.bytes > 0) {
     if (!workspace || workspace_bytes < plan.bytes)
       return fail(H3A_ERR_INVALID_ARG, "workspace of %zu bytes needed, %zu given", plan.bytes,
                   workspace ? workspace_bytes : (size_t)0);

@@ -60,6 +60,10 @@ namespace h3a {
 #ifndef H3A_DENSE_QUEUES
 #define H3A_DENSE_QUEUES 1
 #endif
+// The same for the block-sparse ping-pong kernels (pairs of query blocks).
+#ifndef H3A_SPARSE_QUEUES
+#define H3A_SPARSE_QUEUES 1
+#endif
 // Scheduling-group hints interleaving MFMA / LDS reads / VALU in the stage body.
 #ifndef H3A_SCHED_HINTS
 #define H3A_SCHED_HINTS 0
@@ -1187,7 +1191,11 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   auto &kbuf_all = lds.k;
   auto &vbuf_all = lds.v;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  // Opaque to the compiler, so nothing computed from the lane index is hoisted
+  // out of the kernel's work-item loop to stay live through the stage loop.
+  int lane = tid & 63;
+  asm volatile("" : "+v"(lane));
   const int g = lane >> 5, l32 = lane & 31;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const bool lead = wave_u < NW / 2;  // group A
@@ -1245,7 +1253,10 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     // 128-row blocks of a pair share one row; blk_q = 192: three 64-row ones).
     auto stages_of = [&](int qb) __attribute__((always_inline)) -> int {
       if (qb >= a.nqt) return 0;
-      const int cnt = a.counts[(int64_t)bh * a.nqb + qb / a.qmul];
+      // Through the constant address space: the counts are not written during
+      // the kernel, so this stays a scalar load after an earlier work item's
+      // stores (a global pointer would have to be re-read per lane).
+      const int cnt = ((const __attribute__((address_space(4))) int32_t *)a.counts)[(int64_t)bh * a.nqb + qb / a.qmul];
       return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
     };
     auto part_of = [&](int n, int &first) __attribute__((always_inline)) -> int {
@@ -1812,12 +1823,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
   // pointer the compiler cannot follow across iterations: kept in SGPRs over
   // the whole loop instead, they push the stage loop's register allocation
   // into waiting for every LDS operand read (lgkmcnt(0) before each MFMA).
-  // The block-sparse kernels run one item per workgroup.
-  if constexpr (kSparse) {
-    pc.begin(blockIdx.x == 0, blockIdx.x);
-    pingpong_item<L, NSUB, kSparse, kKeySplit>(a, blockIdx.x, false, lds, pc);
-    return;
-  }
+  // With one item per workgroup the loop runs once.
   typedef const __attribute__((address_space(4))) AttnArgs *KernargPtr;
   for (int item = blockIdx.x;;) {
     KernargPtr kp = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
@@ -2054,17 +2060,20 @@ int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
 int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k_blocks, SplitPlan *plan) {
   const int rows = sparse_sub_block_rows(blk_q);
   const int64_t nsub = (Sq + rows - 1) / rows;
+  const bool pingpong = rows == 128 ? H3A_SPARSE_PINGPONG : H3A_SPARSE64_PINGPONG;
   return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_k_blocks * (blk_k / 64),
-                    H3A_SPARSE_PINGPONG && rows == 128, false, plan);
+                    H3A_SPARSE_PINGPONG && rows == 128, pingpong && H3A_SPARSE_QUEUES, plan);
 }
 
 // Workgroups of a persistent launch of `kernel` (512 threads): every CU
 // filled to its occupancy, cached per device.
-static int persistent_grid(const void *kernel, int *grid) {
-  static std::atomic<int> grid_cache[64];
+// `slot` names the kernel in the cache (0 dense, 1 sparse pairs, 2 sparse key-split).
+static int persistent_grid(const void *kernel, int slot, int *grid) {
+  static std::atomic<int> grid_cache[64][3];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(H3A_ERR_HIP, "hipGetDevice failed");
-  int n = (dev >= 0 && dev < 64) ? grid_cache[dev].load(std::memory_order_relaxed) : 0;
+  std::atomic<int> *cached = (dev >= 0 && dev < 64) ? &grid_cache[dev][slot] : nullptr;
+  int n = cached ? cached->load(std::memory_order_relaxed) : 0;
   if (n <= 0) {
     int cus = 0, per_cu = 0;
     const int rc = device_cu_count(&cus);
@@ -2072,7 +2081,7 @@ static int persistent_grid(const void *kernel, int *grid) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 512, 0) != hipSuccess || per_cu <= 0)
       return fail(H3A_ERR_HIP, "hipOccupancyMaxActiveBlocksPerMultiprocessor failed");
     n = cus * per_cu;
-    if (dev >= 0 && dev < 64) grid_cache[dev].store(n, std::memory_order_relaxed);
+    if (cached) cached->store(n, std::memory_order_relaxed);
   }
   *grid = n;
   return H3A_OK;
@@ -2092,7 +2101,7 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
   auto kernel = attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>;
   int grid = a.total, rc;
   if (plan.dynamic) {
-    rc = persistent_grid(reinterpret_cast<const void *>(kernel), &grid);
+    rc = persistent_grid(reinterpret_cast<const void *>(kernel), 0, &grid);
     if (rc) return rc;
     if (grid > a.total) grid = a.total;
     a.sched = reinterpret_cast<int *>(static_cast<char *>(ws) + plan.sched_off);
@@ -2109,20 +2118,35 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
 }
 
 int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s) {
-  if (plan.pieces < 2) return launch_attn_sparse(a, blk_q, s);
-  if (sparse_sub_block_rows(blk_q) != 128) return fail(H3A_ERR_INVALID_ARG, "split plan for 64-row query blocks");
+  if (plan.pieces < 2 && !plan.dynamic) return launch_attn_sparse(a, blk_q, s);
+  const int rows = sparse_sub_block_rows(blk_q);
+  if (plan.pieces >= 2 && rows != 128) return fail(H3A_ERR_INVALID_ARG, "split plan for 64-row query blocks");
   AttnArgs p = a;
-  p.split_first = plan.first;
-  p.split_pieces = plan.pieces;
-  p.ws = static_cast<float *>(ws);
+  if (plan.pieces >= 2) {
+    p.split_first = plan.first;
+    p.split_pieces = plan.pieces;
+    p.ws = static_cast<float *>(ws);
+  }
   const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
   p.total = (int)total;
-  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SparseLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
-  int rc = check_launch("attn_fwd_pingpong_kernel<sparse, split>");
-  if (rc) return rc;
-  const int64_t rows = (int64_t)(plan.tiles - plan.first) * 256;
-  hipLaunchKernelGGL(split_combine_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, p);
+  auto kernel = rows == 128 ? attn_fwd_pingpong_kernel<SparseLayout, 2, true>
+                            : attn_fwd_pingpong_kernel<SparseLayout, 2, true, true>;
+  int grid = p.total, rc;
+  if (plan.dynamic) {
+    rc = persistent_grid(reinterpret_cast<const void *>(kernel), rows == 128 ? 1 : 2, &grid);
+    if (rc) return rc;
+    if (grid > p.total) grid = p.total;
+    p.sched = reinterpret_cast<int *>(static_cast<char *>(ws) + plan.sched_off);
+    hipLaunchKernelGGL(sched_clear_kernel, dim3(1), dim3(256), 0, s, p.sched);
+    rc = check_launch("sched_clear_kernel");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(512), 0, s, p);
+  rc = check_launch("attn_fwd_pingpong_kernel<sparse, split>");
+  if (rc || plan.pieces < 2) return rc;
+  const int64_t nrows = (int64_t)(plan.tiles - plan.first) * 256;
+  hipLaunchKernelGGL(split_combine_kernel, dim3((unsigned)((nrows + 7) / 8)), dim3(256), 0, s, p);
   return check_launch("split_combine_kernel<sparse>");
 }
 

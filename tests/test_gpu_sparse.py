@@ -436,3 +436,28 @@ def test_sparse_h56_s42120_full_shape(gpu, blk):
             ref = torch.softmax(s, -1) @ vf
             assert_close_absmax(o[0, h, i0:i1].float().cpu().numpy(), ref.cpu().numpy(),
                                 what=f"blk={blk} h={h} q0={i0}")
+
+
+@pytest.mark.parametrize("blk", [128, 64, 256, 192])
+def test_sparse_queued_matches_one_pair_per_workgroup(gpu, blk):
+    """Four rounds of query-block pairs and more run on a persistent grid that takes pairs
+    from per-XCD queues (h3a_attn_fwd_blocksparse_ws, 1 KiB of counters in the workspace).
+    Without a split tail each pair's arithmetic is that of the one-pair-per-workgroup
+    launch, so with uneven and empty lists the outputs are equal bit for bit."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rows = 128 if blk % 128 == 0 else 64  # query sub-block height of the kernel
+    B, H, S = 4, max(cus // 4, 1), 8 * rows  # 4 pairs per head: 4 * CUs pairs, no remainder
+    nq = nk = -(-S // blk)
+    rng = np.random.default_rng(31 + blk)
+    bmap = (rng.random((B, H, nq, nk)) < 0.5).astype(np.uint8)
+    bmap[:, :, 0] = 0  # empty lists
+    bmap[0, 0, -1] = 1  # a full one
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    assert ops.sparse_workspace_bytes(B, H, S, S, blk, blk, lut.shape[3]) == 1024
+    g = torch.Generator(device=gpu).manual_seed(blk)
+    q, k, v = (torch.randn(B, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    want = ops.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk, split_tail=False)
+    got = ops.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"blk={blk}: queued dispatch differs from one pair per workgroup"
+    assert not got[:, :, :blk].any(), "rows of empty lists must be 0"
