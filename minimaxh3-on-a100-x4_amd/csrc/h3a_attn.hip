@@ -168,6 +168,22 @@ namespace h3a {
 #ifndef H3A_PP_A_SOFT
 #define H3A_PP_A_SOFT 1
 #endif
+// LDS DMA spread over the ping-pong matrix clusters, one instruction after
+// every few MFMAs, instead of issued in bursts (whose instructions queue for
+// the CU's load path and stall the issuing wave): dense, group A fetches all
+// of K(j+2) and V(j+1) during its MFMA(j); block-sparse, each group fetches
+// its own during its MFMA(j).
+#ifndef H3A_PP_DMA_IN_CLUSTER
+#define H3A_PP_DMA_IN_CLUSTER 0
+#endif
+#ifndef H3A_SPARSE_PP_IN_CLUSTER
+#define H3A_SPARSE_PP_IN_CLUSTER 0
+#endif
+// The same for the key-split kernel (64-row query blocks) alone: same-box A/B
+// +2 % there, while dense and the 128-row pairs measured 1.5-2 % slower.
+#ifndef H3A_SPARSE64_PP_IN_CLUSTER
+#define H3A_SPARSE64_PP_IN_CLUSTER 1
+#endif
 // Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
 // during the softmax cluster (2), or never (0).
 #ifndef H3A_PP_PRIO
@@ -289,6 +305,7 @@ struct StageBytes {
 // NaN/Inf) and the per-lane offsets are loop-invariant.
 template <int NW, class L, bool kIsV, int ROWS = kBN>
 struct TileDma {
+  static constexpr int kWaves = NW;
   static constexpr int kSlots = kIsV ? L::kVSlots : L::kKSlots;  // per row
   static constexpr int kInstTotal = ROWS * kSlots / 64;           // 64 lanes per instruction
   static constexpr int kInst = (kInstTotal + NW - 1) / NW;        // per wave (the last may be idle)
@@ -380,6 +397,27 @@ struct TileDma {
   __device__ __forceinline__ void finish(uint16_t *) const {}
 };
 
+// One wave's share of a stage's TileDma fetch issued one instruction at a
+// time (issue_desc taken apart), to spread it over a matrix cluster.
+template <class Dma>
+struct DmaSeq {
+  static constexpr int kCount = Dma::kInst;
+  const Dma &dma;
+  u32x4 d;
+  uint32_t cur, m0;
+  int i;
+  __device__ __forceinline__ DmaSeq(const Dma &dma_, u32x4 d_, uint16_t *tile)
+      : dma(dma_), d(d_), cur(dma_.first()), m0(lds_address(tile) + (uint32_t)dma_.wave * 1024u), i(0) {}
+  __device__ __forceinline__ void issue() {
+    dma.issue_one(d, i, cur, m0);
+    ++i;
+    if (i < Dma::kInst) {
+      cur = dma.next(cur);
+      m0 = opaque_sadd<1024u * Dma::kWaves>(m0);
+    }
+  }
+};
+
 // Wave-uniform position of a K or V stream in a contiguous range of key
 // stages: the byte address of the next stage's first row and the number of
 // valid rows from there on (it goes negative past the range's end, where the
@@ -456,10 +494,17 @@ struct TileRegs {
 // 32u..32u+31 of the stage.  In the S^T accumulator layout lane l owns query
 // l%32; register r of s[u] holds key 32u + 8*(r/4) + 4*(l/32) + r%4.
 
+// score_tile and pv_tile call hook(step) after each k-step's MFMAs (by
+// default nothing): where a matrix cluster's LDS DMA instructions go when they
+// are spread over it.
+struct NoHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
 // S^T (32*NSUB keys x 32 queries of this wave) = K_stage Q^T.
-template <class L, int NSUB>
+template <class L, int NSUB, class Hook = NoHook>
 __device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&qf)[8], int k_rd,
-                                           f32x16 (&s)[NSUB]) {
+                                           f32x16 (&s)[NSUB], Hook hook = Hook{}) {
 #pragma unroll
   for (int u = 0; u < NSUB; ++u) s[u] = f32x16{0.f};
   const char *kb = reinterpret_cast<const char *>(kbuf);
@@ -471,6 +516,7 @@ __device__ __forceinline__ void score_tile(const uint16_t *kbuf, const u32x4 (&q
       const u32x4 a = *(const u32x4 *)(p + 32 * u * L::kKRow);
       s[u] = mfma_32x32x16(a, qf[ks], s[u]);
     }
+    hook(ks);
   }
 }
 
@@ -496,9 +542,9 @@ __device__ __forceinline__ void pack_p(const f32x16 (&s)[NSUB], u32x4 (&pf)[2 * 
 // V[key][32*dt + l%32] for the 4 keys of its k-slots, in the score
 // accumulator's key order.  L::v_base / L::v_off place that in the layout.
 // O^T (128 dims x 32 queries) += V^T_stage P^T over NKS sixteen-key steps.
-template <class L, int NKS>
+template <class L, int NKS, class Hook = NoHook>
 __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[NKS], int v_rd,
-                                        f32x16 (&o)[4]) {
+                                        f32x16 (&o)[4], Hook hook = Hook{}) {
   const char *vb = reinterpret_cast<const char *>(vbuf);
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) {
@@ -509,6 +555,7 @@ __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[
       const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * L::kVRow));
       o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[ks], o[dt]);
     }
+    hook(ks);
   }
 }
 
@@ -1348,8 +1395,12 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   TileDma<NWD, L, true, BN> vdma;
   kdma.init(a.kss, NWD == NW ? wave_u : (wave_u & 3), lane);
   vdma.init(a.vss, NWD == NW ? wave_u : (wave_u & 3), lane);
-  constexpr int kKA = kSplitDma ? H3A_PP_A_KINST : 0, kVA = kSplitDma ? H3A_PP_A_VINST : 0;
   constexpr int kKI = decltype(kdma)::kInst, kVI = decltype(vdma)::kInst;
+  // Dense, DMA spread over group A's matrix clusters: group A fetches all.
+  constexpr bool kDenseIn = kSplitDma && H3A_PP_DMA_IN_CLUSTER;
+  constexpr bool kSpIn = kSpDma && (kKeySplit ? H3A_SPARSE64_PP_IN_CLUSTER : H3A_SPARSE_PP_IN_CLUSTER);
+  constexpr int kKA = kDenseIn ? kKI : (kSplitDma ? H3A_PP_A_KINST : 0);
+  constexpr int kVA = kDenseIn ? kVI : (kSplitDma ? H3A_PP_A_VINST : 0);
   auto fetch_k = [&](const uint16_t *base, int key0, uint16_t *tile) __attribute__((always_inline)) {
     if constexpr (kSplitDma) {
       if (lead) kdma.template issue_range<0, kKA>(base, a.kss, key0, a.Skv, tile);
@@ -1516,11 +1567,11 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     constexpr int I1 = decltype(top)::value ? kVTop : decltype(vdma)::kInst;
     vdma.template issue_range<I0, I1>(Vb, a.vss, key_v, a.Skv, vbuf[P ^ 1]);
   };
-  constexpr bool kALate = kSplitDma && H3A_PP_A_LATE && (kKA + kVA > 0);
+  constexpr bool kALate = kSplitDma && !kDenseIn && H3A_PP_A_LATE && (kKA + kVA > 0);
   // Group A's share at the top of its softmax slot: the buffers it fills were
   // last read in MFMA(j-1), and it waits for the share before the barrier
   // that ends the slot, as for any share.
-  constexpr bool kASoft = kSplitDma && !kALate && H3A_PP_A_SOFT && (kKA + kVA > 0);
+  constexpr bool kASoft = kSplitDma && !kDenseIn && !kALate && H3A_PP_A_SOFT && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
   // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
@@ -1557,6 +1608,40 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
 #endif
     if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(0);
   };
+  // The matrix cluster with this wave's fetch of K(j+2) (kseq) and V(j+1)
+  // (vseq) spread over it: the K instructions after evenly spaced score
+  // k-steps, the V ones after the PV key steps.  Each DMA instruction is
+  // volatile asm that touches memory, so it keeps its place among the LDS
+  // operand reads, which the scheduling groups interleave with the MFMAs.
+  auto mfma_dma = [&](auto par, auto &kseq, auto &vseq) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    constexpr int NK = std::remove_reference_t<decltype(kseq)>::kCount;
+    constexpr int NV = std::remove_reference_t<decltype(vseq)>::kCount;
+    constexpr int NKS = 2 * WS;  // PV key steps
+    static_assert(NK > 0 && 8 % NK == 0, "K instructions spread evenly over 8 score k-steps");
+    static_assert(NV > 0 && (NV % NKS == 0 || NKS % NV == 0), "V instructions spread evenly over the PV steps");
+    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(1);
+    score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s, [&](int ks) __attribute__((always_inline)) {
+      if ((ks + 1) % (8 / NK) == 0) kseq.issue();
+    });
+    pv_tile<L, NKS>(vbuf[P], pf, v_rd, o, [&](int ks) __attribute__((always_inline)) {
+      if constexpr (NV >= NKS) {
+#pragma unroll
+        for (int t = 0; t < NV / NKS; ++t) vseq.issue();
+      } else {
+        if ((ks + 1) % (NKS / NV) == 0) vseq.issue();
+      }
+    });
+#if H3A_PP_READ_AHEAD
+    __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
+#pragma unroll
+    for (int i = 0; i < 16 * WS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
+    }
+#endif
+    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(0);
+  };
   auto soft = [&](int j) __attribute__((always_inline)) {
     if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(1);
     const int key0 = (kSparse ? soft_key : key_base(j + 1)) + 32 * kh;
@@ -1577,7 +1662,28 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   pc.loop_begin();
   if (lead) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
-      if constexpr (kSpDma) {
+      if constexpr (kSpIn) {
+        constexpr int P = decltype(par)::value;
+        pc.mark(0);
+        stage_keys(j);
+        {
+          DmaSeq<decltype(kdma)> kseq(kdma, kdma.desc(Kb, a.kss, key_k, a.Skv), kbuf[P]);
+          DmaSeq<decltype(vdma)> vseq(vdma, vdma.desc(Vb, a.vss, key_v, a.Skv), vbuf[P ^ 1]);
+          mfma_dma(par, kseq, vseq);
+        }
+        pc.mark(1);
+        mid_barrier<kSparse>();
+        pc.mark(2);
+        lut_next(j);
+        if (j + 1 < niter) soft(j);
+        pc.mark(3);
+        wait_vmem_all();
+        pc.mark(4);
+        slot_barrier();
+        pc.mark(5);
+        pc.stage_done();
+        return;
+      } else if constexpr (kSpDma) {
         pc.mark(0);
         mfma(par);
         pc.mark(1);
@@ -1625,6 +1731,28 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         pc.stage_done();
         return;
       }
+      if constexpr (kDenseIn) {
+        constexpr int P = decltype(par)::value;
+        pc.mark(0);
+        {
+          DmaSeq<decltype(kdma)> kseq(kdma, kcur.desc(), kbuf[P]);
+          DmaSeq<decltype(vdma)> vseq(vdma, vcur.desc(), vbuf[P ^ 1]);
+          mfma_dma(par, kseq, vseq);
+        }
+        kcur.advance();
+        vcur.advance();
+        pc.mark(1);
+        mid_barrier<kSparse>();
+        pc.mark(2);
+        if (j + 1 < niter) soft(j);
+        pc.mark(3);
+        wait_vmem_all();
+        pc.mark(4);
+        slot_barrier();
+        pc.mark(5);
+        pc.stage_done();
+        return;
+      }
       if constexpr (!kALate && !kASoft) dma(par, j);
       pc.mark(0);
       mfma(par);
@@ -1655,7 +1783,29 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     // kFirst: stage 0, which has no softmax before its matrix cluster (P(0)
     // came from the prologue); peeled off so that the loop body has no branch.
     auto stage = [&](auto par, int j, auto first) __attribute__((always_inline)) {
-      if constexpr (kSpDma) {
+      if constexpr (kSpIn) {
+        constexpr int P = decltype(par)::value;
+        pc.mark(0);
+        stage_keys(j);  // also sets the key SOFT(j-1) masks with: stage j's first
+        lut_next(j);
+        if constexpr (!decltype(first)::value) soft(j - 1);
+        pc.mark(1);
+        // This wave's fetch of K(j+1) and V(j), issued during MFMA(j-1).
+        wait_vmem_all();
+        pc.mark(4);
+        mid_barrier<kSparse>();
+        pc.mark(2);
+        {
+          DmaSeq<decltype(kdma)> kseq(kdma, kdma.desc(Kb, a.kss, key_k, a.Skv), kbuf[P]);
+          DmaSeq<decltype(vdma)> vseq(vdma, vdma.desc(Vb, a.vss, key_v, a.Skv), vbuf[P ^ 1]);
+          mfma_dma(par, kseq, vseq);
+        }
+        pc.mark(3);
+        slot_barrier();
+        pc.mark(5);
+        pc.stage_done();
+        return;
+      } else if constexpr (kSpDma) {
         pc.mark(0);
         stage_keys(j);  // also sets the key SOFT(j-1) masks with: stage j's first
         dma_k(std::true_type{}, par);
