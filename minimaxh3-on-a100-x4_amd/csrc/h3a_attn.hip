@@ -372,8 +372,14 @@ struct TileDma {
   // The same with the stage's descriptor given (StageCursor::desc).
   template <int I0, int I1>
   __device__ __forceinline__ void issue_desc(u32x4 d, uint16_t *tile) const {
+    issue_desc_off<I0, I1>(d, tile, 0u);
+  }
+  // The same with a descriptor of the whole (b,h) slice and the stage's byte
+  // offset in it, soff, added to every lane's offset (one v_add).
+  template <int I0, int I1>
+  __device__ __forceinline__ void issue_desc_off(u32x4 d, uint16_t *tile, uint32_t soff) const {
     if constexpr (I1 > I0) {
-      uint32_t cur = first();
+      uint32_t cur = first() + soff;
 #pragma unroll
       for (int i = 0; i < I0; ++i) cur = next(cur);
       uint32_t m0 = lds_address(tile) + (uint32_t)(wave + I0 * NW) * 1024u;
@@ -406,8 +412,9 @@ struct DmaSeq {
   u32x4 d;
   uint32_t cur, m0;
   int i;
-  __device__ __forceinline__ DmaSeq(const Dma &dma_, u32x4 d_, uint16_t *tile)
-      : dma(dma_), d(d_), cur(dma_.first()), m0(lds_address(tile) + (uint32_t)dma_.wave * 1024u), i(0) {}
+  // soff: the stage's byte offset when d describes the whole (b,h) slice.
+  __device__ __forceinline__ DmaSeq(const Dma &dma_, u32x4 d_, uint16_t *tile, uint32_t soff)
+      : dma(dma_), d(d_), cur(dma_.first() + soff), m0(lds_address(tile) + (uint32_t)dma_.wave * 1024u), i(0) {}
   __device__ __forceinline__ void issue() {
     dma.issue_one(d, i, cur, m0);
     ++i;
@@ -1223,7 +1230,7 @@ struct PingPongLds {
 // range of a split tile, or (sparse) a pair of query blocks or a piece of one.
 // `remapped`: the item number is already XCD-aware (taken from the queues),
 // so whole tiles are not remapped.
-template <class L, int NSUB, bool kSparse, bool kKeySplit>
+template <class L, int NSUB, bool kSparse, bool kKeySplit, bool kWideKV>
 __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item, const bool remapped,
                                               PingPongLds<L, NSUB, kSparse> &lds, PhaseClock &pc) {
   constexpr int NW = 8;
@@ -1396,6 +1403,30 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   kdma.init(a.kss, NWD == NW ? wave_u : (wave_u & 3), lane);
   vdma.init(a.vss, NWD == NW ? wave_u : (wave_u & 3), lane);
   constexpr int kKI = decltype(kdma)::kInst, kVI = decltype(vdma)::kInst;
+  // Sparse stage fetches.  By default one descriptor per (b,h) slice, built
+  // here, and each stage's byte offset added to the lanes' offsets: the
+  // per-stage descriptor (a 64-bit base and a row count for the range check)
+  // cost ~35 scalar instructions per stage.  Rows past Skv and stages past a
+  // list (key Skv) fall outside the slice's range and load zeros, as with
+  // the per-stage descriptors.  kWideKV: offsets up to (Skv + 64) rows would
+  // pass 2^32 bytes, so every stage gets its own descriptor based on its
+  // first row.
+  constexpr bool kHeadDesc = kSpDma && !kWideKV;
+  const u32x4 kd_head = stage_desc(Kb, a.kss, a.Skv), vd_head = stage_desc(Vb, a.vss, a.Skv);
+  const uint32_t krow_bytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a.kss * 2));
+  const uint32_t vrow_bytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a.vss * 2));
+  auto k_desc = [&](int key0) __attribute__((always_inline)) {
+    if constexpr (kHeadDesc) return kd_head; else return kdma.desc(Kb, a.kss, key0, a.Skv);
+  };
+  auto v_desc = [&](int key0) __attribute__((always_inline)) {
+    if constexpr (kHeadDesc) return vd_head; else return vdma.desc(Vb, a.vss, key0, a.Skv);
+  };
+  auto k_soff = [&](int key0) __attribute__((always_inline)) {
+    return kHeadDesc ? (uint32_t)key0 * krow_bytes : 0u;
+  };
+  auto v_soff = [&](int key0) __attribute__((always_inline)) {
+    return kHeadDesc ? (uint32_t)key0 * vrow_bytes : 0u;
+  };
   // Dense, DMA spread over group A's matrix clusters: group A fetches all.
   constexpr bool kDenseIn = kSplitDma && H3A_PP_DMA_IN_CLUSTER;
   constexpr bool kSpIn = kSpDma && (kKeySplit ? H3A_SPARSE64_PP_IN_CLUSTER : H3A_SPARSE_PP_IN_CLUSTER);
@@ -1559,13 +1590,13 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     constexpr int P = decltype(par)::value;
     constexpr int I0 = decltype(top)::value ? 0 : kKTop;
     constexpr int I1 = decltype(top)::value ? kKTop : decltype(kdma)::kInst;
-    kdma.template issue_range<I0, I1>(Kb, a.kss, key_k, a.Skv, kbuf[P]);
+    kdma.template issue_desc_off<I0, I1>(k_desc(key_k), kbuf[P], k_soff(key_k));
   };
   auto dma_v = [&](auto top, auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
     constexpr int I0 = decltype(top)::value ? 0 : kVTop;
     constexpr int I1 = decltype(top)::value ? kVTop : decltype(vdma)::kInst;
-    vdma.template issue_range<I0, I1>(Vb, a.vss, key_v, a.Skv, vbuf[P ^ 1]);
+    vdma.template issue_desc_off<I0, I1>(v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
   };
   constexpr bool kALate = kSplitDma && !kDenseIn && H3A_PP_A_LATE && (kKA + kVA > 0);
   // Group A's share at the top of its softmax slot: the buffers it fills were
@@ -1667,8 +1698,8 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         pc.mark(0);
         stage_keys(j);
         {
-          DmaSeq<decltype(kdma)> kseq(kdma, kdma.desc(Kb, a.kss, key_k, a.Skv), kbuf[P]);
-          DmaSeq<decltype(vdma)> vseq(vdma, vdma.desc(Vb, a.vss, key_v, a.Skv), vbuf[P ^ 1]);
+          DmaSeq<decltype(kdma)> kseq(kdma, k_desc(key_k), kbuf[P], k_soff(key_k));
+          DmaSeq<decltype(vdma)> vseq(vdma, v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
           mfma_dma(par, kseq, vseq);
         }
         pc.mark(1);
@@ -1735,8 +1766,8 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         constexpr int P = decltype(par)::value;
         pc.mark(0);
         {
-          DmaSeq<decltype(kdma)> kseq(kdma, kcur.desc(), kbuf[P]);
-          DmaSeq<decltype(vdma)> vseq(vdma, vcur.desc(), vbuf[P ^ 1]);
+          DmaSeq<decltype(kdma)> kseq(kdma, kcur.desc(), kbuf[P], 0u);
+          DmaSeq<decltype(vdma)> vseq(vdma, vcur.desc(), vbuf[P ^ 1], 0u);
           mfma_dma(par, kseq, vseq);
         }
         kcur.advance();
@@ -1796,8 +1827,8 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         mid_barrier<kSparse>();
         pc.mark(2);
         {
-          DmaSeq<decltype(kdma)> kseq(kdma, kdma.desc(Kb, a.kss, key_k, a.Skv), kbuf[P]);
-          DmaSeq<decltype(vdma)> vseq(vdma, vdma.desc(Vb, a.vss, key_v, a.Skv), vbuf[P ^ 1]);
+          DmaSeq<decltype(kdma)> kseq(kdma, k_desc(key_k), kbuf[P], k_soff(key_k));
+          DmaSeq<decltype(vdma)> vseq(vdma, v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
           mfma_dma(par, kseq, vseq);
         }
         pc.mark(3);
@@ -1959,7 +1990,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   pc.finish(wave, lane);
 }
 
-template <class L, int NSUB, bool kSparse = false, bool kKeySplit = false>
+template <class L, int NSUB, bool kSparse = false, bool kKeySplit = false, bool kWideKV = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) PingPongLds<L, NSUB, kSparse> lds;
@@ -1997,7 +2028,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       if (item < 0) break;
     }
     pc.begin(blockIdx.x == 0, item);
-    pingpong_item<L, NSUB, kSparse, kKeySplit>(args, item, args.sched != nullptr, lds, pc);
+    pingpong_item<L, NSUB, kSparse, kKeySplit, kWideKV>(args, item, args.sched != nullptr, lds, pc);
     KernargPtr kq = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(kq));
     if (!kq->sched) break;
@@ -2267,6 +2298,20 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
   return check_launch("split_combine_kernel");
 }
 
+// The block-sparse ping-pong kernel for query blocks of `rows` rows; the
+// wide-K/V instantiation when stage offsets from the (b,h) slice base could
+// pass 2^32 bytes (see kWideKV).
+typedef void (*PingPongKernel)(AttnArgs);
+static PingPongKernel sparse_pingpong_kernel(const AttnArgs &a, int rows) {
+  const int64_t stride = a.kss > a.vss ? a.kss : a.vss;
+  const bool wide = ((int64_t)a.Skv + 64) * stride * 2 >= ((int64_t)1 << 32);
+  if (rows == 128)
+    return wide ? attn_fwd_pingpong_kernel<SparseLayout, 2, true, false, true>
+                : attn_fwd_pingpong_kernel<SparseLayout, 2, true, false, false>;
+  return wide ? attn_fwd_pingpong_kernel<SparseLayout, 2, true, true, true>
+              : attn_fwd_pingpong_kernel<SparseLayout, 2, true, true, false>;
+}
+
 int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s) {
   if (plan.pieces < 2 && !plan.dynamic) return launch_attn_sparse(a, blk_q, s);
   const int rows = sparse_sub_block_rows(blk_q);
@@ -2280,8 +2325,7 @@ int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan
   const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
   p.total = (int)total;
-  auto kernel = rows == 128 ? attn_fwd_pingpong_kernel<SparseLayout, 2, true>
-                            : attn_fwd_pingpong_kernel<SparseLayout, 2, true, true>;
+  const PingPongKernel kernel = sparse_pingpong_kernel(p, rows);
   int grid = p.total, rc;
   if (plan.dynamic) {
     rc = persistent_grid(reinterpret_cast<const void *>(kernel), rows == 128 ? 1 : 2, &grid);
@@ -2307,10 +2351,7 @@ int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
     const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
     if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
     p.total = (int)pairs;
-    if (rows == 128)
-      hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SparseLayout, 2, true>), dim3(p.total), dim3(512), 0, s, p);
-    else
-      hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SparseLayout, 2, true, true>), dim3(p.total), dim3(512), 0, s, p);
+    hipLaunchKernelGGL(sparse_pingpong_kernel(p, rows), dim3(p.total), dim3(512), 0, s, p);
     return check_launch("attn_fwd_pingpong_kernel<sparse>");
   }
   if (rows == 128) {
