@@ -29,18 +29,21 @@ FLOP_PER_CLK = 256 * 4096  # dense bf16 MFMA, whole chip
 # counter scaled by what it reads for a 2048 MiB device copy); its line
 # "roofline.traffic = <bytes> B" is read at run time.
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_h56_s42120_counters.txt")
+SPARSE_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_sparse_h56_s42120_counters.txt")
 B, H, S, D, LAYERS = 1, 56, 42120, 128, 50
 
 
-def measured_traffic():
-    """(bytes per dense launch, source) from the committed counter summary, or (None, reason)."""
+def measured_traffic(path=TRAFFIC_SUMMARY, key=""):
+    """(bytes per launch, source) from a committed counter summary's "roofline.traffic[.key] = X B"
+    line, or (None, reason)."""
     import re
+    pat = r"\s*roofline\.traffic" + (r"\." + re.escape(key) if key else "") + r"\s*=\s*([0-9.]+[eE][+]?[0-9]+)\s*B\b"
     try:
-        with open(TRAFFIC_SUMMARY) as f:
+        with open(path) as f:
             for ln in f:
-                m = re.match(r"\s*roofline\.traffic\s*=\s*([0-9.]+[eE][+]?[0-9]+)\s*B\b", ln)
+                m = re.match(pat, ln)
                 if m:
-                    return float(m.group(1)), os.path.relpath(TRAFFIC_SUMMARY, ROOT)
+                    return float(m.group(1)), os.path.relpath(path, ROOT)
     except OSError as e:
         return None, f"unreadable: {e}"
     return None, "no roofline.traffic line"
@@ -332,6 +335,7 @@ def run_sparse(args, torch, h3attn, dev):
                 events[i][1].record(stream)
 
     wall, avg_kernel_ms = _timed(step, args.steps, args.warmup, L, torch, stream)
+    _calib_copy(args, torch, dev)
     ghz, clock_note = measure_clock_sparse(items[0], blk) if not args.no_clock else (None, "skipped")
     flops = sum(it[5] for it in items) / L
     value = flops * L * args.steps / wall / 1e12
@@ -341,13 +345,15 @@ def run_sparse(args, torch, h3attn, dev):
                 {"workload": f"block-sparse attention, {L} layers per step", "B": B, "H": H, "S": S,
                  "D": D, "blk_q": blk, "blk_k": blk,
                  "keep": f"{int(0.25 * nk)} of {nk} key tiles + diagonal"})
+    traffic, traffic_src = measured_traffic(SPARSE_TRAFFIC_SUMMARY, f"sparse{blk}")
     res.update({
         "ms_per_layer": round(avg_kernel_ms, 3),
         "kept_fraction": round(flops / flops_per_layer(), 4),
         "dense_equivalent_tflops": round(flops_per_layer() / (avg_kernel_ms * 1e-3) / 1e12, 1),
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": ("attn_fwd_pingpong_kernel<SwzLayout,2,sparse> (pairs of 128-row query blocks; "
                                 "+ split_combine_kernel for the split tail)" if blk % 128 == 0
                                 else "attn_fwd_pingpong_kernel<SwzLayout,2,sparse,key-split> (pairs of 64-row "

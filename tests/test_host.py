@@ -68,6 +68,22 @@ def test_bench_refuses_multi_gpu():
     assert "one MI355X" in r.stderr
 
 
+def test_bench_reads_traffic_from_the_committed_counter_summaries():
+    """The roofline "traffic" of the dense and sparse bench lines comes from the
+    profiles/ counter summaries (a "roofline.traffic[.key] = X B" line), not a constant."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench_mod", f"{ROOT}/bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    dense, src = bench.measured_traffic()
+    assert src.endswith("attn_dense_h56_s42120_counters.txt") and 2.4e9 < dense < 2e10
+    for blk in (128, 64):
+        t, src = bench.measured_traffic(bench.SPARSE_TRAFFIC_SUMMARY, f"sparse{blk}")
+        assert src.endswith("attn_sparse_h56_s42120_counters.txt") and 1e9 < t < 1e11, (blk, t, src)
+    t, why = bench.measured_traffic(bench.SPARSE_TRAFFIC_SUMMARY, "sparse192")
+    assert t is None and "no roofline.traffic" in why
+
+
 # ----------------------------------------------------------------------------- h3_sla schedule
 def test_schedule_parsing():
     assert sla.parse_ranges("31-42,46,48-49") == list(range(31, 43)) + [46, 48, 49]
