@@ -177,12 +177,20 @@ namespace h3a {
 #define H3A_PP_DMA_IN_CLUSTER 0
 #endif
 #ifndef H3A_SPARSE_PP_IN_CLUSTER
-#define H3A_SPARSE_PP_IN_CLUSTER 0
+#define H3A_SPARSE_PP_IN_CLUSTER 1
 #endif
-// The same for the key-split kernel (64-row query blocks) alone: same-box A/B
-// +2 % there, while dense and the 128-row pairs measured 1.5-2 % slower.
+// The same for the key-split kernel (64-row query blocks).
 #ifndef H3A_SPARSE64_PP_IN_CLUSTER
 #define H3A_SPARSE64_PP_IN_CLUSTER 1
+#endif
+// Fetch spread over a cluster: all of it among the PV MFMAs, one instruction
+// every NP / NI MFMAs (1), or the K instructions among the score MFMAs and the
+// V ones among the PV MFMAs (0), where the score operand reads issued ahead
+// pull the K instructions to the cluster's start.  Same-box A/B of (1): 64-row
+// pairs +2.2 % over (0), 128-row pairs +0.6 % over the fetch at the slot tops
+// (where (0) lost 2 %); dense -1.2 % against its own placement.
+#ifndef H3A_PP_DMA_PV_ONLY
+#define H3A_PP_DMA_PV_ONLY 1
 #endif
 // Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
 // during the softmax cluster (2), or never (0).
@@ -501,9 +509,9 @@ struct TileRegs {
 // 32u..32u+31 of the stage.  In the S^T accumulator layout lane l owns query
 // l%32; register r of s[u] holds key 32u + 8*(r/4) + 4*(l/32) + r%4.
 
-// score_tile and pv_tile call hook(step) after each k-step's MFMAs (by
-// default nothing): where a matrix cluster's LDS DMA instructions go when they
-// are spread over it.
+// score_tile calls hook(k-step) after each k-step's MFMAs and pv_tile
+// hook(4 * key step + dim tile) after each MFMA (by default nothing): where a
+// matrix cluster's LDS DMA instructions go when they are spread over it.
 struct NoHook {
   __device__ __forceinline__ void operator()(int) const {}
 };
@@ -561,8 +569,8 @@ __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[
       const u32x2 lo = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p));
       const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * L::kVRow));
       o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[ks], o[dt]);
+      hook(4 * ks + dt);
     }
-    hook(ks);
   }
 }
 
@@ -1644,6 +1652,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // k-steps, the V ones after the PV key steps.  Each DMA instruction is
   // volatile asm that touches memory, so it keeps its place among the LDS
   // operand reads, which the scheduling groups interleave with the MFMAs.
+  constexpr bool kDmaPvOnly = H3A_PP_DMA_PV_ONLY;
   auto mfma_dma = [&](auto par, auto &kseq, auto &vseq) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
     constexpr int NK = std::remove_reference_t<decltype(kseq)>::kCount;
@@ -1653,14 +1662,26 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     static_assert(NV > 0 && (NV % NKS == 0 || NKS % NV == 0), "V instructions spread evenly over the PV steps");
     if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(1);
     score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s, [&](int ks) __attribute__((always_inline)) {
-      if ((ks + 1) % (8 / NK) == 0) kseq.issue();
+      if (!kDmaPvOnly && (ks + 1) % (8 / NK) == 0) kseq.issue();
     });
-    pv_tile<L, NKS>(vbuf[P], pf, v_rd, o, [&](int ks) __attribute__((always_inline)) {
-      if constexpr (NV >= NKS) {
+    pv_tile<L, NKS>(vbuf[P], pf, v_rd, o, [&](int t) __attribute__((always_inline)) {
+      if constexpr (kDmaPvOnly) {
+        // All NK + NV instructions among the PV MFMAs, K first, evenly spaced.
+        constexpr int NP = 4 * NKS, NI = NK + NV;
 #pragma unroll
-        for (int t = 0; t < NV / NKS; ++t) vseq.issue();
-      } else {
-        if ((ks + 1) % (NKS / NV) == 0) vseq.issue();
+        for (int i = 0; i < NI; ++i) {
+          if (t == i * NP / NI) {
+            if (i < NK) kseq.issue(); else vseq.issue();
+          }
+        }
+      } else if (t % 4 == 3) {
+        const int ks = t / 4;
+        if constexpr (NV >= NKS) {
+#pragma unroll
+          for (int u = 0; u < NV / NKS; ++u) vseq.issue();
+        } else {
+          if ((ks + 1) % (NKS / NV) == 0) vseq.issue();
+        }
       }
     });
 #if H3A_PP_READ_AHEAD
