@@ -46,6 +46,7 @@
 #include "h3a_device.h"
 #include "h3a_internal.h"
 #include "h3a_lut.h"
+#include "h3a_queue.h"
 
 namespace h3a {
 
@@ -1190,39 +1191,15 @@ __device__ __forceinline__ void mid_barrier() {
 // score sub-tile, 16 MFMAs per stage) with its own running max, row sum and
 // O; after the loop the key-half-1 wave hands (O, m, l) to its partner
 // through LDS, which merges them as the split-tail combine does.
-// Dynamic dispatch of the ping-pong kernel: kQueues queues, one per XCD.
-// Queue x holds XCD x's share of the whole work items (the contiguous range
-// xcd_remap deals it: consecutive query tiles of the same heads, whose K/V
-// the XCD's L2 then shares) followed by its share of the split pieces.  A
-// workgroup takes items from its own XCD's queue and, once that is empty,
-// from the others in turn, so XCDs that run at a higher clock finish the
-// slower ones' work instead of idling.  Each queue is a counter (one 128-byte
-// line each) that sched_clear_kernel zeroes before the launch.
-constexpr int kQueues = 8;
-constexpr int kQueueStride = 32;  // ints
-constexpr size_t kSchedBytes = (size_t)kQueues * kQueueStride * sizeof(int);
-
-struct QueueShare {
-  int first, len;
-};
-__device__ __forceinline__ QueueShare queue_share(int n, int x) {
-  const int per = n / kQueues, rem = n % kQueues;
-  return {x * per + (x < rem ? x : rem), per + (x < rem ? 1 : 0)};
-}
-
-// The next work item for a workgroup on XCD xcc (items 0..whole-1 are whole
-// tiles, whole + p is split piece p), or -1 when every queue is empty.
+// The next work item from the per-XCD queues (see take_item_with) for a
+// workgroup on XCD xcc, counters at `sched`.
 __device__ __forceinline__ int take_item(int *sched, int whole, int pieces, int xcc) {
-  for (int t = 0; t < kQueues; ++t) {
-    const int x = (xcc + t) & (kQueues - 1);
-    const QueueShare sw = queue_share(whole, x), sp = queue_share(pieces, x);
-    const int len = sw.len + sp.len;
-    int *ctr = sched + x * kQueueStride;
-    if (t > 0 && __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= len) continue;
-    const int i = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (i < len) return i < sw.len ? sw.first + i : whole + sp.first + (i - sw.len);
-  }
-  return -1;
+  return take_item_with(
+      whole, pieces, xcc,
+      [&](int x) { return __hip_atomic_load(sched + x * kQueueStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
+      [&](int x) {
+        return __hip_atomic_fetch_add(sched + x * kQueueStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      });
 }
 
 template <class L, int NSUB, bool kSparse>

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "h3a_queue.h"
+
 namespace h3a {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -148,15 +150,6 @@ __device__ __forceinline__ float dot2_bf16_ones(uint32_t w, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
 }
 
-// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X.  Remap
-// the dispatch index so each XCD walks one contiguous range of work items
-// (consecutive query tiles of the same head), which keeps that head's K/V
-// stream resident in the XCD's own L2.  Bijective for any total.
-__device__ __forceinline__ int xcd_remap(int i, int total) {
-  constexpr int kXcds = 8;
-  const int per = total / kXcds, rem = total % kXcds;
-  const int x = i % kXcds, idx = i / kXcds;
-  return x * per + (x < rem ? x : rem) + idx;
-}
+// xcd_remap (the XCD-aware deal of work items) lives in h3a_queue.h.
 
 }  // namespace h3a
