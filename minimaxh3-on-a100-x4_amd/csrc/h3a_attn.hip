@@ -193,6 +193,12 @@ namespace h3a {
 #ifndef H3A_PP_DMA_PV_ONLY
 #define H3A_PP_DMA_PV_ONLY 1
 #endif
+// Ping-pong epilogue: O stored through a wave-private LDS tile, 4 whole rows
+// per store instruction (1), or straight from the MFMA layout, 16 bytes into
+// each of 32 rows per instruction (0).
+#ifndef H3A_PP_STORE_LDS
+#define H3A_PP_STORE_LDS 1
+#endif
 // Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
 // during the softmax cluster (2), or never (0).
 #ifndef H3A_PP_PRIO
@@ -1287,15 +1293,31 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // of the group's list.
   int ngrp = niter, gj0 = 0;
   const int32_t *lut_row = nullptr;
+  int e_pre[4] = {0, 0, 0, 0};
   if constexpr (kSparse) {
     // Query sub-block qb reads LUT row qb / a.qmul (blk_q = 256: the two
     // 128-row blocks of a pair share one row; blk_q = 192: three 64-row ones).
-    auto stages_of = [&](int qb) __attribute__((always_inline)) -> int {
+    // The counts and the LUT are read through the constant address space:
+    // they are not written during the kernel, so these stay scalar loads
+    // after an earlier work item's stores (a global pointer would have to be
+    // re-read per lane).  Both counts and the LUT entries of the first four
+    // stages are loaded up front, unconditionally (indices clamped into their
+    // rows), so that one wait covers them all: for a whole pair (no split)
+    // stage j's entry is entry block_of_stage(j) of the row, and an entry at
+    // or past the end of the list is never used (its stage's key is Skv).
+    typedef const __attribute__((address_space(4))) int32_t *ConstInts;
+    const int qb = 2 * qt + grp, qo = 2 * qt + 1 - grp;
+    const ConstInts crow = (ConstInts)a.counts + (int64_t)bh * a.nqb;
+    const int cnt_own = crow[(qb < a.nqt ? qb : 0) / a.qmul];
+    const int cnt_oth = crow[(qo < a.nqt ? qo : 0) / a.qmul];
+    lut_row = a.lut + ((int64_t)bh * a.nqb + (qb < a.nqt ? qb : 0) / a.qmul) * a.lut_stride;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = block_of_stage(j, a.sub);
+      e_pre[j] = ((ConstInts)lut_row)[e < a.lut_stride ? e : a.lut_stride - 1];
+    }
+    auto stages_of = [&](int qb, int cnt) __attribute__((always_inline)) -> int {
       if (qb >= a.nqt) return 0;
-      // Through the constant address space: the counts are not written during
-      // the kernel, so this stays a scalar load after an earlier work item's
-      // stores (a global pointer would have to be re-read per lane).
-      const int cnt = ((const __attribute__((address_space(4))) int32_t *)a.counts)[(int64_t)bh * a.nqb + qb / a.qmul];
       return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
     };
     auto part_of = [&](int n, int &first) __attribute__((always_inline)) -> int {
@@ -1306,12 +1328,10 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
       first = (int)((int64_t)n * split_part / a.split_pieces);
       return (int)((int64_t)n * (split_part + 1) / a.split_pieces) - first;
     };
-    const int qb = 2 * qt + grp;
     int other_j0;
-    ngrp = part_of(stages_of(qb), gj0);
-    const int nother = part_of(stages_of(2 * qt + 1 - grp), other_j0);
+    ngrp = part_of(stages_of(qb, cnt_own), gj0);
+    const int nother = part_of(stages_of(qo, cnt_oth), other_j0);
     niter = ngrp > nother ? ngrp : nother;
-    lut_row = a.lut + ((int64_t)bh * a.nqb + (qb < a.nqt ? qb : 0) / a.qmul) * a.lut_stride;
   }
   // Sparse: LUT entry of local stage j (a key block of a.sub stages; read
   // through the constant address space, so it is a scalar load), and the
@@ -1335,6 +1355,12 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     }
   };
   auto key_base = [&](int j) __attribute__((always_inline)) -> int { return key_of_entry(j, lut_entry(j)); };
+  // The same for the prologue's stages 0-3, from the entries loaded up front.
+  auto pro_entry = [&](int j) __attribute__((always_inline)) -> int {
+    if constexpr (kSparse) return split_part < 0 ? e_pre[j] : lut_entry(j);
+    else return 0;
+  };
+  auto pro_key = [&](int j) __attribute__((always_inline)) -> int { return key_of_entry(j, pro_entry(j)); };
   if (kSparse && niter == 0) {
     // Neither query block of the pair keeps a key block (in this piece): O = 0,
     // or an empty partial result (m = -inf, l = 0, O = 0).
@@ -1357,11 +1383,13 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     return;
   }
 
+  // Global loads: as flat loads they would also count as LDS/scalar accesses
+  // and hold up the next wait for those.
   u32x4 qf[8];
   if (qrow < a.Sq) {
     const uint16_t *p = Qb + (int64_t)qrow * a.qss + 8 * g;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const u32x4 *)(p + ks * 16);
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const __attribute__((address_space(1))) u32x4 *)(p + ks * 16);
   } else {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qf[ks] = u32x4{0, 0, 0, 0};
@@ -1483,29 +1511,30 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   vst.init(a.vss, tid & 255);
 
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
+  const int pkey0 = pro_key(0), pkey1 = pro_key(1);
   if constexpr (kSpDma) {
-    kdma.issue(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
-    vdma.issue(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
-    kdma.issue(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+    kdma.issue(Kb, a.kss, pkey0, a.Skv, kbuf[0]);
+    vdma.issue(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
+    kdma.issue(Kb, a.kss, pkey1, a.Skv, kbuf[1]);
     wait_vmem_all();
   } else if constexpr (kSparse) {
-    kst.start(Kb, a.kss, key_base(0), a.Skv, kbuf[0]);
-    vst.start(Vb, a.vss, key_base(0), a.Skv, vbuf[0]);
+    kst.start(Kb, a.kss, pkey0, a.Skv, kbuf[0]);
+    vst.start(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
     kst.finish(kbuf[0]);
     vst.finish(vbuf[0]);
-    kst.start(Kb, a.kss, key_base(1), a.Skv, kbuf[1]);
+    kst.start(Kb, a.kss, pkey1, a.Skv, kbuf[1]);
     kst.finish(kbuf[1]);
   } else {
-    fetch_k(Kb, key_base(0), kbuf[0]);
-    fetch_v(Vb, key_base(0), vbuf[0]);
-    fetch_k(Kb, key_base(1), kbuf[1]);
+    fetch_k(Kb, pkey0, kbuf[0]);
+    fetch_v(Vb, pkey0, vbuf[0]);
+    fetch_k(Kb, pkey1, kbuf[1]);
     wait_vmem_all();
   }
   __syncthreads();
   f32x16 s[WS];
   u32x4 pf[2 * WS];
   score_tile<L, WS>(kbuf[0], qf, k_rd, s);
-  softmax_stage<WS>(s, key_base(0) + 32 * kh, a.Skv, g, a.sl2, m, lsum, o, pf);
+  softmax_stage<WS>(s, pkey0 + 32 * kh, a.Skv, g, a.sl2, m, lsum, o, pf);
   __syncthreads();  // kbuf[0] is free for K(2)
 
   auto dma = [&](auto par, int j) __attribute__((always_inline)) {
@@ -1521,7 +1550,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // stage_keys, so the scalar load's wait falls on the following barrier with
   // a softmax cluster in between.  The softmax masks with a held key too:
   // stage j+1's for group A (SOFT(j)), stage j's for group B (SOFT(j-1)).
-  int kw0 = key_base(0), kw1 = key_base(1), kw2 = key_base(2), e3 = lut_entry(3);
+  int kw0 = pkey0, kw1 = pkey1, kw2 = pro_key(2), e3 = pro_entry(3);
   int soft_key = 0;
   // stage_keys(j) takes stage j's keys (K(j+2), V(j+1), the softmax mask)
   // and moves the window on; load_k / load_v issue the loads.  Group A calls
@@ -1915,13 +1944,21 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     }
   }
   pc.loop_end();
-  // Sparse, loads inside the matrix cluster: group B's last stage issued
-  // loads (of nothing: keys past its list) that no stage writes out.
-  if constexpr (kSparse) wait_vmem_all();
+  // Sparse: group B's last stage issued loads (of nothing: keys past its
+  // list) into group B's K/V buffers that may still be in flight.  The
+  // key-split exchange below writes those buffers from other waves, so there
+  // every wave waits for its loads and a barrier follows.  Otherwise nothing
+  // touches group B's buffers before this wave's next fetch into them, which
+  // lands after these (a wave's loads complete in order), and the kernel
+  // waits for them before it exits.
+  if constexpr (kKeySplit) {
+    wait_vmem_all();
+    __syncthreads();
+  }
 
   if constexpr (kKeySplit) {
-    // The loop ended on a barrier after every LDS read and write of the
-    // stages, so a group's own K/V buffers hold the exchange: O of each
+    // Every LDS read and write of the stages is complete (the barrier
+    // above), so a group's own K/V buffers hold the exchange: O of each
     // slice's key-half-1 wave in the K buffers (lane-major: 64 consecutive
     // floats per register), its m and l in the V buffers.
     static_assert(sizeof(kbuf_all[0]) >= 2 * 64 * 64 * sizeof(float), "O exchange fits a group's K buffers");
@@ -1973,6 +2010,50 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     return;
   }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+#if H3A_PP_STORE_LDS
+  // The wave's normalised O (32 rows x 128 dims, bf16) leaves through LDS.
+  // A lane holds 4-dim pieces of one row, so stored directly every
+  // instruction would write 16 bytes into each of 32 rows; written into a
+  // wave-private tile (256-byte rows, 16-byte chunks XOR-swizzled by row) and
+  // read back a chunk per lane, every store writes 4 whole rows.  The tile is
+  // free: key-split, the wave's own exchange slot, which it has read;
+  // otherwise a quarter of group A's K or V buffers, whose fetches all
+  // completed before the loop's last barrier (group B's last loads, still in
+  // flight for other waves, only touch group B's buffers).
+  {
+    uint8_t *tile;
+    if constexpr (kKeySplit) {
+      tile = reinterpret_cast<uint8_t *>(&kbuf[0][0]) + rq * (64 * 64 * 4);
+    } else {
+      tile = (wave_u < 4 ? reinterpret_cast<uint8_t *>(&kbuf_all[0][0][0])
+                         : reinterpret_cast<uint8_t *>(&vbuf_all[0][0][0])) + (wave_u & 3) * (32 * 256);
+    }
+    static_assert(sizeof(kbuf_all[0]) >= 4 * 32 * 256 && sizeof(vbuf_all[0]) >= 4 * 32 * 256,
+                  "four O tiles fit group A's K buffers and its V buffers");
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const u32x2 val = {pack_bf16x2(o[dt][4 * rr + 0] * inv, o[dt][4 * rr + 1] * inv),
+                           pack_bf16x2(o[dt][4 * rr + 2] * inv, o[dt][4 * rr + 3] * inv)};
+        const int c = 4 * dt + rr;  // 16-byte chunk of the row: dims 8c .. 8c+7
+        *(u32x2 *)(tile + l32 * 256 + ((c ^ (l32 & 15)) << 4) + 8 * g) = val;
+      }
+    }
+    // Buffer stores over the wave's valid rows: rows past Sq fall outside the
+    // resource and are dropped, so no store sits behind a branch (and a
+    // later vmcnt wait can count exactly the stores issued).
+    const int q0 = __builtin_amdgcn_readfirstlane(qrow - l32), ch = lane & 15;
+    const int nrows = a.Sq - q0 < 32 ? a.Sq - q0 : 32;
+    const __amdgpu_buffer_rsrc_t ores = stage_rsrc(Ob + (int64_t)q0 * a.oss, a.oss, nrows);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + (lane >> 4);
+      const u32x4 val = *(const u32x4 *)(tile + r * 256 + ((ch ^ (r & 15)) << 4));
+      __builtin_amdgcn_raw_buffer_store_b128(val, ores, (int)((uint32_t)r * (uint32_t)a.oss * 2u + 16u * ch), 0, 0);
+    }
+  }
+#else
   if (qrow < a.Sq) {
     uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
 #pragma unroll
@@ -1985,6 +2066,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
       }
     }
   }
+#endif
   pc.finish(wave, lane);
 }
 
@@ -2015,6 +2097,10 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     AttnArgs args;
     __builtin_memcpy(&args, words, sizeof(args));
     if (args.sched) {
+      // A take is an agent-scope atomic's round trip, about 3000 shader
+      // cycles under load.  Issued during the work item's prologue or right
+      // after its stage loop instead, it measured as fast or slower for
+      // every kernel.
       __syncthreads();
       if (threadIdx.x == 0) {
         const int xcc = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & (kQueues - 1));  // XCC_ID
@@ -2031,6 +2117,9 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
     asm volatile("" : "+s"(kq));
     if (!kq->sched) break;
   }
+  // The last work item's trailing loads (see pingpong_item) land before the
+  // workgroup ends and its LDS is released.
+  if constexpr (kSparse) wait_vmem_all();
 }
 
 // Clears the dispatch queues' counters before a dynamic launch (a kernel, not

@@ -49,22 +49,30 @@ __host__ __device__ __forceinline__ int queue_item(int whole, int pieces, int x,
   return i < sw.len ? sw.first + i : whole + sp.first + (i - sw.len);
 }
 
-// The next work item for a workgroup on XCD xcc, or -1 when every queue is
-// empty: its own queue first, then the others in turn.  load(x) reads queue
+// The next work item for a workgroup on XCD xcc (0 <= xcc < kQueues), or -1
+// when every queue is empty: its own queue first, then the others in turn.  load(x) reads queue
 // x's counter, fetch_add(x) increments it and returns the old value (agent-
 // scope atomics on the GPU).  A counter may run past its queue's length; such
-// takes find nothing.
+// takes find nothing.  A take can be split in two: the fetch-add on the own
+// queue first (its value, `own`, is only needed later), then take_finish.
 template <class Load, class FetchAdd>
-__host__ __device__ __forceinline__ int take_item_with(int whole, int pieces, int xcc, Load load,
-                                                       FetchAdd fetch_add) {
-  for (int t = 0; t < kQueues; ++t) {
+__host__ __device__ __forceinline__ int take_finish(int whole, int pieces, int xcc, int own, Load load,
+                                                    FetchAdd fetch_add) {
+  if (own < queue_len(whole, pieces, xcc)) return queue_item(whole, pieces, xcc, own);
+  for (int t = 1; t < kQueues; ++t) {
     const int x = (xcc + t) & (kQueues - 1);
     const int len = queue_len(whole, pieces, x);
-    if (t > 0 && load(x) >= len) continue;
+    if (load(x) >= len) continue;
     const int i = fetch_add(x);
     if (i < len) return queue_item(whole, pieces, x, i);
   }
   return -1;
+}
+
+template <class Load, class FetchAdd>
+__host__ __device__ __forceinline__ int take_item_with(int whole, int pieces, int xcc, Load load,
+                                                       FetchAdd fetch_add) {
+  return take_finish(whole, pieces, xcc, fetch_add(xcc), load, fetch_add);
 }
 
 }  // namespace h3a

@@ -99,7 +99,8 @@ static bool check_order(int whole, int pieces) {
 
 // Workgroups as threads taking concurrently through std::atomic counters
 // (relaxed, as on the GPU), each until it gets -1, as the kernel's item loop
-// does.  Checks: every item handed out exactly once, and once any take
+// does, half of the takes split into the own queue's fetch-add and a later
+// take_finish.  Checks: every item handed out exactly once, and once any take
 // returns -1 every queue's counter has reached its length (all items claimed).
 static bool check_concurrent(int whole, int pieces, int threads, unsigned seed) {
   const int n = whole + pieces;
@@ -117,7 +118,16 @@ static bool check_concurrent(int whole, int pieces, int threads, unsigned seed) 
       auto add = [&](int q) { return ctr[q].fetch_add(1, std::memory_order_relaxed); };
       for (;;) {
         if (rng() % 4 == 0) std::this_thread::yield();
-        const int it = h3a::take_item_with(whole, pieces, xcc, load, add);
+        int it;
+        if (rng() % 2) {
+          it = h3a::take_item_with(whole, pieces, xcc, load, add);
+        } else {
+          // The split take: the own queue's fetch-add, other takers, then the
+          // finish (as a work item's epilogue runs between the two halves).
+          const int own = add(xcc);
+          std::this_thread::yield();
+          it = h3a::take_finish(whole, pieces, xcc, own, load, add);
+        }
         if (it < 0) {
           for (int q = 0; q < kQueues; ++q)
             if (ctr[q].load() < h3a::queue_len(whole, pieces, q)) bad.fetch_or(1);
