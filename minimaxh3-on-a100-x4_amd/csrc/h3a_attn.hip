@@ -1294,6 +1294,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   int ngrp = niter, gj0 = 0;
   const int32_t *lut_row = nullptr;
   int e_pre[4] = {0, 0, 0, 0};
+  const uint32_t smag = stage_magic(a.sub);  // block_of_stage_magic(t, smag) = t / a.sub
   if constexpr (kSparse) {
     // Query sub-block qb reads LUT row qb / a.qmul (blk_q = 256: the two
     // 128-row blocks of a pair share one row; blk_q = 192: three 64-row ones).
@@ -1313,7 +1314,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     lut_row = a.lut + ((int64_t)bh * a.nqb + (qb < a.nqt ? qb : 0) / a.qmul) * a.lut_stride;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int e = block_of_stage(j, a.sub);
+      const int e = block_of_stage_magic(j, smag);
       e_pre[j] = ((ConstInts)lut_row)[e < a.lut_stride ? e : a.lut_stride - 1];
     }
     auto stages_of = [&](int qb, int cnt) __attribute__((always_inline)) -> int {
@@ -1337,19 +1338,24 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // through the constant address space, so it is a scalar load), and the
   // stage's first key from it.  Past this group's last stage, and for LUT
   // entries that name no key block, the key is Skv, which loads nothing.
+  // Both are branch-free scalar code (stage_magic, selects): they run in the
+  // softmax slots of every stage.  The entry index is clamped into the
+  // group's part of the row (entry 0 for an empty list, whose keys are all
+  // Skv whatever the entry).
   auto lut_entry = [&](int j) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      if (ngrp == 0) return -1;
       const __attribute__((address_space(4))) int32_t *row =
           (const __attribute__((address_space(4))) int32_t *)lut_row;
-      return row[block_of_stage(gj0 + (j < ngrp ? j : ngrp - 1), a.sub)];
+      const int jc = j < ngrp ? j : ngrp - 1;
+      return row[block_of_stage_magic(gj0 + (jc > 0 ? jc : 0), smag)];
     } else {
       return 0;
     }
   };
   auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      return j < ngrp ? stage_key0(a, gj0 + j, kb) : a.Skv;
+      const int key0 = lut_stage_key0_magic(gj0 + j, kb, a.nkb, a.blk_k, a.sub, smag, a.Skv);
+      return j < ngrp ? key0 : a.Skv;
     } else {
       return j < niter ? (j0 + j) * BN : a.Skv;
     }

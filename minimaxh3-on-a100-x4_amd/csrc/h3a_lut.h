@@ -16,6 +16,18 @@ __host__ __device__ __forceinline__ int block_of_stage(int t, int sub) {
   return sub == 3 ? (int)(((uint64_t)(uint32_t)t * 0x55555556u) >> 32) : t >> (sub >> 1);
 }
 
+// The same without a branch on sub: t / sub = high 32 bits of (2t) * magic,
+// magic = ceil(2^31 / sub) for sub = 1, 2, 4 (exact powers of two) and
+// (2^32 + 1) / 6 for sub = 3 (2t * magic / 2^32 = (t / 3)(1 + 2^-32), whose
+// floor is t / 3 for 0 <= t < 2^31).  stage_magic is computed once per work
+// item; block_of_stage_magic is one shift and one multiply-high.
+__host__ __device__ __forceinline__ uint32_t stage_magic(int sub) {
+  return sub == 3 ? 0x2AAAAAABu : 0x80000000u >> (sub >> 1);
+}
+__host__ __device__ __forceinline__ int block_of_stage_magic(int t, uint32_t magic) {
+  return (int)(((uint64_t)((uint32_t)t << 1) * magic) >> 32);
+}
+
 // First key of stage t of a LUT row whose entry for that stage's block is
 // kb, or Skv (a stage that loads nothing and is fully masked) when kb names
 // no key block (kb < 0 or kb >= nkb = ceil(Skv / blk_k)).  kb is checked
@@ -25,6 +37,15 @@ __host__ __device__ __forceinline__ int lut_stage_key0(int t, int kb, int nkb, i
   if ((uint32_t)kb >= (uint32_t)nkb) return Skv;
   const int key0 = kb * blk_k + (t - block_of_stage(t, sub) * sub) * kLutStageKeys;
   return key0 < Skv ? key0 : Skv;
+}
+// The same with the block from block_of_stage_magic (magic = stage_magic(sub))
+// and selects instead of an early return; the key is formed in unsigned
+// arithmetic (it only wraps for a kb that is then discarded).
+__host__ __device__ __forceinline__ int lut_stage_key0_magic(int t, int kb, int nkb, int blk_k, int sub,
+                                                             uint32_t magic, int Skv) {
+  const uint32_t off = (uint32_t)(t - block_of_stage_magic(t, magic) * sub) * (uint32_t)kLutStageKeys;
+  const int key0 = (int)((uint32_t)kb * (uint32_t)blk_k + off);
+  return (uint32_t)kb >= (uint32_t)nkb ? Skv : (key0 < Skv ? key0 : Skv);
 }
 
 }  // namespace h3a

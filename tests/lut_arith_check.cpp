@@ -24,11 +24,17 @@ int main() {
   for (int t : {INT_MAX, INT_MAX - 1, INT_MAX - 2, 1 << 30, (1 << 30) + 1, (1 << 30) - 1, 3 << 29})
     ts.push_back(t);
   for (int sub = 1; sub <= 4; ++sub)
-    for (int t : ts)
+    for (int t : ts) {
       if (h3a::block_of_stage(t, sub) != t / sub) {
         printf("block_of_stage(%d, %d) = %d, want %d\n", t, sub, h3a::block_of_stage(t, sub), t / sub);
         return 1;
       }
+      if (h3a::block_of_stage_magic(t, h3a::stage_magic(sub)) != t / sub) {
+        printf("block_of_stage_magic(%d, %d) = %d, want %d\n", t, sub,
+               h3a::block_of_stage_magic(t, h3a::stage_magic(sub)), t / sub);
+        return 1;
+      }
+    }
   const int skvs[] = {1, 63, 64, 65, 127, 129, 255, 257, 42120, 46052, 1 << 24, INT_MAX - 256};
   for (int Skv : skvs)
     for (int blk_k : {64, 128, 192, 256}) {
@@ -47,6 +53,12 @@ int main() {
           if (got != want || got < 0 || got > Skv) {
             printf("lut_stage_key0(t=%d, kb=%d, nkb=%lld, blk_k=%d, Skv=%d) = %d, want %d\n", t, kb,
                    (long long)nkb, blk_k, Skv, got, want);
+            return 1;
+          }
+          const int got_m = h3a::lut_stage_key0_magic(t, kb, (int)nkb, blk_k, sub, h3a::stage_magic(sub), Skv);
+          if (got_m != want) {
+            printf("lut_stage_key0_magic(t=%d, kb=%d, nkb=%lld, blk_k=%d, Skv=%d) = %d, want %d\n", t, kb,
+                   (long long)nkb, blk_k, Skv, got_m, want);
             return 1;
           }
         }
