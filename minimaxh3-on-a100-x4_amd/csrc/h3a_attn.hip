@@ -1018,10 +1018,20 @@ template <int NSUB, bool kMaybeEmpty = false>
 __device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0, int Skv, int g, float sl2,
                                                     float &m, float &lsum, f32x16 (&o)[4],
                                                     u32x4 (&pf)[2 * NSUB]) {
-  if (key0 + 32 * NSUB > Skv) mask_tail<NSUB>(s, key0, Skv, g);
+  // Both branches are rare (a stage that reaches past Skv, a refresh).  With
+  // 64-key waves they are marked so (kHint), and the common path falls
+  // through instead of branching around their code in every stage (measured
+  // +0.4 % dense, +0.5 % 128x128 sparse); the 32-key waves of the key-split
+  // kernel lost 3 % with that layout.  (The hint has to sit in the branch
+  // condition itself.)
+  constexpr bool kHint = NSUB >= 2;
+  const bool past = key0 + 32 * NSUB > Skv;
+  if (kHint ? __builtin_expect(past, 0) : past) mask_tail<NSUB>(s, key0, Skv, g);
   float ps;
   exp_pack_sum<NSUB>(s, sl2, kMaybeEmpty && m == kNegInf ? 0.f : m, pf, ps);
-  if (__builtin_amdgcn_ballot_w64(!(ps <= kStaleSumLimit) || (kMaybeEmpty && m == kNegInf)) != 0) {
+  const bool refresh =
+      __builtin_amdgcn_ballot_w64(!(ps <= kStaleSumLimit) || (kMaybeEmpty && m == kNegInf)) != 0;
+  if (kHint ? __builtin_expect(refresh, 0) : refresh) {
     const float mnew = fmaxf(m, tile_max<NSUB>(s, sl2));
     const float alpha = fast_exp2(m - (kMaybeEmpty && mnew == kNegInf ? 0.f : mnew));
     m = mnew;
@@ -1354,7 +1364,11 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   };
   auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      const int key0 = lut_stage_key0_magic(gj0 + j, kb, a.nkb, a.blk_k, a.sub, smag, a.Skv);
+      // Two equivalent forms; each measured faster in one kernel (the
+      // arithmetic one +0.5 % in the 128-row pairs, the select one +0.6 % in
+      // the key-split pairs), through the code layout around them.
+      const int key0 = kKeySplit ? lut_stage_key0_sel(gj0 + j, kb, a.nkb, a.blk_k, a.sub, smag, a.Skv)
+                                 : lut_stage_key0_magic(gj0 + j, kb, a.nkb, a.blk_k, a.sub, smag, a.Skv);
       return j < ngrp ? key0 : a.Skv;
     } else {
       return j < niter ? (j0 + j) * BN : a.Skv;

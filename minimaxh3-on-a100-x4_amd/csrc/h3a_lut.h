@@ -39,13 +39,26 @@ __host__ __device__ __forceinline__ int lut_stage_key0(int t, int kb, int nkb, i
   return key0 < Skv ? key0 : Skv;
 }
 // The same with the block from block_of_stage_magic (magic = stage_magic(sub))
-// and selects instead of an early return; the key is formed in unsigned
-// arithmetic (it only wraps for a kb that is then discarded).
-__host__ __device__ __forceinline__ int lut_stage_key0_magic(int t, int kb, int nkb, int blk_k, int sub,
-                                                             uint32_t magic, int Skv) {
+// and the range checks as selects; the key is formed in unsigned arithmetic
+// (it only wraps for a kb that is then discarded).
+__host__ __device__ __forceinline__ int lut_stage_key0_sel(int t, int kb, int nkb, int blk_k, int sub,
+                                                           uint32_t magic, int Skv) {
   const uint32_t off = (uint32_t)(t - block_of_stage_magic(t, magic) * sub) * (uint32_t)kLutStageKeys;
   const int key0 = (int)((uint32_t)kb * (uint32_t)blk_k + off);
   return (uint32_t)kb >= (uint32_t)nkb ? Skv : (key0 < Skv ? key0 : Skv);
+}
+
+// The same as pure arithmetic, with the block from block_of_stage_magic
+// (magic = stage_magic(sub)): an entry outside [0, nkb) is replaced by nkb,
+// whose first key nkb * blk_k is already >= Skv, so the final min with Skv
+// gives Skv for it.  Unsigned, so nothing overflows for Skv <= INT_MAX - 256
+// (nkb * blk_k + off < Skv + 2 * blk_k < 2^32).
+__host__ __device__ __forceinline__ int lut_stage_key0_magic(int t, int kb, int nkb, int blk_k, int sub,
+                                                             uint32_t magic, int Skv) {
+  const uint32_t off = (uint32_t)(t - block_of_stage_magic(t, magic) * sub) * (uint32_t)kLutStageKeys;
+  const uint32_t kbc = (uint32_t)kb < (uint32_t)nkb ? (uint32_t)kb : (uint32_t)nkb;
+  const uint32_t key0 = kbc * (uint32_t)blk_k + off;
+  return (int)(key0 < (uint32_t)Skv ? key0 : (uint32_t)Skv);
 }
 
 }  // namespace h3a

@@ -56,9 +56,10 @@ int main() {
             return 1;
           }
           const int got_m = h3a::lut_stage_key0_magic(t, kb, (int)nkb, blk_k, sub, h3a::stage_magic(sub), Skv);
-          if (got_m != want) {
-            printf("lut_stage_key0_magic(t=%d, kb=%d, nkb=%lld, blk_k=%d, Skv=%d) = %d, want %d\n", t, kb,
-                   (long long)nkb, blk_k, Skv, got_m, want);
+          const int got_s = h3a::lut_stage_key0_sel(t, kb, (int)nkb, blk_k, sub, h3a::stage_magic(sub), Skv);
+          if (got_m != want || got_s != want) {
+            printf("lut_stage_key0_magic / _sel(t=%d, kb=%d, nkb=%lld, blk_k=%d, Skv=%d) = %d / %d, want %d\n", t,
+                   kb, (long long)nkb, blk_k, Skv, got_m, got_s, want);
             return 1;
           }
         }
