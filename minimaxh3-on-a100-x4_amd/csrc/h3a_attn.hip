@@ -142,9 +142,14 @@ namespace h3a {
 #define H3A_SPARSE64_PINGPONG 1
 #endif
 // LDS operand reads issued ahead of the first MFMA of a ping-pong matrix
-// cluster (0: leave the order to the scheduler).
+// cluster (0: leave the order to the scheduler); block-sparse kernels and
+// the dense kernel separately (same-box sweep: dense 4 +0.4 % over 6, 8
+// -0.4 %; sparse 6, with 4 -0.3 % at 128x128 and -0.9 % at 64x64).
 #ifndef H3A_PP_READ_AHEAD
 #define H3A_PP_READ_AHEAD 6
+#endif
+#ifndef H3A_PP_DENSE_READ_AHEAD
+#define H3A_PP_DENSE_READ_AHEAD 4
 #endif
 // Dense ping-pong fetch split: instructions of each K and V stage (4 per wave
 // column: waves w and w+4 of the two groups) that the group-A wave issues
@@ -200,9 +205,14 @@ namespace h3a {
 #define H3A_PP_STORE_LDS 1
 #endif
 // Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
-// during the softmax cluster (2), or never (0).
+// during the softmax cluster (2), or never (0); block-sparse kernels and the
+// dense kernel separately (same-box sweep: dense 0 +0.2 % over 1; sparse 1,
+// with 0 -2.8 % at 128x128 and -3 % at 64x64).
 #ifndef H3A_PP_PRIO
 #define H3A_PP_PRIO 1
+#endif
+#ifndef H3A_PP_DENSE_PRIO
+#define H3A_PP_DENSE_PRIO 0
 #endif
 // Workgroup barrier between the two clusters of a ping-pong stage (1), or
 // only the one at the end of the stage (0), which the LDS buffers need.  The
@@ -1463,6 +1473,8 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // Dense, DMA spread over group A's matrix clusters: group A fetches all.
   constexpr bool kDenseIn = kSplitDma && H3A_PP_DMA_IN_CLUSTER;
   constexpr bool kSpIn = kSpDma && (kKeySplit ? H3A_SPARSE64_PP_IN_CLUSTER : H3A_SPARSE_PP_IN_CLUSTER);
+  constexpr int kReadAhead = kSparse ? H3A_PP_READ_AHEAD : H3A_PP_DENSE_READ_AHEAD;
+  constexpr int kPrio = kSparse ? H3A_PP_PRIO : H3A_PP_DENSE_PRIO;
   constexpr int kKA = kDenseIn ? kKI : (kSplitDma ? H3A_PP_A_KINST : 0);
   constexpr int kVA = kDenseIn ? kVI : (kSplitDma ? H3A_PP_A_VINST : 0);
   auto fetch_k = [&](const uint16_t *base, int key0, uint16_t *tile) __attribute__((always_inline)) {
@@ -1639,11 +1651,11 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   constexpr bool kASoft = kSplitDma && !kDenseIn && !kALate && H3A_PP_A_SOFT && (kKA + kVA > 0);
   // One basic block: 16*NSUB MFMAs (the last stage's scores are of
   // the zero tile past the keys and are discarded), with the 24*NSUB LDS
-  // operand reads issued ahead of them: H3A_PP_READ_AHEAD up front, then 2
+  // operand reads issued ahead of them: kReadAhead up front, then 2
   // after each MFMA, so every read is in flight for several MFMAs.
   auto mfma = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
-    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(1);
+    if (kPrio == 1) __builtin_amdgcn_s_setprio(1);
 #if H3A_PP_PV_FIRST
     pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o);
     score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s);
@@ -1662,16 +1674,16 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
       kst.start(Kb, a.kss, key_k, a.Skv, nullptr);
       vst.start(Vb, a.vss, key_v, a.Skv, nullptr);
     }
-#if H3A_PP_READ_AHEAD
-    __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
+    if constexpr (kReadAhead > 0) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kReadAhead, 0);
 #pragma unroll
-    for (int i = 0; i < 16 * WS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
-      if (kLoadsIn && i >= 16 * WS - 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      for (int i = 0; i < 16 * WS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
+        if (kLoadsIn && i >= 16 * WS - 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
     }
-#endif
-    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(0);
+    if (kPrio == 1) __builtin_amdgcn_s_setprio(0);
   };
   // The matrix cluster with this wave's fetch of K(j+2) (kseq) and V(j+1)
   // (vseq) spread over it: the K instructions after evenly spaced score
@@ -1686,7 +1698,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     constexpr int NKS = 2 * WS;  // PV key steps
     static_assert(NK > 0 && 8 % NK == 0, "K instructions spread evenly over 8 score k-steps");
     static_assert(NV > 0 && (NV % NKS == 0 || NKS % NV == 0), "V instructions spread evenly over the PV steps");
-    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(1);
+    if (kPrio == 1) __builtin_amdgcn_s_setprio(1);
     score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s, [&](int ks) __attribute__((always_inline)) {
       if (!kDmaPvOnly && (ks + 1) % (8 / NK) == 0) kseq.issue();
     });
@@ -1710,18 +1722,18 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         }
       }
     });
-#if H3A_PP_READ_AHEAD
-    __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READ_AHEAD, 0);
+    if constexpr (kReadAhead > 0) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kReadAhead, 0);
 #pragma unroll
-    for (int i = 0; i < 16 * WS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
+      for (int i = 0; i < 16 * WS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
+      }
     }
-#endif
-    if (H3A_PP_PRIO == 1) __builtin_amdgcn_s_setprio(0);
+    if (kPrio == 1) __builtin_amdgcn_s_setprio(0);
   };
   auto soft = [&](int j) __attribute__((always_inline)) {
-    if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(1);
+    if (kPrio == 2) __builtin_amdgcn_s_setprio(1);
     const int key0 = (kSparse ? soft_key : key_base(j + 1)) + 32 * kh;
 #if H3A_PP_STALE_MAX
     softmax_stage_stale<WS, kSparse>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
@@ -1734,7 +1746,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     pin(lsum);
     pin(m);
 #endif
-    if (H3A_PP_PRIO == 2) __builtin_amdgcn_s_setprio(0);
+    if (kPrio == 2) __builtin_amdgcn_s_setprio(0);
   };
 
   pc.loop_begin();
