@@ -1094,12 +1094,17 @@ struct PhaseClock {
       last = __builtin_amdgcn_s_memtime();
     }
   }
-  // Ticks since the previous mark go to phase i.
+  // Ticks since the previous mark go to phase i.  A mark is a scheduling
+  // fence, so each phase holds exactly the code written between its marks
+  // (s_memtime depends on nothing, and the scheduler would otherwise move it
+  // among the MFMAs of a cluster).
   __device__ __forceinline__ void mark(int i) {
     if constexpr (H3A_PROFILE) {
+      __builtin_amdgcn_sched_barrier(0);
       const uint64_t t = __builtin_amdgcn_s_memtime();
       ph[i] += (uint32_t)(t - last);
       last = t;
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   __device__ __forceinline__ void loop_begin() {
