@@ -30,6 +30,7 @@ FLOP_PER_CLK = 256 * 4096  # dense bf16 MFMA, whole chip
 # "roofline.traffic = <bytes> B" is read at run time.
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_h56_s42120_counters.txt")
 SPARSE_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_sparse_h56_s42120_counters.txt")
+PROLOGUE_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "prologue_s8192_h56.txt")
 B, H, S, D, LAYERS = 1, 56, 42120, 128, 50
 
 
@@ -420,6 +421,7 @@ def run_prologue(args, torch, h3attn, dev):
     _calib_copy(args, torch, dev)
     nbytes = prologue_bytes(s_len, H, rot)
     gbs = nbytes / (avg_kernel_ms * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic(PROLOGUE_TRAFFIC_SUMMARY, "prologue")
     res = _base(args, "qk-RMSNorm+RoPE prologue GB/s (algorithmic bytes) at S=8192,H=56,D=128",
                 nbytes * n * args.steps / (span_ms * 1e-3) / 1e9, "GB/s", span_ms / args.steps,
                 {"workload": f"in-place qk-RMSNorm + split-half RoPE on fused-QKV views, {n} calls per step "
@@ -428,7 +430,7 @@ def run_prologue(args, torch, h3attn, dev):
     res.update({
         "us_per_call": round(avg_kernel_ms * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(gbs / 8000.0, 4), "traffic": None,
+                     "frac": round(gbs / 8000.0, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "qk_rmsnorm_rope_kernel", "bytes_per_launch": nbytes,
                      "avg_launch_ms": round(avg_kernel_ms, 4)},
     })

@@ -6,13 +6,13 @@
 // the fused QKV projection output.  It is HBM-bound: every q/k row is read
 // once and written once (4*S*H*D*2 bytes) plus one rope row per token.
 //
-// Layout of the work: one wave owns one (b,s) token and a chunk of 16 heads.
-// Its four 16-lane groups walk the chunk one head each per step; within a
-// group each lane holds 8 consecutive dims (one 128-bit access), so one wave
-// access moves four whole 256-byte head rows (1 KB contiguous in the fused
-// QKV layout).  The token's RoPE matrices and the two weight vectors are
-// loaded into registers once per wave and reused for all 2 x 16 rows; the
-// 8 row loads of the chunk are issued before any math.  The sum of squares
+// Layout of the work: one wave owns one (b,s) token and a chunk of HPW heads
+// (28 or 16, chosen per launch).  Its four 16-lane groups walk the chunk
+// one head each per step; within a group each lane holds 8 consecutive dims
+// (one 128-bit access), so one wave access moves four whole 256-byte head rows
+// (1 KB contiguous in the fused QKV layout).  The token's RoPE matrices and
+// the two weight vectors are loaded into registers once per wave and reused
+// for all 2 x HPW rows; the chunk's row loads are issued before any math.  The sum of squares
 // is reduced across the 16 lanes with xor shuffles; the RoPE partner dims
 // (i, i+rot/2) sit rot/16 lanes apart and are fetched with one shuffle each.
 #include "h3a_device.h"
@@ -43,8 +43,13 @@ __device__ __forceinline__ u32x4 pack8(const float (&x)[8]) {
                pack_bf16x2(x[6], x[7])};
 }
 
-constexpr int kHeadsPerWave = 16;
-constexpr int kSteps = kHeadsPerWave / 4;  // heads per 16-lane group
+// Heads per wave (HPW, a multiple of 4: four 16-lane groups): 28 when it
+// divides H, otherwise 16.  At H=56, 28 gives two full waves per token, each
+// reading the token's RoPE row once (same box: 5.41 TB/s against 5.15 with 16
+// heads, of which the fourth wave per token has 8; 4.80 with 8 full waves and
+// 5.00 with one wave of all 56, whose 201 VGPRs halve the waves in flight);
+// non-temporal stores changed nothing.
+__host__ __device__ constexpr int rope_heads_per_wave(int H) { return H % 28 == 0 ? 28 : 16; }
 
 // y = rmsnorm(x) * w, then rotate pairs (i, i+rot/2) with the lane's 2x2 matrices.
 __device__ __forceinline__ void norm_rope_row(float (&x)[8], const float (&w)[8], float eps,
@@ -71,7 +76,10 @@ __device__ __forceinline__ void norm_rope_row(float (&x)[8], const float (&w)[8]
   }
 }
 
+template <int kHeadsPerWave>
 __global__ void __launch_bounds__(256) qk_rmsnorm_rope_kernel(RopeArgs a) {
+  static_assert(kHeadsPerWave % 4 == 0, "four 16-lane groups per wave");
+  constexpr int kSteps = kHeadsPerWave / 4;  // heads per 16-lane group
   const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, c = lane & 15;
   const int nchunk = (a.H + kHeadsPerWave - 1) / kHeadsPerWave;
   const int64_t item = (int64_t)blockIdx.x * 4 + (tid >> 6);  // (token, head chunk)
@@ -121,15 +129,19 @@ __global__ void __launch_bounds__(256) qk_rmsnorm_rope_kernel(RopeArgs a) {
 }
 
 int launch_qk_rmsnorm_rope(const RopeArgs &a, hipStream_t s) {
-  const int64_t items = (int64_t)a.B * a.S * ((a.H + kHeadsPerWave - 1) / kHeadsPerWave);
+  const int hpw = rope_heads_per_wave(a.H);
+  const int64_t items = (int64_t)a.B * a.S * ((a.H + hpw - 1) / hpw);
   const int64_t blocks = (items + 3) / 4;
-  hipLaunchKernelGGL(qk_rmsnorm_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  if (hpw == 28)
+    hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<28>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(qk_rmsnorm_rope_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, s, a);
   return check_launch("qk_rmsnorm_rope_kernel");
 }
 
 int rope_kernel_attrs(double out[6]) {
   hipFuncAttributes fa;
-  const void *fn = reinterpret_cast<const void *>(&qk_rmsnorm_rope_kernel);
+  const void *fn = reinterpret_cast<const void *>(&qk_rmsnorm_rope_kernel<28>);  // the H=56 width
   if (hipFuncGetAttributes(&fa, fn) != hipSuccess) return fail(H3A_ERR_HIP, "hipFuncGetAttributes failed");
   int blocks = 0, dev = 0, clk = 0, max_threads = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) != hipSuccess ||

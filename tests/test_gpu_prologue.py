@@ -52,6 +52,7 @@ def _run_gpu(xq, xk, w, rope, rot, device, fused_layout):
 
 @pytest.mark.parametrize("S,H,rot,fused", [
     (37, 3, 128, False), (37, 3, 64, True), (5, 1, 0, False), (200, 7, 128, True), (64, 56, 32, True),
+    (33, 28, 128, True), (17, 84, 64, False),  # 28 heads per wave: one chunk, three chunks
 ])
 def test_prologue_small(gpu, S, H, rot, fused):
     rng = np.random.default_rng(S * 100 + rot)

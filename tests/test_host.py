@@ -69,7 +69,7 @@ def test_bench_refuses_multi_gpu():
 
 
 def test_bench_reads_traffic_from_the_committed_counter_summaries():
-    """The roofline "traffic" of the dense and sparse bench lines comes from the
+    """The roofline "traffic" of the dense, sparse and prologue bench lines comes from the
     profiles/ counter summaries (a "roofline.traffic[.key] = X B" line), not a constant."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("bench_mod", f"{ROOT}/bench.py")
@@ -82,6 +82,10 @@ def test_bench_reads_traffic_from_the_committed_counter_summaries():
         assert src.endswith("attn_sparse_h56_s42120_counters.txt") and 1e9 < t < 1e11, (blk, t, src)
     t, why = bench.measured_traffic(bench.SPARSE_TRAFFIC_SUMMARY, "sparse192")
     assert t is None and "no roofline.traffic" in why
+    # the prologue moves each byte once: its counters read the algorithmic bytes
+    t, src = bench.measured_traffic(bench.PROLOGUE_TRAFFIC_SUMMARY, "prologue")
+    alg = bench.prologue_bytes(8192, 56, 128)
+    assert src.endswith("prologue_s8192_h56.txt") and 0.99 * alg < t < 1.02 * alg, (t, alg)
 
 
 # ----------------------------------------------------------------------------- h3_sla schedule
