@@ -76,6 +76,37 @@ def test_sparse_mixed_block_sizes(gpu, blk_q, blk_k, S, split):
     assert_close_absmax(got, ref, what=f"sparse blk_q={blk_q} blk_k={blk_k}")
 
 
+@pytest.mark.parametrize("blk_q,blk_k,Sq,Skv,split", [(128, 128, 700, 1100, True), (64, 64, 1100, 700, False),
+                                                       (192, 128, 900, 1300, True), (256, 64, 1000, 600, False)])
+def test_sparse_batched_cross_lengths_strided_side_stream(gpu, blk_q, blk_k, Sq, Skv, split):
+    """B=2 with Sq != Skv (either way round), q read from a [B,Sq,H,D] buffer and k/v from
+    one fused [B,Skv,2*H*D] buffer through strided [B,H,S,D] views, O written into a
+    strided view, on a side stream: the masked oracle on the same block map."""
+    rng = np.random.default_rng(blk_q * 31 + blk_k + Sq + Skv)
+    B, H, D = 2, 3, 128
+    q, k, v = randn_bf16(rng, (B, H, Sq, D)), randn_bf16(rng, (B, H, Skv, D)), randn_bf16(rng, (B, H, Skv, D))
+    nk = -(-Skv // blk_k)
+    bmap = oracle.block_map(q, k, blk_q, blk_k, keep=max(1, nk // 3), force_diag=True)
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    qbuf = to_dev_bf16(np.ascontiguousarray(q.transpose(0, 2, 1, 3)), gpu)          # [B,Sq,H,D]
+    kv = np.concatenate([k.transpose(0, 2, 1, 3).reshape(B, Skv, H * D),
+                         v.transpose(0, 2, 1, 3).reshape(B, Skv, H * D)], axis=2)    # [B,Skv,2HD]
+    kvbuf = to_dev_bf16(np.ascontiguousarray(kv), gpu)
+    qd = qbuf.transpose(1, 2)
+    kd = kvbuf[:, :, :H * D].view(B, Skv, H, D).transpose(1, 2)
+    vd = kvbuf[:, :, H * D:].view(B, Skv, H, D).transpose(1, 2)
+    obuf = torch.full((B, Sq, H, D), 7.0, dtype=torch.bfloat16, device=gpu)
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        h3attn.attn_fwd_blocksparse(qd, kd, vd, lut, cnt, blk_q, blk_k, out=obuf.transpose(1, 2),
+                                    split_tail=split)
+    side.synchronize()
+    got = oracle.bf16_to_f32(from_dev_bf16(obuf.transpose(1, 2))).reshape(B, H, Sq, D)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk_q, blk_k=blk_k)
+    assert_close_absmax(got, ref, what=f"sparse B=2 Sq={Sq} Skv={Skv} blk_q={blk_q} blk_k={blk_k}")
+
+
 def test_sparse_unsupported_block_sizes_raise(gpu):
     q = torch.zeros(1, 1, 256, 128, dtype=torch.bfloat16, device=gpu)
     lut = torch.zeros(1, 1, 8, 1, dtype=torch.int32, device=gpu)
