@@ -84,6 +84,42 @@ def test_graph_capture_of_wide_block_select(gpu):
             assert torch.equal(o, w), f"replay {r}: {name} differs from the eager call"
 
 
+def test_graph_replay_of_queued_launches(gpu):
+    """Launches of at least four rounds of work items run on the persistent grid fed by
+    the per-XCD queues, whose counters a kernel zeroes before each launch, and here also
+    split their last round (H=9, S=32768: 1152 tiles, and 1152 pairs of 128-row blocks).
+    Dense and block-sparse attention captured in one graph: every replay, with eager
+    work and cleared outputs in between, equals the eager calls bit for bit."""
+    g = torch.Generator(device=gpu).manual_seed(43)
+    B, H, S = 1, 9, 32768
+    q, k, v = (torch.randn(B, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    nq = S // 128
+    bmap = torch.rand(B, H, nq, nq, generator=g, device=gpu) < 0.25
+    diag = torch.arange(nq, device=gpu)
+    bmap[..., diag, diag] = True
+    lut, cnt = h3attn.block_map_to_lut(bmap.to(torch.uint8))
+    partials = 128 * 2 * 256 * 130 * 4  # 128 last-round items, two key ranges each
+    assert ops.attn_workspace_bytes(B, H, S, S) >= partials + 1024
+    assert ops.sparse_workspace_bytes(B, H, S, S, 128, 128, lut.shape[3]) >= partials + 1024
+
+    def fn():
+        return h3attn.attn_fwd(q, k, v), h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, 128, 128)
+
+    want = [t.clone() for t in fn()]
+    torch.cuda.synchronize()
+    graph, outs = graphs.capture(fn, warmup=1)
+    other = torch.randn(1, 2, 300, 128, device=gpu, dtype=torch.bfloat16)
+    for r in range(3):
+        h3attn.attn_fwd(other, other, other)  # unrelated eager work between replays
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, o, w in zip(("dense", "sparse"), outs, want):
+            assert torch.equal(o, w), f"replay {r}: {name} differs from the eager call"
+
+
 def test_graph_capture_requires_capture_before_replay(gpu):
     layers, _ = _layers(gpu, n=1)
     with pytest.raises(RuntimeError):
