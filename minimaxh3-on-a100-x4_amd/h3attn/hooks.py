@@ -30,7 +30,7 @@ from typing import Callable
 
 import torch
 
-from . import ops, profiling, sla
+from . import _lib, ops, profiling, sla
 
 _state = threading.local()
 
@@ -88,12 +88,8 @@ def make_override(attention: Callable = hip_optimized_attention, log=print):
 
 # ---------------------------------------------------------------------------
 # h3_sla-compatible scope flag, schedule and sparse override
-def install_scope_patch(attention_cls) -> None:
-    """Mark DiT-block attention calls (rope_freqs is not None) in a thread-local flag (idempotent)."""
-    fwd = attention_cls.forward
-    if getattr(fwd, "_h3attn_scope", False):
-        return
-
+def _scope_wrap(fwd):
+    """`fwd` with the DiT-scope flag and the block's layer tag set around each call."""
     def scoped(self, x, rope_freqs=None, transformer_options={}):
         prev = getattr(_state, "on", False), getattr(_state, "layer", None)
         _state.on = rope_freqs is not None
@@ -105,11 +101,39 @@ def install_scope_patch(attention_cls) -> None:
 
     scoped._h3attn_scope = True
     scoped._h3attn_orig = fwd
-    attention_cls.forward = scoped
+    return scoped
+
+
+def install_scope_patch(attention_cls) -> None:
+    """Mark DiT-block attention calls (rope_freqs is not None) in a thread-local flag (idempotent).
+
+    The scope wrapper stays outermost: install() / uninstall() place the
+    patched forward beneath it whichever of the two is installed first.
+    """
+    if not getattr(attention_cls.forward, "_h3attn_scope", False):
+        attention_cls.forward = _scope_wrap(attention_cls.forward)
 
 
 def in_dit_scope() -> bool:
     return bool(getattr(_state, "on", False))
+
+
+def _first_sigma(transformer_options) -> bool:
+    """True at the first sampling step of a run: the current sigma is the schedule's first.
+
+    ComfyUI passes the step's sigma as transformer_options["sigmas"] and the
+    run's whole schedule as ["sample_sigmas"]; without either (or if they
+    cannot be read) every call counts as a first step, as the node treats it
+    (custom_nodes/h3_sla/__init__.py:157-162).
+    """
+    try:
+        cur = transformer_options.get("sigmas")
+        run = transformer_options.get("sample_sigmas")
+        if cur is None or run is None:
+            return True
+        return float(cur.flatten()[0]) >= float(run.flatten()[0]) - 1e-6
+    except Exception:
+        return True
 
 
 class Schedule:
@@ -118,18 +142,26 @@ class Schedule:
     blk is checked here, when the schedule is built, as the node checks its
     kernel when it patches the model (h3_sla:331): an unsupported size raises
     ValueError instead of turning every sparse layer into a dense one later.
-    timing (default: env H3_SLA_TIMING == "1", as at h3_sla:147) records HIP
-    events around each sparse layer; they are resolved at the last layer of a
-    step (h3_sla:199-212) into attn_ms / attn_n per layer.
+
+    Layer 0 of every step resolves the timing events still pending from the
+    previous step; layer 0 of a run's first step (its first sigma) also counts
+    a new generation and logs the schedule summary on rank 0
+    (h3_sla:155-170).  timing (default: env H3_SLA_TIMING == "1", as at
+    h3_sla:147) records HIP events around each sparse layer; they are also
+    resolved at a step's last layer, whatever its keep, into attn_ms / attn_n
+    per layer.  A failure while resolving them is logged and drops the
+    events: timing never changes what a layer computes.
     """
 
     def __init__(self, name: str, keeps, blk: int = 64, force_diag: bool = False, smooth_k: bool = True,
-                 timing: bool | None = None):
+                 timing: bool | None = None, log=print):
         self.name, self.keeps, self.blk = name, [float(x) for x in keeps], sla.check_block(blk)
         self.force_diag, self.smooth_k = force_diag, smooth_k
         self.default_keep = max(set(self.keeps), key=self.keeps.count) if self.keeps else 1.0
         self.summary = sla.schedule_summary(name, self.keeps, self.blk) if self.keeps else None
         self.timing = (os.environ.get("H3_SLA_TIMING") == "1") if timing is None else bool(timing)
+        self.log = log
+        self.generation = 0
         self._ev = []
         self.attn_ms = [0.0] * len(self.keeps)
         self.attn_n = [0] * len(self.keeps)
@@ -143,11 +175,26 @@ class Schedule:
         """Resolve the recorded events into attn_ms / attn_n (synchronises on the last one)."""
         if not self._ev:
             return
-        self._ev[-1][2].synchronize()
-        for layer, a, b in self._ev:
-            self.attn_ms[layer] += a.elapsed_time(b)
+        pending, self._ev = self._ev, []
+        try:
+            pending[-1][2].synchronize()
+            times = [(layer, a.elapsed_time(b)) for layer, a, b in pending]
+        except Exception as e:
+            self.log(f"[h3_sla] timing events dropped: {e}")
+            return
+        for layer, ms in times:
+            self.attn_ms[layer] += ms
             self.attn_n[layer] += 1
-        self._ev = []
+
+    def generation_start(self, transformer_options) -> bool:
+        """Layer 0 of a step: flush timings; at a run's first sigma, count and report a generation."""
+        self.flush_timing()
+        if not _first_sigma(transformer_options or {}):
+            return False
+        self.generation += 1
+        if int(os.environ.get("RANK", "0")) == 0 and self.summary is not None:
+            self.log(sla.format_summary(self.summary))
+        return True
 
     def attn_ms_per_layer_call(self):
         """Mean sparse-attention ms per call for each layer (None where it never ran)."""
@@ -158,20 +205,26 @@ class Schedule:
 
     def run(self, layer, q, k, v, transformer_options=None):
         """[1,H,S,D] sparse output, or None (keep >= 1: caller runs dense)."""
+        if layer == 0:
+            self.generation_start(transformer_options)
         keep = self.keep_for(layer)
+        tracked = self.timing and layer is not None and 0 <= layer < len(self.keeps)
+        last = layer is not None and layer == len(self.keeps) - 1
         if keep >= 1.0:
-            return None
-        if self.timing and layer is not None and 0 <= layer < len(self.keeps):
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record()
-            o = self._sparse(q, k, v, keep)
-            b.record()
-            self._ev.append((layer, a, b))
-            if layer == len(self.keeps) - 1:  # end of a denoise step
+            if last:
                 self.flush_timing()
-            return o
-        return self._sparse(q, k, v, keep)
+            return None
+        if not tracked:
+            return self._sparse(q, k, v, keep)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        o = self._sparse(q, k, v, keep)
+        b.record()
+        self._ev.append((layer, a, b))
+        if last:
+            self.flush_timing()
+        return o
 
 
 def make_sla_override(topk: float = 0.35, blk: int = 64, schedule: Schedule | None = None,
@@ -179,28 +232,115 @@ def make_sla_override(topk: float = 0.35, blk: int = 64, schedule: Schedule | No
     """HIP counterpart of h3_sla's _make_override (custom_nodes/h3_sla/__init__.py:265-284).
 
     Active only inside DiT-block attention (install_scope_patch) with mask=None
-    and head_dim 128; returns [1,S,H*D]; any exception falls back to `func`.
-    The block size is checked here (ValueError), not at the first call.
+    and head_dim 128; returns [1,S,H*D].  Without a schedule every such call
+    keeps `topk`; with one, the layer index the scope patch recorded picks the
+    keep (a keep of 1 or more leaves the layer to `func`, dense).  Any
+    exception is logged and the call goes to `func`, so a sparse failure
+    costs speed, never the output.  The block size is checked here
+    (ValueError), not at the first call.
     """
     blk = sla.check_block(blk)
 
+    def sparse(q, k, v, transformer_options):
+        if schedule is None:
+            return sla.sparse_attention(q, k, v, topk, blk)
+        return schedule.run(getattr(_state, "layer", None), q, k, v, transformer_options)
+
     def override(func, *args, **kwargs):
-        try:
-            if in_dit_scope() and _gate(args, kwargs):
-                q, k, v = args[0], args[1], args[2]
+        if in_dit_scope() and _gate(args, kwargs):
+            q, k, v = args[0], args[1], args[2]
+            try:
+                o = sparse(q, k, v, kwargs.get("transformer_options"))
+            except Exception as e:
+                log(f"[h3attn] sparse override fell back to dense: {e}")
+                o = None
+            if o is not None:
                 _, H, S, D = q.shape
-                if schedule is None:
-                    o = sla.sparse_attention(q, k, v, topk, blk)
-                else:
-                    o = schedule.run(getattr(_state, "layer", None), q, k, v, kwargs.get("transformer_options"))
-                if o is not None:
-                    return o.transpose(1, 2).reshape(1, S, H * D)
-        except Exception as e:  # never break a render on a sparse path
-            log(f"[h3attn] sparse override fell back to dense: {e}")
+                return o.transpose(1, 2).reshape(1, S, H * D)
         return func(*args, **kwargs)
 
     override.h3sla = schedule
     return override
+
+
+def _dit_blocks(model):
+    """The DiT blocks of a ModelPatcher (.model.diffusion_model.blocks), a diffusion model (.blocks)
+    or a sequence of blocks."""
+    for path in (("model", "diffusion_model", "blocks"), ("diffusion_model", "blocks"), ("blocks",)):
+        obj = model
+        for name in path:
+            obj = getattr(obj, name, None)
+            if obj is None:
+                break
+        if obj is not None:
+            return list(obj)
+    if isinstance(model, (list, tuple)) or hasattr(model, "__iter__"):
+        return list(model)
+    raise AttributeError(f"no DiT blocks found on {type(model).__name__}")
+
+
+def tag_layers(model, log=print):
+    """Record each DiT block's index as block.attn._h3sla_layer; returns the block count or None.
+
+    The scope patch reads the tag, so a per-layer schedule knows which layer
+    it runs (custom_nodes/h3_sla/__init__.py:296-305).  A model without
+    MiniMax-H3 blocks is logged and left untagged (None): every call then
+    gets the schedule's default keep.
+    """
+    try:
+        blocks = _dit_blocks(model)
+        for i, block in enumerate(blocks):
+            block.attn._h3sla_layer = i
+        return len(blocks)
+    except Exception as e:
+        log(f"[h3_sla] could not tag DiT layers ({e}); per-layer presets need MiniMax-H3 blocks")
+        return None
+
+
+def _attention_class(model):
+    """The class of the model's DiT-block attention, else comfy.ldm.minimax.model.Attention."""
+    try:
+        return type(_dit_blocks(model)[0].attn)
+    except Exception:
+        import comfy.ldm.minimax.model as mm  # ComfyUI is optional: imported only here
+        return mm.Attention
+
+
+def patch_model(model, topk: float = 0.35, blk: int = 64, enabled: bool = True, preset: str = "off",
+                layer_keep: str = "", attention_cls=None, log=print):
+    """The H3SLAPatch node's patch() on libh3attn (custom_nodes/h3_sla/__init__.py:328-346).
+
+    Returns a clone of the ComfyUI ModelPatcher `model` whose
+    transformer_options carry the block-sparse override, or `model` itself
+    when not enabled.  preset "off": one keep (`topk`) on every DiT layer.
+    Otherwise the blocks are tagged with their layer index, the per-layer
+    schedule is resolved (sla.resolve_schedule) and logged.  The scope patch
+    goes on `attention_cls` (by default the class of the blocks' attention
+    modules, comfy.ldm.minimax.model.Attention in ComfyUI) and the library is loaded here, so that a missing build fails now rather
+    than mid-render.  An unsupported `blk` or preset raises ValueError.
+    """
+    if not enabled:
+        return model
+    blk = sla.check_block(blk)
+    if attention_cls is None:
+        attention_cls = _attention_class(model)
+    install_scope_patch(attention_cls)
+    _lib.lib()
+    m = model.clone()
+    m.model_options = dict(m.model_options)
+    opts = dict(m.model_options.get("transformer_options", {}))
+    m.model_options["transformer_options"] = opts
+    mode = (preset or "off").lower()
+    if mode == "off":
+        opts["optimized_attention_override"] = make_sla_override(float(topk), blk, log=log)
+        log(f"[h3_sla] H3SLAPatch: topk={float(topk):.3f} (sparsity={100 * (1 - float(topk)):.0f}%) blk={blk}")
+        return m
+    n = tag_layers(m, log=log) or 50
+    name, keeps = sla.resolve_schedule(mode, float(topk), layer_keep, n)
+    sched = Schedule(name, keeps, blk, log=log)
+    opts["optimized_attention_override"] = make_sla_override(float(topk), blk, schedule=sched, log=log)
+    log(f"[h3_sla] H3SLAPatch: per-layer schedule blk={blk}\n" + sla.format_summary(sched.summary))
+    return m
 
 
 def get_schedule(transformer_options):
@@ -268,9 +408,13 @@ def install(attention_cls=None, prologue: Callable = ops.rms_rope_split_half_,
     if attention_cls is None:
         import comfy.ldm.minimax.model as mm  # ComfyUI is optional: imported only here
         attention_cls = mm.Attention
-    if getattr(attention_cls.forward, "_h3attn_patched", False):
+    fwd = attention_cls.forward
+    scoped = getattr(fwd, "_h3attn_scope", False)
+    inner = fwd._h3attn_orig if scoped else fwd
+    if getattr(inner, "_h3attn_patched", False):
         return False
-    attention_cls.forward = make_attention_forward(attention_cls.forward, prologue, attention, timer)
+    patched = make_attention_forward(inner, prologue, attention, timer)
+    attention_cls.forward = _scope_wrap(patched) if scoped else patched
     return True
 
 
@@ -279,9 +423,11 @@ def uninstall(attention_cls=None) -> bool:
         import comfy.ldm.minimax.model as mm
         attention_cls = mm.Attention
     fwd = attention_cls.forward
-    if not getattr(fwd, "_h3attn_patched", False):
+    scoped = getattr(fwd, "_h3attn_scope", False)
+    inner = fwd._h3attn_orig if scoped else fwd
+    if not getattr(inner, "_h3attn_patched", False):
         return False
-    attention_cls.forward = fwd._h3attn_orig
+    attention_cls.forward = _scope_wrap(inner._h3attn_orig) if scoped else inner._h3attn_orig
     return True
 
 

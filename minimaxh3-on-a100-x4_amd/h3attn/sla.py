@@ -130,6 +130,7 @@ def format_summary(sm: dict) -> str:
 # multiples of their 64-key stage.  The h3_sla node offers 16..256 in steps of
 # 16 (custom_nodes/h3_sla/__init__.py:315); the others are refused up front.
 SUPPORTED_BLOCKS = (64, 128, 192, 256)
+BLOCK_STEP = 64  # spacing of SUPPORTED_BLOCKS
 
 
 def check_block(blk) -> int:

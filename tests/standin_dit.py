@@ -9,6 +9,9 @@ plain torch (fp32 math), i.e. the "stock" math the patched forward must match.
 """
 from __future__ import annotations
 
+import copy
+import types
+
 import torch
 import torch.nn as nn
 
@@ -91,3 +94,49 @@ class Attention(nn.Module):
         out = optimized_attention(q, k, v, self.heads, mask=None, skip_reshape=True,
                                   transformer_options=transformer_options)
         return self.out_proj(out.squeeze(0))
+
+
+class DiTBlock(nn.Module):
+    """A DiT block reduced to what the hooks touch: its self-attention at `.attn`."""
+
+    def __init__(self, dim, heads, attention_cls=Attention, dtype=None, device=None):
+        super().__init__()
+        self.attn = attention_cls(dim, heads, dtype=dtype, device=device)
+
+    def forward(self, x, rope_freqs=None, transformer_options={}):
+        return x + self.attn(x, rope_freqs=rope_freqs, transformer_options=transformer_options)
+
+
+class MiniMaxH3Model(nn.Module):
+    """`depth` DiT blocks run in order (the diffusion model's block loop, without the MLPs)."""
+
+    def __init__(self, dim, heads, depth=50, attention_cls=Attention, dtype=None, device=None):
+        super().__init__()
+        self.blocks = nn.ModuleList(DiTBlock(dim, heads, attention_cls, dtype, device) for _ in range(depth))
+
+    def forward(self, x, rope_freqs=None, transformer_options={}):
+        for block in self.blocks:
+            x = block(x, rope_freqs=rope_freqs, transformer_options=transformer_options)
+        return x
+
+
+class ModelPatcher:
+    """The parts of ComfyUI's ModelPatcher a model-patching node uses: .model.diffusion_model,
+    .model_options (with "transformer_options") and clone(), which shares the weights."""
+
+    def __init__(self, diffusion_model, model_options=None):
+        self.model = types.SimpleNamespace(diffusion_model=diffusion_model)
+        self.model_options = {"transformer_options": {}} if model_options is None else model_options
+
+    def clone(self):
+        return ModelPatcher(self.model.diffusion_model, copy.deepcopy(self.model_options))
+
+    def __call__(self, x, rope_freqs, sigma=None, sample_sigmas=None):
+        """One sampling step: the diffusion model under this patcher's transformer_options, with the
+        step's sigma and the run's sigma schedule added as the sampler adds them."""
+        opts = dict(self.model_options.get("transformer_options", {}))
+        if sigma is not None:
+            opts["sigmas"] = torch.tensor([float(sigma)])
+        if sample_sigmas is not None:
+            opts["sample_sigmas"] = torch.tensor([float(s) for s in sample_sigmas])
+        return self.model.diffusion_model(x, rope_freqs=rope_freqs, transformer_options=opts)

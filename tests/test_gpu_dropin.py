@@ -119,10 +119,12 @@ def test_reference_harness_flow(gpu):
     assert rel < 5e-3 and torch.isfinite(o).all().item(), rel
 
 
-def test_installed_optimized_attention_keeps_sla_layers_sparse(gpu):
+def test_installed_optimized_attention_keeps_sla_layers_sparse(gpu, monkeypatch):
     """install_optimized_attention + make_sla_override(keep < 1): the DiT's attention
-    calls reach the sparse override, so the output differs from dense and equals the
-    sparse path's; with keep = 1 the HIP dense kernel runs."""
+    calls reach the sparse override, whose output on the layer's q/k/v matches the
+    masked oracle at that keep, and the module output equals the sparse path's; with
+    keep = 1 the HIP dense kernel runs."""
+    from test_gpu_hooks import _capture_sparse, _check_against_masked_oracle
     class A(standin_dit.Attention):
         pass
 
@@ -136,6 +138,7 @@ def test_installed_optimized_attention_keeps_sla_layers_sparse(gpu):
     sparse = hooks.make_sla_override(schedule=hooks.Schedule("custom", [0.5] * 50, blk=64))
     dense = hooks.make_sla_override(schedule=hooks.Schedule("custom", [1.0] * 50, blk=64))
     orig = standin_dit.optimized_attention
+    captured = _capture_sparse(monkeypatch, {0})
     with torch.no_grad():
         want_sparse = m(x, rope_freqs=rope, transformer_options={"optimized_attention_override": sparse}).float()
         want_dense = m(x, rope_freqs=rope, transformer_options={"optimized_attention_override": dense}).float()
@@ -146,6 +149,7 @@ def test_installed_optimized_attention_keeps_sla_layers_sparse(gpu):
             got_plain = m(x, rope_freqs=rope).float()
         finally:
             standin_dit.optimized_attention = orig
+    _check_against_masked_oracle(captured[0], 0.5)
     assert torch.equal(got_sparse, want_sparse)
     assert not torch.equal(got_sparse, got_dense)
     assert_close_absmax(got_dense.cpu().numpy(), want_dense.cpu().numpy(), what="dense via HIP")

@@ -9,8 +9,9 @@ import torch
 
 import h3attn
 import standin_dit
-from conftest import assert_close_absmax
-from h3attn import hooks
+import oracle
+from conftest import assert_close_absmax, from_dev_bf16
+from h3attn import hooks, sla
 
 pytestmark = pytest.mark.gpu
 
@@ -63,8 +64,38 @@ def test_patched_optimized_attention(gpu):
     assert_close_absmax(masked.float().cpu().numpy(), want.cpu().numpy(), what="masked fallback")
 
 
-def test_sparse_override_in_dit_scope(gpu):
-    """h3_sla-style override: keep < 1 runs the block-sparse kernel, keep = 1 runs dense."""
+def _capture_sparse(monkeypatch, layers):
+    """Wrap sla.sparse_attention to keep (q, k, v, keep, kwargs, output) of the given layers."""
+    real = sla.sparse_attention
+    got = {}
+
+    def spy(q, k, v, keep, blk, **kw):
+        o = real(q, k, v, keep, blk, **kw)
+        layer = hooks._state.layer
+        if layer in layers:
+            got[layer] = tuple(from_dev_bf16(t) for t in (q, k, v)) + (keep, blk, kw, from_dev_bf16(o))
+        return o
+
+    monkeypatch.setattr(sla, "sparse_attention", spy)
+    return got
+
+
+def _check_against_masked_oracle(captured, keep):
+    """The captured layer output equals the oracle's attention masked by the oracle's block map at
+    `keep` (top floor(keep * nk) key blocks by mean-pooled score, no forced diagonal)."""
+    q, k, v, used_keep, blk, kw, o = captured
+    assert used_keep == keep and not kw.get("force_diag", False)
+    nk = -(-q.shape[2] // blk)
+    bmap = oracle.block_map(q, k, blk, blk, keep=sla.keep_count(keep, nk), force_diag=False)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
+    got = oracle.bf16_to_f32(o).reshape(o.shape)
+    assert_close_absmax(got, ref, what=f"sparse layer at keep {keep}")
+    return got, bmap
+
+
+def test_sparse_override_in_dit_scope(gpu, monkeypatch):
+    """h3_sla-style override: keep < 1 runs the block-sparse kernel on the layer's q/k/v (checked
+    against the masked oracle), keep = 1 runs dense."""
     class A(standin_dit.Attention):
         pass
 
@@ -76,13 +107,58 @@ def test_sparse_override_in_dit_scope(gpu):
     rope = h3attn.rope_freqs(S, 128, device=gpu)
     dense_sched = hooks.Schedule("custom", [1.0] * 50, blk=64)
     sparse_sched = hooks.Schedule("custom", [0.5] * 50, blk=64)
+    captured = _capture_sparse(monkeypatch, {0})
     with torch.no_grad():
         stock = m(x, rope_freqs=rope).float()
         d = m(x, rope_freqs=rope, transformer_options={
             "optimized_attention_override": hooks.make_sla_override(schedule=dense_sched)}).float()
+        assert captured == {}
         logs = []
-        s = m(x, rope_freqs=rope, transformer_options={
+        m(x, rope_freqs=rope, transformer_options={
             "optimized_attention_override": hooks.make_sla_override(schedule=sparse_sched, log=logs.append)})
     assert torch.equal(d, stock)
-    assert logs == [] and torch.isfinite(s.float()).all()
-    assert not torch.equal(s.float(), stock)  # half the key blocks were skipped
+    assert logs == []
+    _check_against_masked_oracle(captured[0], 0.5)
+
+
+def test_patched_model_runs_scheduled_keeps_against_masked_oracle(gpu, monkeypatch):
+    """hooks.patch_model with the "balanced" preset on a 50-block stand-in DiT with the HIP forward
+    installed: layer 30 (SLA15) and layer 31 (SLA25) each match the masked oracle at their own
+    keep, and not at the other's (custom_nodes/h3_sla/__init__.py:44-49, 296-305, 328-346)."""
+    class A(standin_dit.Attention):
+        pass
+
+    torch.manual_seed(0)
+    dm = standin_dit.MiniMaxH3Model(512, 4, depth=50, attention_cls=A, dtype=torch.bfloat16, device=gpu)
+    with torch.no_grad():
+        for blk in dm.blocks:
+            a = blk.attn
+            a.qkv_proj.weight.normal_(0, 512 ** -0.5)
+            a.out_proj.weight.normal_(0, 0.1 * 512 ** -0.5)
+            a.q_norm.weight.copy_(1 + 0.05 * torch.randn(128, device=gpu))
+            a.k_norm.weight.copy_(1 + 0.05 * torch.randn(128, device=gpu))
+    mp = standin_dit.ModelPatcher(dm)
+    try:
+        assert hooks.install(A)
+        logs = []
+        pm = hooks.patch_model(mp, topk=0.35, blk=64, preset="balanced", log=logs.append)
+        keeps = hooks.get_schedule(pm.model_options["transformer_options"]).keeps
+        assert (keeps[30], keeps[31]) == (0.15, 0.25)
+        captured = _capture_sparse(monkeypatch, {30, 31})
+        S = 1000  # 16 key blocks: keep 0.15 -> 2 blocks, 0.25 -> 4
+        x = torch.randn(S, 512, device=gpu, dtype=torch.bfloat16)
+        rope = h3attn.rope_freqs(S, 128, device=gpu)
+        with torch.no_grad():
+            out = pm(x, rope)
+        torch.cuda.synchronize()
+    finally:
+        hooks.uninstall(A)
+    assert torch.isfinite(out.float()).all()
+    for layer, keep, other in ((30, 0.15, 0.25), (31, 0.25, 0.15)):
+        got, bmap = _check_against_masked_oracle(captured[layer], keep)
+        assert int(bmap[0, 0, 0].sum()) == sla.keep_count(keep, 16)
+        q, k, v = captured[layer][:3]
+        wrong = oracle.attn_fwd(q, k, v, block_map=oracle.block_map(q, k, 64, 64, keep=sla.keep_count(other, 16),
+                                                                     force_diag=False), blk_q=64, blk_k=64)
+        with pytest.raises(AssertionError):
+            assert_close_absmax(got, wrong, what="the other layer's keep")

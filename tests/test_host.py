@@ -151,6 +151,37 @@ def test_install_patch_matches_stock_forward_and_is_idempotent():
     assert torch.equal(got_norope, want_norope)
 
 
+@pytest.mark.parametrize("scope_first", [True, False])
+def test_install_and_scope_patch_compose_in_either_order(scope_first):
+    """The patched forward sits beneath the scope wrapper whichever is installed first, so the
+    override still sees the DiT scope and the layer tag; uninstall keeps the scope wrapper."""
+    class A(standin_dit.Attention):
+        pass
+
+    torch.manual_seed(2)
+    m = A(256, 2)
+    m._h3sla_layer = 7
+    seen = []
+
+    def attention(q, k, v, heads, **kw):
+        seen.append((hooks.in_dit_scope(), hooks._state.layer))
+        return _cpu_attention(q, k, v, heads, **kw)
+
+    if scope_first:
+        hooks.install_scope_patch(A)
+    assert hooks.install(A, prologue=standin_dit.rms_rope_split_half_, attention=attention)
+    hooks.install_scope_patch(A)
+    assert not hooks.install(A, prologue=standin_dit.rms_rope_split_half_, attention=attention)
+    x, rope = torch.randn(10, 256), h3attn.rope_freqs(10, 128)
+    with torch.no_grad():
+        m(x, rope_freqs=rope)
+        assert seen == [(True, 7)]
+        assert hooks.uninstall(A) and not hooks.uninstall(A)
+        assert getattr(A.forward, "_h3attn_scope", False)
+        m(x, rope_freqs=rope)  # stock forward again: the attention above is no longer called
+    assert seen == [(True, 7)]
+
+
 def test_override_gate_and_fallback():
     calls = []
 
@@ -279,6 +310,153 @@ class _FakeSyncEvent:
 
     def elapsed_time(self, other):
         return float(other.t - self.t)
+
+
+class _LostEvent(_FakeSyncEvent):
+    def synchronize(self):
+        raise RuntimeError("event lost")
+
+
+def test_schedule_timing_with_a_dense_last_layer(monkeypatch):
+    """Events are resolved at a step's last layer even when it runs dense, and at layer 0 of the
+    next step; a failure while resolving them is logged and never reaches the layer's output."""
+    monkeypatch.setattr(torch.cuda, "Event", lambda enable_timing=True: _FakeSyncEvent())
+    monkeypatch.setattr(sla, "sparse_attention", lambda q, k, v, keep, blk, **kw: q)
+    logs = []
+    sched = hooks.Schedule("custom", [0.5, 0.5, 1.0], blk=64, timing=True, log=logs.append)
+    q = torch.zeros(1, 1, 4, 128)
+    for _ in range(3):
+        for layer in range(3):
+            sched.run(layer, q, q, q)
+        assert sched._ev == []
+    assert sched.attn_n == [3, 3, 0]
+    # a step cut short after layer 0: its event is resolved by the next step's layer 0
+    sched.run(0, q, q, q)
+    assert len(sched._ev) == 1
+    sched.run(0, q, q, q)
+    assert sched.attn_n[0] == 4 and len(sched._ev) == 1
+    monkeypatch.setattr(torch.cuda, "Event", lambda enable_timing=True: _LostEvent())
+    sched._ev = []
+    assert sched.run(0, q, q, q) is q and sched.run(1, q, q, q) is q
+    assert sched.run(2, q, q, q) is None  # dense layer: resolves (and drops) the lost events
+    assert sched._ev == [] and any("timing events dropped" in s for s in logs)
+
+
+def _patcher(depth=50, dim=256, heads=2, seed=0):
+    class A(standin_dit.Attention):
+        pass
+
+    torch.manual_seed(seed)
+    return standin_dit.ModelPatcher(standin_dit.MiniMaxH3Model(dim, heads, depth, attention_cls=A)), A
+
+
+@pytest.mark.parametrize("preset,layer_keep", [("off", ""), ("quality", ""), ("balanced", ""), ("speed", ""),
+                                               ("custom", "25:31-42,46-49;20:43;100:0,17")])
+def test_patch_model_runs_each_layer_at_its_scheduled_keep(monkeypatch, preset, layer_keep):
+    """hooks.patch_model (H3SLAPatch.patch, custom_nodes/h3_sla/__init__.py:328-346) on a 50-block
+    stand-in DiT: one forward runs every layer at the keep resolve_schedule gives it (layers at
+    keep 1 run dense through the original attention), for every preset."""
+    used, dense = [], []
+
+    def fake_sparse(q, k, v, keep, blk, **kw):
+        used.append((hooks._state.layer, keep, blk))
+        return q.clone()
+
+    monkeypatch.setattr(sla, "sparse_attention", fake_sparse)
+    mp, A = _patcher()
+    logs = []
+    pm = hooks.patch_model(mp, topk=0.35, blk=64, preset=preset, layer_keep=layer_keep, log=logs.append)
+    assert pm is not mp and mp.model_options == {"transformer_options": {}}
+    assert hooks.in_dit_scope() is False and getattr(A.forward, "_h3attn_scope", False)
+    x = torch.randn(12, 256)
+    rope = h3attn.rope_freqs(12, 128)
+    impl = standin_dit._attention_impl
+    monkeypatch.setattr(standin_dit, "_attention_impl",
+                        lambda *a, **kw: dense.append(hooks._state.layer) or impl(*a, **kw))
+    with torch.no_grad():
+        pm(x, rope)
+    name, keeps = sla.resolve_schedule(preset, 0.35, layer_keep, 50)
+    sched = hooks.get_schedule(pm.model_options["transformer_options"])
+    if preset == "off":
+        assert sched is None  # one keep everywhere: no schedule, no layer tags
+        assert used == [(None, 0.35, 64)] * 50 and dense == []
+        assert any("topk=0.350" in s for s in logs)
+        return
+    assert sched.keeps == keeps and sched.name == name and sched.blk == 64
+    assert [layer for layer, _, _ in used] == [i for i, kv in enumerate(keeps) if kv < 1]
+    assert [kv for _, kv, _ in used] == [kv for kv in keeps if kv < 1]
+    assert dense == [i for i, kv in enumerate(keeps) if kv >= 1]
+    assert [b.attn._h3sla_layer for b in mp.model.diffusion_model.blocks] == list(range(50))
+    assert sla.format_summary(sched.summary) in "\n".join(logs)
+    if preset == "balanced":  # the 14 layers at 0.25 that an untagged model would run at 0.15
+        assert [i for i, kv in enumerate(keeps) if kv == 0.25] == list(range(31, 43)) + [48, 49]
+
+
+def test_patch_model_disabled_and_bad_arguments(monkeypatch):
+    mp, A = _patcher(depth=3)
+    assert hooks.patch_model(mp, enabled=False) is mp
+    with pytest.raises(ValueError, match="preset"):
+        hooks.patch_model(mp, preset="fastest")
+    with pytest.raises(ValueError, match="block size"):
+        hooks.patch_model(mp, blk=48)
+    assert mp.model_options == {"transformer_options": {}}
+
+
+def test_schedule_reports_each_generation_at_its_first_sigma(monkeypatch):
+    """Layer 0 at a run's first sigma logs the schedule summary (rank 0) and counts a generation
+    (custom_nodes/h3_sla/__init__.py:155-170); later steps of the same run do not."""
+    monkeypatch.setattr(sla, "sparse_attention", lambda q, k, v, keep, blk, **kw: q.clone())
+    mp, _ = _patcher(depth=4)
+    logs = []
+    pm = hooks.patch_model(mp, topk=0.15, preset="custom", layer_keep="25:1-2", log=logs.append)
+    sched = hooks.get_schedule(pm.model_options["transformer_options"])
+    head = "[h3_sla] SLA preset: custom"
+    assert sum(s.count(head) for s in logs) == 1  # at patch time
+    logs.clear()
+    x, rope = torch.randn(12, 256), h3attn.rope_freqs(12, 128)
+    sigmas = [14.6, 7.0, 2.0, 0.0]
+    with torch.no_grad():
+        for _ in range(2):
+            for s in sigmas[:-1]:
+                pm(x, rope, sigma=s, sample_sigmas=sigmas)
+        assert sched.generation == 2 and sum(s.count(head) for s in logs) == 2
+        monkeypatch.setenv("RANK", "1")  # other ranks count but do not log
+        pm(x, rope, sigma=sigmas[0], sample_sigmas=sigmas)
+        monkeypatch.delenv("RANK")
+        assert sched.generation == 3 and sum(s.count(head) for s in logs) == 2
+        pm(x, rope)  # no sigmas: every call counts as a first step
+    assert sched.generation == 4
+
+
+def test_tag_layers():
+    mp, _ = _patcher(depth=5)
+    blocks = mp.model.diffusion_model.blocks
+    assert hooks.tag_layers(mp) == 5
+    assert [b.attn._h3sla_layer for b in blocks] == [0, 1, 2, 3, 4]
+    assert hooks.tag_layers(mp.model.diffusion_model) == 5
+    assert hooks.tag_layers(list(blocks)[2:]) == 3 and blocks[2].attn._h3sla_layer == 0
+    logs = []
+    assert hooks.tag_layers(object(), log=logs.append) is None
+    assert any("could not tag" in s for s in logs)
+
+
+def test_comfy_node_interface(monkeypatch):
+    """node.H3SLAPatch has the h3_sla node's inputs and output (custom_nodes/h3_sla/__init__.py:308-346)."""
+    from h3attn import node
+    monkeypatch.setattr(sla, "sparse_attention", lambda q, k, v, keep, blk, **kw: q.clone())
+    cls = node.NODE_CLASS_MAPPINGS["H3SLAPatch"]
+    spec = cls.INPUT_TYPES()
+    assert list(spec["required"]) == ["model", "topk", "blk", "enabled"]
+    assert list(spec["optional"]) == ["preset", "layer_keep"]
+    assert spec["required"]["topk"][1]["default"] == 0.35 and spec["required"]["blk"][1]["default"] == 64
+    assert spec["optional"]["preset"][0] == sla.PRESET_CHOICES
+    assert cls.RETURN_TYPES == ("MODEL",) and cls.FUNCTION == "patch"
+    lo, hi, step = (spec["required"]["blk"][1][k] for k in ("min", "max", "step"))
+    assert set(range(lo, hi + 1, step)) == set(sla.SUPPORTED_BLOCKS)
+    mp, _ = _patcher(depth=50)
+    (pm,) = cls().patch(mp, 0.35, 64, True, "speed", "")
+    assert hooks.get_schedule(pm.model_options["transformer_options"]).keeps == sla.resolve_schedule("speed")[1]
+    assert cls().patch(mp, 0.35, 64, False)[0] is mp
 
 
 def test_installed_optimized_attention_still_calls_the_override():
