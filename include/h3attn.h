@@ -9,7 +9,14 @@
  *   - Device pointers and every outer stride must be 16-byte aligned
  *     (strides multiple of 8 elements) so rows move as 128-bit accesses.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
- *     and never synchronised.  No global mutable state: thread-safe.
+ *     and never synchronised.  Thread-safe: the only state shared between
+ *     calls is (a) per-device caches of the CU count, occupancy and the
+ *     scratch address, each set once and read atomically; (b) the static
+ *     scratch array of h3a_attn_fwd_noalloc, one per GPU and shared by every
+ *     call of that entry point on it, so such calls that overlap on one GPU
+ *     race (see there); (c) in the profile build only, the phase-profile
+ *     slots, which every launch of a ping-pong kernel overwrites
+ *     (h3a_prof_read).
  *   - Return 0 (H3A_OK) on success, a non-zero H3A_ERR_* code otherwise;
  *     h3a_last_error() then holds a thread-local message.  Argument checks run
  *     before any HIP call, so bad arguments never reach the GPU.

@@ -47,227 +47,29 @@
 #include "h3a_internal.h"
 #include "h3a_lut.h"
 #include "h3a_queue.h"
+#include "h3a_stale.h"
 
 namespace h3a {
 
-#ifndef H3A_LAZY_RESCALE
-#define H3A_LAZY_RESCALE 1
-#endif
-#ifndef H3A_XCD_REMAP
-#define H3A_XCD_REMAP 1
-#endif
-// Dense problems of several rounds of tiles on a persistent grid fed by
-// per-XCD work queues (1), or one tile per workgroup (0).
-#ifndef H3A_DENSE_QUEUES
-#define H3A_DENSE_QUEUES 1
-#endif
-// The same for the block-sparse ping-pong kernels (pairs of query blocks).
-#ifndef H3A_SPARSE_QUEUES
-#define H3A_SPARSE_QUEUES 1
-#endif
-// Scheduling-group hints interleaving MFMA / LDS reads / VALU in the stage body.
-#ifndef H3A_SCHED_HINTS
-#define H3A_SCHED_HINTS 0
-#endif
-// Waves (32 query rows each) per dense workgroup.
-#ifndef H3A_DENSE_WAVES
-#define H3A_DENSE_WAVES 8
-#endif
-// Dense path: ping-pong wave groups (attn_fwd_pingpong_kernel, 8 waves)
-// instead of attn_fwd_kernel.
-#ifndef H3A_DENSE_PINGPONG
-#define H3A_DENSE_PINGPONG 1
-#endif
-// Keep each softmax cluster's results inside its own slot (see pin()).
-#ifndef H3A_PP_PIN_SOFTMAX
-#define H3A_PP_PIN_SOFTMAX 1
-#endif
-// LDS stage layout of the dense kernels (0: SwzLayout, 1: PadLayout).
-#ifndef H3A_DENSE_LAYOUT
-#define H3A_DENSE_LAYOUT 0
-#endif
-// Keys per stage of the dense ping-pong kernel (64 or 128).
-#ifndef H3A_DENSE_BN
-#define H3A_DENSE_BN 64
-#endif
-// Ping-pong matrix cluster: PV of the current stage before the next stage's
-// scores (P's registers die before the new scores are written).
-#ifndef H3A_PP_PV_FIRST
-#define H3A_PP_PV_FIRST 0
-#endif
-// Ping-pong softmax against a stale reference max: no per-stage row max, only
-// a check of the stage's p sum (1), or the per-stage max with lazy refresh (0).
-#ifndef H3A_PP_STALE_MAX
-#define H3A_PP_STALE_MAX 1
-#endif
-// Block-sparse attention with 128-row query blocks: ping-pong kernel over
-// pairs of query blocks with register-staged K/V (1), or the single-group
-// attn_fwd_kernel (0).
-#ifndef H3A_SPARSE_PINGPONG
-#define H3A_SPARSE_PINGPONG 1
-#endif
-// Sparse ping-pong with register staging (H3A_SPARSE_PP_DMA=0): a group
-// issues its K/V loads right after its matrix cluster (1), at the top of its
-// softmax slot (0), the K loads after the matrix cluster and the V loads at
-// the top of the softmax slot (2), or interleaved with the last 8 MFMAs of
-// the matrix cluster (3).
-#ifndef H3A_SPARSE_PP_EARLY
-#define H3A_SPARSE_PP_EARLY 1
-#endif
-// Block-sparse attn_fwd_kernel: K/V staged through VGPRs (1) or by LDS DMA (0).
-#ifndef H3A_SPARSE_REGS
-#define H3A_SPARSE_REGS 1
-#endif
-// Sparse ping-pong (pairs of query blocks): each group fetches its own K/V
-// stages by LDS DMA into swizzled rows (1), or stages them through VGPRs into
-// padded rows (0).  With DMA, KTOP of a wave's 4 K loads and VTOP of its 4 V
-// loads per stage go at the top of its softmax slot, the rest right after its
-// matrix cluster.
-#ifndef H3A_SPARSE_PP_DMA
-#define H3A_SPARSE_PP_DMA 1
-#endif
-#ifndef H3A_SPARSE_PP_KTOP
-#define H3A_SPARSE_PP_KTOP 4
-#endif
-#ifndef H3A_SPARSE_PP_VTOP
-#define H3A_SPARSE_PP_VTOP 0
-#endif
-// 64-row query blocks: 4-wave key-split workgroups (1) or 2-wave workgroups (0).
-#ifndef H3A_SPARSE64_KEYSPLIT
-#define H3A_SPARSE64_KEYSPLIT 1
-#endif
-// 64-row query blocks: the ping-pong kernel over pairs of blocks, each group
-// key-split over its block (1), or the single-group kernel above (0).
-#ifndef H3A_SPARSE64_PINGPONG
-#define H3A_SPARSE64_PINGPONG 1
-#endif
-// LDS operand reads issued ahead of the first MFMA of a ping-pong matrix
-// cluster (0: leave the order to the scheduler); block-sparse kernels and
-// the dense kernel separately (same-box sweep: dense 4 +0.4 % over 6, 8
-// -0.4 %; sparse 6, with 4 -0.3 % at 128x128 and -0.9 % at 64x64).
-#ifndef H3A_PP_READ_AHEAD
-#define H3A_PP_READ_AHEAD 6
-#endif
-#ifndef H3A_PP_DENSE_READ_AHEAD
-#define H3A_PP_DENSE_READ_AHEAD 4
-#endif
-// Dense ping-pong fetch split: instructions of each K and V stage (4 per wave
-// column: waves w and w+4 of the two groups) that the group-A wave issues
-// (H3A_PP_A_KINST of K, H3A_PP_A_VINST of V); the group-B wave issues the
-// rest, at the top of its softmax cluster.  -1: every wave issues 2 + 2 over
-// an 8-wave layout.  Default: group B fetches K, group A fetches V at the top
-// of its own softmax cluster (H3A_PP_A_SOFT), so each softmax slot carries
-// half of the fetch.
-#ifndef H3A_PP_A_KINST
-#define H3A_PP_A_KINST 0
-#endif
-#ifndef H3A_PP_A_VINST
-#define H3A_PP_A_VINST 4
-#endif
-// 1: group A issues its share of the fetch after its matrix cluster (while
-// the last MFMAs drain) instead of before it.
-#ifndef H3A_PP_A_LATE
-#define H3A_PP_A_LATE 0
-#endif
-// 1: group A issues its share of the fetch at the top of its softmax slot
-// (after the mid-stage barrier, while group B's MFMAs run) instead.
-#ifndef H3A_PP_A_SOFT
-#define H3A_PP_A_SOFT 1
-#endif
-// LDS DMA spread over the ping-pong matrix clusters, one instruction after
-// every few MFMAs, instead of issued in bursts (whose instructions queue for
-// the CU's load path and stall the issuing wave): dense, group A fetches all
-// of K(j+2) and V(j+1) during its MFMA(j); block-sparse, each group fetches
-// its own during its MFMA(j).
-#ifndef H3A_PP_DMA_IN_CLUSTER
-#define H3A_PP_DMA_IN_CLUSTER 0
-#endif
-#ifndef H3A_SPARSE_PP_IN_CLUSTER
-#define H3A_SPARSE_PP_IN_CLUSTER 1
-#endif
-// The same for the key-split kernel (64-row query blocks).
-#ifndef H3A_SPARSE64_PP_IN_CLUSTER
-#define H3A_SPARSE64_PP_IN_CLUSTER 1
-#endif
-// Fetch spread over a cluster: all of it among the PV MFMAs, one instruction
-// every NP / NI MFMAs (1), or the K instructions among the score MFMAs and the
-// V ones among the PV MFMAs (0), where the score operand reads issued ahead
-// pull the K instructions to the cluster's start.  Same-box A/B of (1): 64-row
-// pairs +2.2 % over (0), 128-row pairs +0.6 % over the fetch at the slot tops
-// (where (0) lost 2 %); dense -1.2 % against its own placement.
-#ifndef H3A_PP_DMA_PV_ONLY
-#define H3A_PP_DMA_PV_ONLY 1
-#endif
-// Ping-pong epilogue: O stored through a wave-private LDS tile, 4 whole rows
-// per store instruction (1), or straight from the MFMA layout, 16 bytes into
-// each of 32 rows per instruction (0).
-#ifndef H3A_PP_STORE_LDS
-#define H3A_PP_STORE_LDS 1
-#endif
-// Wave priority raised (s_setprio 1) during the ping-pong matrix cluster (1),
-// during the softmax cluster (2), or never (0); block-sparse kernels and the
-// dense kernel separately (same-box sweep: dense 0 +0.2 % over 1; sparse 1,
-// with 0 -2.8 % at 128x128 and -3 % at 64x64).
-#ifndef H3A_PP_PRIO
-#define H3A_PP_PRIO 1
-#endif
-#ifndef H3A_PP_DENSE_PRIO
-#define H3A_PP_DENSE_PRIO 0
-#endif
-// Workgroup barrier between the two clusters of a ping-pong stage (1), or
-// only the one at the end of the stage (0), which the LDS buffers need.  The
-// end barrier alone keeps the groups one cluster apart once each softmax slot
-// carries half of the fetch; with group B fetching everything the mid barrier
-// paid for itself.
-#ifndef H3A_PP_MID_BARRIER
-#define H3A_PP_MID_BARRIER 0
-#endif
-// LDS operand reads issued after each MFMA of a ping-pong matrix cluster.
-#ifndef H3A_PP_READS_PER_MFMA
-#define H3A_PP_READS_PER_MFMA 2
-#endif
-// Ping-pong matrix cluster with the score and PV MFMAs alternating
-// (qk_pv_interleaved) instead of all score MFMAs first.
-#ifndef H3A_PP_INTERLEAVE
-#define H3A_PP_INTERLEAVE 0
-#endif
-// Row sum from the bf16-rounded P (v_dot2, 16 ops) instead of the unrounded
-// p (32 adds).  Off by default: the reference sums unrounded p.
-#ifndef H3A_ROWSUM_BF16
-#define H3A_ROWSUM_BF16 0
-#endif
-
-// Phase profile build (libh3attn_prof.so): the dense ping-pong kernel stamps
-// the shader clock at its cluster boundaries (see PhaseClock).
+// Phase profile build (libh3attn_prof.so): the ping-pong kernel stamps the
+// shader clock at its cluster boundaries (see PhaseClock).
 #ifndef H3A_PROFILE
 #define H3A_PROFILE 0
-#endif
-// Tuning builds only: every workgroup records its start and end
-// (s_memrealtime) and its XCC / hardware ids in g_timeline, read back with
-// h3a_timeline_read (exported only by such builds).
-#ifndef H3A_TIMELINE
-#define H3A_TIMELINE 0
 #endif
 
 constexpr int kD = 128;
 constexpr int kBN = 64;               // keys per pipeline stage
 constexpr float kRescaleSlack = 8.f;  // log2 headroom before the running max is refreshed
-// Largest stage p sum (per lane: 32 keys of one query row) accepted without a
-// refresh of the stale reference max.  Every p of a stage is then <= 2^16, so
-// a row's unnormalised O is bounded by 2 * 2^16 * ceil(Skv/64) * max|v|: it
-// stays finite for max|v| < 2^128 / (2^17 * ceil(Skv/64)), about 3.9e30 at
-// Skv = 42120 (a max-subtracted softmax with p <= 1 allows up to ~8e33 there).
-constexpr float kStaleSumLimit = 0x1p16f;
 
 __device__ __forceinline__ int stage_key0(const AttnArgs &a, int t, int kb) {
   return lut_stage_key0(t, kb, a.nkb, a.blk_k, a.sub, a.Skv);
 }
 
 // ---------------------------------------------------------------------------
-// LDS layouts of a 64-key K or V stage.  A layout fixes the row pitch, which
-// 16-byte global chunk each 16-byte LDS slot holds, and how the MFMA operand
-// reads address the stage.  Both are bank-conflict free for the reads below
-// (SQ_LDS_BANK_CONFLICT = 0 measured for each).
+// LDS layout of a 64-key K or V stage: the row pitch, which 16-byte global
+// chunk each 16-byte LDS slot holds, and how the MFMA operand reads address
+// the stage.  Bank-conflict free for the reads below (SQ_LDS_BANK_CONFLICT = 0
+// measured).  The kernels take the layout as a template parameter L.
 //
 // SwzLayout: 256-byte rows; chunk c of row r sits in slot c ^ swz(r).
 //   K: swz(r) = r & 15.  A 128-bit read of one chunk by 16 consecutive rows
@@ -275,9 +77,6 @@ __device__ __forceinline__ int stage_key0(const AttnArgs &a, int t, int kb) {
 //   V: swz(r) = 4 * (r & 3).  A transpose read by 32 lanes covers 4 rows x
 //      4 chunks, which land on 16 distinct bank groups: all 64 banks once.
 //   Read offsets are base ^ const, held per lane.
-// PadLayout: K rows of 272 bytes (17 slots), V rows of 320 bytes (20 slots),
-//   chunk c in slot c; the extra slots are padding that shifts consecutive
-//   rows across the banks.  Read offsets are base + immediate.
 struct SwzLayout {
   static constexpr int kKRow = 256, kVRow = 256;  // bytes
   static constexpr int kKSlots = 16, kVSlots = 16;
@@ -298,21 +97,6 @@ struct SwzLayout {
     return row * kVRow + 64 * i + 16 * c + 8 * (lane & 1);
   }
   __device__ __forceinline__ static int v_off(int vb, int dt) { return vb ^ (64 * dt); }
-};
-
-struct PadLayout {
-  static constexpr int kKRow = 272, kVRow = 320;  // bytes
-  static constexpr int kKSlots = 17, kVSlots = 20;
-  // Padding slots load a duplicate of an in-row chunk (never read back).
-  __device__ __forceinline__ static int k_chunk(int, int slot) { return slot & 15; }
-  __device__ __forceinline__ static int v_chunk(int, int slot) { return slot & 15; }
-  __device__ __forceinline__ static int k_base(int l32, int g) { return l32 * kKRow + 16 * g; }
-  __device__ __forceinline__ static int k_off(int kb, int ks) { return kb + 32 * ks; }
-  __device__ __forceinline__ static int v_base(int lane) {
-    const int row = 4 * (lane >> 5) + ((lane & 15) >> 2);
-    return row * kVRow + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
-  }
-  __device__ __forceinline__ static int v_off(int vb, int dt) { return vb + 64 * dt; }
 };
 
 template <class L, int ROWS = kBN>
@@ -486,42 +270,6 @@ struct StageCursor {
   }
 };
 
-// Staging through VGPRs into PadLayout: 128-bit buffer loads when the stage
-// starts, ds_write_b128 when it ends.  Thread t of the stream moves chunks
-// idx = t + i*NT (row idx/16, chunk idx%16), so its global offsets and LDS
-// addresses are one base plus compile-time steps.  The block-sparse kernels
-// use it: their key blocks arrive in LUT order, and with LDS DMA instead the
-// same kernel measured a lower L2 hit rate (32 % vs 62 %) and ran 6 % slower.
-template <int NW, bool kIsV>
-struct TileRegs {
-  static constexpr int NT = NW * 64;
-  static constexpr int kInst = (kBN * kD / 8) / NT;  // 16-byte chunks per thread
-  static_assert(kInst * NT == kBN * kD / 8, "stage must split evenly");
-  static constexpr int kRow = kIsV ? PadLayout::kVRow : PadLayout::kKRow;
-  static constexpr bool kAsync = false;
-  u32x4 r[kInst];
-  uint32_t goff;  // global byte offset of chunk 0 (row t/16, chunk t%16)
-  int loff;       // LDS byte offset of chunk 0
-  uint32_t gstep; // global bytes between consecutive chunks of this thread (NT/16 rows)
-
-  __device__ __forceinline__ void init(int64_t ss, int tid) {
-    goff = (uint32_t)(((int64_t)(tid >> 4) * ss + (tid & 15) * 8) * 2);
-    gstep = (uint32_t)((NT / 16) * ss * 2);
-    loff = (tid >> 4) * kRow + (tid & 15) * 16;
-  }
-  __device__ __forceinline__ void start(const uint16_t *base, int64_t ss, int key0, int Skv, uint16_t *) {
-    const int rows = Skv - key0 >= kBN ? kBN : (Skv > key0 ? Skv - key0 : 0);
-    const __amdgpu_buffer_rsrc_t res = stage_rsrc(stage_ptr(base, key0, ss), ss, rows);
-#pragma unroll
-    for (int i = 0; i < kInst; ++i) r[i] = buffer_load_b128(res, goff + i * gstep);
-  }
-  __device__ __forceinline__ void finish(uint16_t *tile) const {
-    char *t = reinterpret_cast<char *>(tile) + loff;
-#pragma unroll
-    for (int i = 0; i < kInst; ++i) *(u32x4 *)(t + i * (NT / 16) * kRow) = r[i];
-  }
-};
-
 // A stage's scores live in NSUB accumulators of 32 keys: s[u] holds keys
 // 32u..32u+31 of the stage.  In the S^T accumulator layout lane l owns query
 // l%32; register r of s[u] holds key 32u + 8*(r/4) + 4*(l/32) + r%4.
@@ -591,32 +339,6 @@ __device__ __forceinline__ void pv_tile(const uint16_t *vbuf, const u32x4 (&pf)[
   }
 }
 
-// S^T(j+1) = K(j+1) Q^T and O^T += V^T(j) P^T(j) for two 32-key score
-// sub-tiles, with the two products' MFMAs alternating: score MFMA i (k-step
-// i/2, sub-tile i%2) then PV MFMA i (key step i/4, dim tile i%4).  A score
-// accumulator is then reused every 4th MFMA and a PV one every 8th, instead
-// of every 2nd (score_tile) and every 4th (pv_tile).
-template <class L>
-__device__ __forceinline__ void qk_pv_interleaved(const uint16_t *kbuf, const uint16_t *vbuf,
-                                                  const u32x4 (&qf)[8], int k_rd, int v_rd,
-                                                  f32x16 (&s)[2], const u32x4 (&pf)[4], f32x16 (&o)[4]) {
-  s[0] = f32x16{0.f};
-  s[1] = f32x16{0.f};
-  const char *kb = reinterpret_cast<const char *>(kbuf);
-  const char *vb = reinterpret_cast<const char *>(vbuf);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int ks = i >> 1, u = i & 1;
-    const u32x4 a = *(const u32x4 *)(kb + L::k_off(k_rd, ks) + 32 * u * L::kKRow);
-    s[u] = mfma_32x32x16(a, qf[ks], s[u]);
-    const int kv = i >> 2, dt = i & 3;
-    const char *p = vb + L::v_off(v_rd, dt) + 16 * kv * L::kVRow;
-    const u32x2 lo = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p));
-    const u32x2 hi = lds_read_tr16_b64(reinterpret_cast<const uint16_t *>(p + 8 * L::kVRow));
-    o[dt] = mfma_32x32x16(u32x4{lo.x, lo.y, hi.x, hi.y}, pf[kv], o[dt]);
-  }
-}
-
 // Max of N values as a tree of v_max3 (depth log3 N), not a dependent chain:
 // the softmax cluster is latency-bound.
 template <int N>
@@ -682,277 +404,12 @@ __device__ __forceinline__ void mask_tail(f32x16 (&s)[NSUB], int key0, int Skv, 
   }
 }
 
-// kRegs: stage K/V through VGPRs into PadLayout (TileRegs) instead of LDS DMA.
-// kKeySplit: a 4-wave workgroup on one 64-row query block.  Wave w takes the
-// 32 query rows of slice w & 1 against key half w >> 1 (keys 32*(w>>1) ..
-// +31) of every 64-key stage, with its own running max, row sum and O; at
-// the end the key-half-1 wave hands (O, m, l) to its partner through LDS and
-// the partner merges them, O = 2^(m1-M) O1 + 2^(m2-M) O2 over the same for
-// l, as the split-tail combine does.  Compared with a 2-wave workgroup on
-// the same block, the K/V stage in LDS feeds twice the waves: 8 per CU
-// instead of 4 (LDS holds two workgroups' double-buffered stages either way).
-template <int NW, class L, bool kRegs, bool kSparse, bool kKeySplit = false>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-attn_fwd_kernel(AttnArgs a) {
-  static_assert(!kRegs || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
-  static_assert(!kKeySplit || NW == 4, "key-split workgroups are 2 query slices x 2 key halves");
-  constexpr int BM = kKeySplit ? 64 : NW * 32;
-  constexpr int NS = kKeySplit ? 1 : 2;  // 32-key score sub-tiles per wave and stage
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][StageBytes<L>::kK / 2];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][StageBytes<L>::kV / 2];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 5, l32 = lane & 31;
-
-#if H3A_XCD_REMAP
-  const int w = xcd_remap(blockIdx.x, a.total);
-#else
-  const int w = blockIdx.x;
-#endif
-  const int qt = w % a.nqt, bh = w / a.nqt;
-  const int h = bh % a.H, b = bh / a.H;
-
-  const uint16_t *Qb = a.q + b * a.qsb + h * a.qsh;
-  const uint16_t *Kb = a.k + b * a.ksb + h * a.ksh;
-  const uint16_t *Vb = a.v + b * a.vsb + h * a.vsh;
-  uint16_t *Ob = a.o + b * a.osb + h * a.osh;
-
-  int niter;
-  const int32_t *lut_row = nullptr;
-  if constexpr (kSparse) {
-    // A LUT row serves a.qmul consecutive query sub-blocks (blk_q = 192:
-    // three 64-row sub-blocks; blk_q = 256 with 128-row sub-blocks: two).
-    const int64_t row = (int64_t)bh * a.nqb + qt / a.qmul;
-    const int cnt = a.counts[row];
-    niter = (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
-    lut_row = a.lut + row * a.lut_stride;
-  } else {
-    niter = (a.Skv + kBN - 1) / kBN;
-  }
-  // First key of stage j, from its LUT entry kb (block-sparse; a key block
-  // of a.sub = 1..4 stages).  Prefetches past the last stage and LUT entries
-  // outside the key range map to Skv: such a stage loads nothing (zeros).
-  // Both are branch-free, so that the scalar work can be scheduled among
-  // the stage's MFMA and VALU instructions: the entry is loaded at a clamped
-  // index (niter >= 1 here) and discarded past the row's last stage.
-  auto lut_entry = [&](int j) __attribute__((always_inline)) -> int {
-    if constexpr (kSparse) {
-      return lut_row[block_of_stage(j < niter ? j : niter - 1, a.sub)];
-    } else {
-      return 0;
-    }
-  };
-  auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
-    if constexpr (kSparse) {
-      return j < niter ? stage_key0(a, j, kb) : a.Skv;
-    } else {
-      return j < niter ? j * kBN : a.Skv;
-    }
-  };
-  auto key_base = [&](int j) __attribute__((always_inline)) -> int { return key_of_entry(j, lut_entry(j)); };
-
-  const int rq = kKeySplit ? (wave & 1) : wave;  // 32-row query slice
-  const int kh = kKeySplit ? (wave >> 1) : 0;    // key half of each stage
-  const int qrow = qt * BM + rq * 32 + l32;
-  if (niter == 0) {
-    // No key block to attend to (block-sparse row with an empty LUT): O = 0.
-    // Leaving before any load also keeps every path into the stage loop free
-    // of outstanding loads, so the loop needs no waits on the Q fragments.
-    if (qrow < a.Sq && kh == 0) {
-      uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
-#pragma unroll
-      for (int c = 0; c < 16; ++c) *(u32x2 *)(p + 8 * c) = u32x2{0, 0};
-    }
-    return;
-  }
-  u32x4 qf[8];
-  if (qrow < a.Sq) {
-    const uint16_t *p = Qb + (int64_t)qrow * a.qss + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const u32x4 *)(p + ks * 16);
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = u32x4{0, 0, 0, 0};
-  }
-
-  f32x16 o[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{0.f};
-  float m = kNegInf;  // running row max, in scale*log2(e) units
-  float lsum = 0.f;   // this lane's share of the running row sum
-  // Key half kh starts 32 rows into the stage: an offset that neither
-  // layout's per-step offsets (XOR or add below 256 bytes) interact with.
-  const int k_rd = L::k_base(l32, g) + kh * 32 * L::kKRow;
-  const int v_rd = L::v_base(lane) + kh * 32 * L::kVRow;
-
-  // Software pipeline: K runs one stage ahead of V.  Entering stage j, LDS
-  // holds V(j) in vbuf[j&1] and K(j+1) in kbuf[(j+1)&1], and the registers
-  // hold the masked scores S(j).  Stage j starts fetching K(j+2) and V(j+1)
-  // for the buffers stage j-1 finished with, computes S(j+1) = K(j+1) Q^T
-  // while the softmax of S(j) runs (independent work the scheduler
-  // interleaves), then O += V(j) P(j); the fetch lands by the stage's barrier.
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  using KStager = std::conditional_t<kRegs, TileRegs<NW, false>, TileDma<NW, L, false>>;
-  using VStager = std::conditional_t<kRegs, TileRegs<NW, true>, TileDma<NW, L, true>>;
-  KStager kst;
-  VStager vst;
-  if constexpr (kRegs) {
-    kst.init(a.kss, tid);
-    vst.init(a.vss, tid);
-  } else {
-    kst.init(a.kss, wave_u, lane);
-    vst.init(a.vss, wave_u, lane);
-  }
-  auto land = [&]() __attribute__((always_inline)) {  // this wave's stage fetches are in LDS
-    if constexpr (KStager::kAsync) wait_vmem_all();
-  };
-  // Entering stage j: the first keys of stages j and j+1, and the LUT entry
-  // of stage j+2.  Stage j loads the entry of stage j+3 and uses it only in
-  // the next stage: with block-sparse LUTs that is a scalar load, whose wait
-  // is then the closing barrier's (which waits for the LDS writes anyway)
-  // rather than a wait for all LDS traffic at the top of the stage.
-  int kw0 = key_base(0), kw1 = key_base(1), e2 = lut_entry(2);
-  f32x16 s[NS];
-  kst.start(Kb, a.kss, kw0, a.Skv, kbuf[0]);
-  vst.start(Vb, a.vss, kw0, a.Skv, vbuf[0]);
-  kst.finish(kbuf[0]);
-  vst.finish(vbuf[0]);
-  land();
-  __syncthreads();
-  kst.start(Kb, a.kss, kw1, a.Skv, kbuf[1]);
-  score_tile<L, NS>(kbuf[0], qf, k_rd, s);
-  kst.finish(kbuf[1]);
-  land();
-  __syncthreads();
-
-  auto stage = [&](auto phase, int j) __attribute__((always_inline)) {
-    constexpr int P = decltype(phase)::value;  // j & 1
-    const int e3 = lut_entry(j + 3);
-    const int kw2 = key_of_entry(j + 2, e2);
-    kst.start(Kb, a.kss, kw2, a.Skv, kbuf[P]);
-    vst.start(Vb, a.vss, kw1, a.Skv, vbuf[P ^ 1]);
-
-    // The two rare branches (tail mask, rescale) come first, so everything
-    // after them is one basic block the scheduler can interleave freely.
-    const int key0 = kw0;
-    if (key0 + kBN > a.Skv) mask_tail<NS>(s, key0 + 32 * kh, a.Skv, g);
-    const float mx = tile_max<NS>(s, a.sl2);
-#if H3A_LAZY_RESCALE
-    // The reference max only has to bound the exponents: keep the stale max
-    // while this stage's row max exceeds it by at most kRescaleSlack (p stays
-    // <= 2^kRescaleSlack, exact in the fp32 sums and bf16-rounded like any p),
-    // and rescale O and l only when some row of the wave outgrows it.
-    if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0) {
-#else
-    {
-#endif
-      const float mnew = fmaxf(m, mx);
-      const float alpha = fast_exp2(m - ((mnew == kNegInf) ? 0.f : mnew));
-      m = mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-    }
-    const float muse = (m == kNegInf) ? 0.f : m;
-
-    // S(j+1) on the MFMA pipe, softmax(j) on the VALU: no dependence between them.
-    f32x16 n[NS];
-    score_tile<L, NS>(kbuf[P ^ 1], qf, k_rd, n);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[0][r] = fast_exp2(fmaf(s[0][r], a.sl2, -muse));
-      if constexpr (NS == 2) s[1][r] = fast_exp2(fmaf(s[1][r], a.sl2, -muse));
-    }
-    u32x4 pf[2 * NS];
-    pack_p<NS>(s, pf);
-#if H3A_ROWSUM_BF16
-#pragma unroll
-    for (int ks = 0; ks < 2 * NS; ++ks)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) lsum = dot2_bf16_ones(pf[ks][c], lsum);
-#else
-    lsum += tile_sum<NS>(s);
-#endif
-    pv_tile<L, 2 * NS>(vbuf[P], pf, v_rd, o);
-    // Explicit copies: written as an unrolled loop, they changed the 2-sub-tile
-    // build's register allocation (237 -> 245 VGPRs) and cost it ~1 %.
-    s[0] = n[0];
-    if constexpr (NS == 2) s[1] = n[1];
-#if H3A_SCHED_HINTS
-    // Interleave the block: each MFMA followed by LDS reads and VALU work
-    // that can issue in its 32-cycle shadow.
-#pragma unroll
-    for (int i = 0; i < 16 * NS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-    }
-#endif
-
-    kst.finish(kbuf[P]);
-    vst.finish(vbuf[P ^ 1]);
-    land();
-    __syncthreads();
-    kw0 = kw1;
-    kw1 = kw2;
-    e2 = e3;
-  };
-
-  for (int j = 0; j < niter; j += 2) {
-    stage(std::integral_constant<int, 0>{}, j);
-    if (j + 1 < niter) stage(std::integral_constant<int, 1>{}, j + 1);
-  }
-
-  if constexpr (kKeySplit) {
-    // The loop ended on a barrier after every read of the K/V buffers, so
-    // they hold the exchange: O of the key-half-1 wave of each query slice
-    // in kbuf (lane-major: 64 consecutive floats per register), its m and
-    // l in vbuf.
-    static_assert(sizeof(kbuf) >= 2 * 64 * 64 * sizeof(float), "O exchange fits kbuf");
-    static_assert(sizeof(vbuf) >= 2 * 2 * 64 * sizeof(float), "m/l exchange fits vbuf");
-    float *xo = reinterpret_cast<float *>(&kbuf[0][0]) + rq * 64 * 64;
-    float *xm = reinterpret_cast<float *>(&vbuf[0][0]) + rq * 2 * 64;
-    if (kh == 1) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) xo[(16 * dt + r) * 64 + lane] = o[dt][r];
-      xm[lane] = m;
-      xm[64 + lane] = lsum;
-    }
-    __syncthreads();
-    if (kh == 1) return;  // no barrier follows
-    const float m2 = xm[lane], l2 = xm[64 + lane];
-    const float mn = fmaxf(m, m2);
-    const float a1 = m == kNegInf ? 0.f : fast_exp2(m - mn);
-    const float a2 = m2 == kNegInf ? 0.f : fast_exp2(m2 - mn);
-    lsum = lsum * a1 + l2 * a2;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a1 + xo[(16 * dt + r) * 64 + lane] * a2;
-  }
-  const float ltot = half_swap_sum(lsum);
-  const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-  if (qrow < a.Sq) {
-    uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const u32x2 val = {pack_bf16x2(o[dt][4 * rr + 0] * inv, o[dt][4 * rr + 1] * inv),
-                           pack_bf16x2(o[dt][4 * rr + 2] * inv, o[dt][4 * rr + 3] * inv)};
-        *(u32x2 *)(p + dt * 32 + 8 * rr) = val;
-      }
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Softmax of one score stage (32*NSUB keys), in place: S -> P (bf16 pairs in
-// pf), the running max m (refreshed lazily, as in attn_fwd_kernel) and this
-// lane's share of the row sum of the unrounded p; O and l are rescaled when
-// the max moves.  VALU work only.
+// pf), the running max m and this lane's share of the row sum of the
+// unrounded p.  m is refreshed lazily: only when some row of the wave exceeds
+// it by more than kRescaleSlack (p then stays <= 2^kRescaleSlack), and O and l
+// are rescaled only then.  VALU work only.
 template <int NSUB>
 __device__ __forceinline__ void softmax_stage(f32x16 (&s)[NSUB], int key0, int Skv, int g, float sl2,
                                               float &m, float &lsum, f32x16 (&o)[4],
@@ -979,13 +436,14 @@ __device__ __forceinline__ void softmax_stage(f32x16 (&s)[NSUB], int key0, int S
 // Softmax of one score stage against the running reference m without
 // computing the stage's row max.  p = 2^(s*sl2 - m) is formed, packed and
 // summed straight away; only if some lane's stage sum exceeds kStaleSumLimit
-// (or is not finite: a score ran 128 or more above m) does the wave take the
-// row max, refresh m, rescale O and l and redo the stage.  m must be finite
-// on entry (the first stage of a key range uses softmax_stage, which sets m
-// to that stage's row max, so every later row sum is >= 1).  p may then reach
-// 2^64 instead of 1: bf16 rounding of P and the fp32 sums are relative, so the
-// normalised O is unchanged, and 2^64 * 2^16 keys * |v| stays far from the
-// fp32 range limit.
+// or is not finite (stage_sum_needs_refresh; +inf when a score ran 128 or
+// more above m) does the wave take the row max, refresh m, rescale O and l
+// and redo the stage.  m must be finite on entry (the first stage of a key
+// range uses softmax_stage, which sets m to that stage's row max, so every
+// later row sum is >= 1).  Every accepted p is then <= its stage sum <=
+// 2^16 instead of <= 1: bf16 rounding of P and the fp32 sums are relative,
+// so the normalised O is unchanged, and the bound on O that this leaves is
+// given with kStaleSumLimit.
 template <int NSUB>
 __device__ __forceinline__ void exp_pack_sum(const f32x16 (&s)[NSUB], float sl2, float m,
                                              u32x4 (&pf)[2 * NSUB], float &ps) {
@@ -1040,7 +498,7 @@ __device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0,
   float ps;
   exp_pack_sum<NSUB>(s, sl2, kMaybeEmpty && m == kNegInf ? 0.f : m, pf, ps);
   const bool refresh =
-      __builtin_amdgcn_ballot_w64(!(ps <= kStaleSumLimit) || (kMaybeEmpty && m == kNegInf)) != 0;
+      __builtin_amdgcn_ballot_w64(stage_sum_needs_refresh(ps) || (kMaybeEmpty && m == kNegInf)) != 0;
   if (kHint ? __builtin_expect(refresh, 0) : refresh) {
     const float mnew = fmaxf(m, tile_max<NSUB>(s, sl2));
     const float alpha = fast_exp2(m - (kMaybeEmpty && mnew == kNegInf ? 0.f : mnew));
@@ -1053,8 +511,8 @@ __device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0,
   lsum += ps;
 }
 
-// Phase profile of the dense ping-pong kernel (H3A_PROFILE builds; every
-// method compiles to nothing otherwise).  Workgroup 0's 8 waves each sum
+// Phase profile of the ping-pong kernels (H3A_PROFILE builds; every method
+// compiles to nothing otherwise).  Workgroup 0's 8 waves each sum
 // s_memtime ticks (the shader clock) per phase of their stage loop, in
 // registers, and store them once after the loop, one row per wave (with
 // dynamic dispatch, for the last work item workgroup 0 ran):
@@ -1071,22 +529,11 @@ constexpr int kProfSlots = H3A_PROF_SLOTS;
 static_assert(H3A_PROF_WAVES == 8, "one row per wave of the dense workgroup");
 __device__ unsigned long long g_prof[H3A_PROF_WAVES][kProfSlots];
 
-constexpr int kTimelineMax = 1 << 16;
-#if H3A_TIMELINE
-__device__ unsigned long long g_timeline[kTimelineMax][4];
-#endif
-
 struct PhaseClock {
   uint32_t ph[kProfSlots];  // a phase sums < 2^32 ticks for any stage count here
-  uint64_t last, t_loop, rt_loop, t_start, c_start;
-  int index;  // work item (timeline builds)
+  uint64_t last, t_loop, rt_loop;
   bool on;
-  __device__ __forceinline__ void begin(bool enabled, int item) {
-    if constexpr (H3A_TIMELINE) {
-      t_start = __builtin_amdgcn_s_memrealtime();
-      c_start = __builtin_amdgcn_s_memtime();
-      index = item;
-    }
+  __device__ __forceinline__ void begin(bool enabled) {
     if constexpr (H3A_PROFILE) {
       on = enabled;
 #pragma unroll
@@ -1127,18 +574,6 @@ struct PhaseClock {
   }
   // After the epilogue's stores: phase 9, then one row per wave to g_prof.
   __device__ __forceinline__ void finish(int wave, int lane) {
-#if H3A_TIMELINE
-    if (wave == 0 && lane == 0 && index < kTimelineMax) {
-      const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
-      const uint64_t c_end = __builtin_amdgcn_s_memtime();
-      const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_ID
-      const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // XCC_ID
-      g_timeline[index][0] = t_start;
-      g_timeline[index][1] = t_end;
-      g_timeline[index][2] = ((uint64_t)xcc << 32) | hw;
-      g_timeline[index][3] = c_end - c_start;
-    }
-#endif
     if constexpr (H3A_PROFILE) {
       if (on) {
         ph[9] = (uint32_t)(__builtin_amdgcn_s_memtime() - last);
@@ -1168,11 +603,12 @@ __device__ __forceinline__ void slot_barrier() {
 // The boundary between the two clusters of a ping-pong stage: a workgroup
 // barrier when kNeeded (the block-sparse kernels: there group B waits for its
 // own fetch right before it, and the barrier is what makes every wave's fetch
-// visible to the group's next matrix cluster) or when H3A_PP_MID_BARRIER asks
-// for one; otherwise only a scheduling fence.
+// visible to the group's next matrix cluster), otherwise only a scheduling
+// fence (dense: the end-of-stage barrier alone keeps the groups one cluster
+// apart once each softmax slot carries half of the fetch).
 template <bool kNeeded>
 __device__ __forceinline__ void mid_barrier() {
-  if constexpr (kNeeded || H3A_PP_MID_BARRIER) {
+  if constexpr (kNeeded) {
     slot_barrier();
   } else {
     __builtin_amdgcn_sched_barrier(0);
@@ -1186,35 +622,29 @@ __device__ __forceinline__ void mid_barrier() {
 // SOFT(j): S(j+1) -> P(j+1).  Group B runs one cluster behind group A, so on
 // every SIMD one wave issues MFMAs while the other issues the softmax's VALU
 // work and the two pipes overlap.  A workgroup barrier ends every stage (and,
-// in the block-sparse kernels or with H3A_PP_MID_BARRIER, also separates its
-// two clusters).
+// in the block-sparse kernels, also separates its two clusters).
 //
 // Slots of stage j after the prologue:
 //   slot 2j+1:  A: MFMA(j)                        B: DMA K(j+2), SOFT(j-1)
 //   slot 2j+2:  A: DMA V(j+1), SOFT(j), wait      B: MFMA(j), wait
-// K(j+2) goes to kbuf[j&1] and V(j+1) to vbuf[(j+1)&1] (by default group B
-// fetches K and group A fetches V, each at the top of its softmax cluster;
-// H3A_PP_A_KINST / H3A_PP_A_VINST / H3A_PP_A_SOFT move the split).  Those
-// buffers were last read by MFMA(j-1), which both groups finished before the
-// barrier that ended stage j-1; the data is read by MFMA(j+1) in stage j+1,
-// after every wave waited for its share of the fetch before the barrier that
-// ends stage j.
+// K(j+2) goes to kbuf[j&1] and V(j+1) to vbuf[(j+1)&1]: group B fetches K and
+// group A fetches V, each at the top of its softmax cluster, so each softmax
+// slot carries half of the fetch.  Those buffers were last read by
+// MFMA(j-1), which both groups finished before the barrier that ended stage
+// j-1; the data is read by MFMA(j+1) in stage j+1, after every wave waited
+// for its share of the fetch before the barrier that ends stage j.
 //
 // kSparse: block-sparse attention over pairs of query blocks.  Group A takes
 // query block 2p and group B block 2p+1 of pair p, each with its own LUT row
 // and its own double-buffered K/V stages in LDS; both step through the longer
 // of the two stage lists (the shorter one's extra stages load nothing and are
-// fully masked).  By default (H3A_SPARSE_PP_DMA) a group fetches its stages
-// by LDS DMA into SwzLayout rows, K(j+2) at the top of its softmax slot and
-// V(j+1) right after its MFMA(j):
-//   slot 2j+1:  A: MFMA(j), DMA V(j+1)        B: DMA K(j+2), SOFT(j-1)
-//   slot 2j+2:  A: DMA K(j+2), SOFT(j)        B: MFMA(j), DMA V(j+1)
+// fully masked).  A group fetches its stages by LDS DMA, one instruction at a
+// time spread over the PV MFMAs of its own matrix cluster (DmaSeq):
+//   slot 2j+1:  A: MFMA(j) + DMA K(j+2), V(j+1)   B: SOFT(j-1), wait
+//   slot 2j+2:  A: SOFT(j), wait                  B: MFMA(j) + DMA K(j+2), V(j+1)
 // Both go to kbuf[j&1] and vbuf[(j+1)&1], last read by the group's own
 // MFMA(j-1) before an earlier barrier; a wave waits for its own DMA before
-// the barrier that precedes the group's MFMA(j+1) (group B lets the loads
-// issued at the top of the current stage stay in flight: vmcnt(kDmaTop)).
-// With register staging (H3A_SPARSE_PP_DMA=0, PadLayout) a group loads
-// through VGPRs in one slot and writes LDS at the end of its softmax slot.
+// the barrier that precedes the group's MFMA(j+1).
 //
 // kKeySplit (with kSparse): pairs of 64-row query blocks.  Each group's 4
 // waves are 2 query slices (32 rows) x 2 key halves: wave (rq, kh) scores its
@@ -1256,8 +686,6 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   constexpr int kKE = PingPongLds<L, NSUB, kSparse>::kKE, kVE = PingPongLds<L, NSUB, kSparse>::kVE;
   static_assert(!kSparse || BN == kBN, "block-sparse stages are 64 keys");
   static_assert(!kKeySplit || (kSparse && NSUB == 2), "key-split pairs are block-sparse, 64-key stages");
-  constexpr bool kSpDma = kSparse && H3A_SPARSE_PP_DMA;  // sparse stages fetched by LDS DMA
-  static_assert(!kSparse || kSpDma || std::is_same<L, PadLayout>::value, "register staging fills PadLayout");
   auto &kbuf_all = lds.k;
   auto &vbuf_all = lds.v;
 
@@ -1286,13 +714,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     split_part = piece % a.split_pieces;
   } else if (kSparse || item < a.split_first) {
     const int whole = a.split_first < a.total ? a.split_first : a.total;
-#if H3A_XCD_REMAP
     w = remapped ? item : xcd_remap(item, whole);
-#else
-    w = item;
-    (void)whole;
-    (void)remapped;
-#endif
   } else {
     piece = item - a.split_first;
     w = a.split_first + piece / a.split_pieces;
@@ -1439,17 +861,15 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   const int k_rd = L::k_base(l32, g) + kh * 32 * L::kKRow;
   const int v_rd = L::v_base(lane) + kh * 32 * L::kVRow;
 
-  // Dense: each K/V stage is fetched by LDS DMA (all 8 waves, or split
-  // between the groups as the knobs say).  Sparse: each group stages its own
-  // stream through VGPRs (TileRegs, its 4 waves).
-  // Dense with H3A_PP_A_KINST >= 0: waves w and w+4 share one column of
-  // the 4-wave layout, split between them as the knobs say.
-  constexpr bool kSplitDma = !kSparse && H3A_PP_A_KINST >= 0;
-  constexpr int NWD = (kSparse || kSplitDma) ? NW / 2 : NW;
-  TileDma<NWD, L, false, BN> kdma;
-  TileDma<NWD, L, true, BN> vdma;
-  kdma.init(a.kss, NWD == NW ? wave_u : (wave_u & 3), lane);
-  vdma.init(a.vss, NWD == NW ? wave_u : (wave_u & 3), lane);
+  // K/V stages are fetched by LDS DMA, the 4 waves of a group each issuing
+  // the instructions of one column of the 4-wave layout (TileDma).  Dense:
+  // group B fetches the K stages and group A the V stages (waves w and w+4
+  // share a column), each at the top of its softmax slot.  Sparse: each
+  // group fetches its own K/V stream, spread over its matrix cluster.
+  TileDma<NW / 2, L, false, BN> kdma;
+  TileDma<NW / 2, L, true, BN> vdma;
+  kdma.init(a.kss, wave_u & 3, lane);
+  vdma.init(a.vss, wave_u & 3, lane);
   constexpr int kKI = decltype(kdma)::kInst, kVI = decltype(vdma)::kInst;
   // Sparse stage fetches.  By default one descriptor per (b,h) slice, built
   // here, and each stage's byte offset added to the lanes' offsets: the
@@ -1459,7 +879,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // the per-stage descriptors.  kWideKV: offsets up to (Skv + 64) rows would
   // pass 2^32 bytes, so every stage gets its own descriptor based on its
   // first row.
-  constexpr bool kHeadDesc = kSpDma && !kWideKV;
+  constexpr bool kHeadDesc = kSparse && !kWideKV;
   const u32x4 kd_head = stage_desc(Kb, a.kss, a.Skv), vd_head = stage_desc(Vb, a.vss, a.Skv);
   const uint32_t krow_bytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a.kss * 2));
   const uint32_t vrow_bytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a.vss * 2));
@@ -1475,29 +895,13 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   auto v_soff = [&](int key0) __attribute__((always_inline)) {
     return kHeadDesc ? (uint32_t)key0 * vrow_bytes : 0u;
   };
-  // Dense, DMA spread over group A's matrix clusters: group A fetches all.
-  constexpr bool kDenseIn = kSplitDma && H3A_PP_DMA_IN_CLUSTER;
-  constexpr bool kSpIn = kSpDma && (kKeySplit ? H3A_SPARSE64_PP_IN_CLUSTER : H3A_SPARSE_PP_IN_CLUSTER);
-  constexpr int kReadAhead = kSparse ? H3A_PP_READ_AHEAD : H3A_PP_DENSE_READ_AHEAD;
-  constexpr int kPrio = kSparse ? H3A_PP_PRIO : H3A_PP_DENSE_PRIO;
-  constexpr int kKA = kDenseIn ? kKI : (kSplitDma ? H3A_PP_A_KINST : 0);
-  constexpr int kVA = kDenseIn ? kVI : (kSplitDma ? H3A_PP_A_VINST : 0);
-  auto fetch_k = [&](const uint16_t *base, int key0, uint16_t *tile) __attribute__((always_inline)) {
-    if constexpr (kSplitDma) {
-      if (lead) kdma.template issue_range<0, kKA>(base, a.kss, key0, a.Skv, tile);
-      else kdma.template issue_range<kKA, kKI>(base, a.kss, key0, a.Skv, tile);
-    } else {
-      kdma.issue(base, a.kss, key0, a.Skv, tile);
-    }
-  };
-  auto fetch_v = [&](const uint16_t *base, int key0, uint16_t *tile) __attribute__((always_inline)) {
-    if constexpr (kSplitDma) {
-      if (lead) vdma.template issue_range<0, kVA>(base, a.vss, key0, a.Skv, tile);
-      else vdma.template issue_range<kVA, kVI>(base, a.vss, key0, a.Skv, tile);
-    } else {
-      vdma.issue(base, a.vss, key0, a.Skv, tile);
-    }
-  };
+  // LDS operand reads issued ahead of a matrix cluster's first MFMA (then 2
+  // after each MFMA), and the wave priority raised (s_setprio 1) during the
+  // cluster: same-box sweeps chose 4 and no raise for the dense kernel, 6
+  // and the raise for the block-sparse ones.
+  constexpr int kReadAhead = kSparse ? 6 : 4;
+  constexpr int kReadsPerMfma = 2;
+  constexpr bool kRaisePrio = kSparse;
 
   // Dense: cursors of the K stream at local stage 2 and the V stream at
   // stage 1, where the loop's fetches start.  The range ends at key_end, so
@@ -1508,65 +912,21 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     kcur.init(Kb, a.kss, (j0 + 2) * BN, key_end);
     vcur.init(Vb, a.vss, (j0 + 1) * BN, key_end);
   }
-  auto fetch_k_cur = [&](uint16_t *tile) __attribute__((always_inline)) {
-    if constexpr (kSplitDma) {
-      if (lead) {
-        if constexpr (kKA > 0) {
-          kdma.template issue_desc<0, kKA>(kcur.desc(), tile);
-          kcur.advance();
-        }
-      } else if constexpr (kKI > kKA) {
-        kdma.template issue_desc<kKA, kKI>(kcur.desc(), tile);
-        kcur.advance();
-      }
-    } else {
-      kdma.template issue_desc<0, kKI>(kcur.desc(), tile);
-      kcur.advance();
-    }
-  };
-  auto fetch_v_cur = [&](uint16_t *tile) __attribute__((always_inline)) {
-    if constexpr (kSplitDma) {
-      if (lead) {
-        if constexpr (kVA > 0) {
-          vdma.template issue_desc<0, kVA>(vcur.desc(), tile);
-          vcur.advance();
-        }
-      } else if constexpr (kVI > kVA) {
-        vdma.template issue_desc<kVA, kVI>(vcur.desc(), tile);
-        vcur.advance();
-      }
-    } else {
-      vdma.template issue_desc<0, kVI>(vcur.desc(), tile);
-      vcur.advance();
-    }
-  };
 
-  // Sparse: each group's 4 waves stage its K/V stream through VGPRs.
-  TileRegs<NW / 2, false> kst;
-  TileRegs<NW / 2, true> vst;
-  kst.init(a.kss, tid & 255);
-  vst.init(a.vss, tid & 255);
-
-  // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).
+  // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).  Dense:
+  // group B fetches the K stages, group A the V stage.
   const int pkey0 = pro_key(0), pkey1 = pro_key(1);
-  if constexpr (kSpDma) {
+  if constexpr (kSparse) {
     kdma.issue(Kb, a.kss, pkey0, a.Skv, kbuf[0]);
     vdma.issue(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
     kdma.issue(Kb, a.kss, pkey1, a.Skv, kbuf[1]);
-    wait_vmem_all();
-  } else if constexpr (kSparse) {
-    kst.start(Kb, a.kss, pkey0, a.Skv, kbuf[0]);
-    vst.start(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
-    kst.finish(kbuf[0]);
-    vst.finish(vbuf[0]);
-    kst.start(Kb, a.kss, pkey1, a.Skv, kbuf[1]);
-    kst.finish(kbuf[1]);
+  } else if (lead) {
+    vdma.issue(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
   } else {
-    fetch_k(Kb, pkey0, kbuf[0]);
-    fetch_v(Vb, pkey0, vbuf[0]);
-    fetch_k(Kb, pkey1, kbuf[1]);
-    wait_vmem_all();
+    kdma.issue(Kb, a.kss, pkey0, a.Skv, kbuf[0]);
+    kdma.issue(Kb, a.kss, pkey1, a.Skv, kbuf[1]);
   }
+  wait_vmem_all();
   __syncthreads();
   f32x16 s[WS];
   u32x4 pf[2 * WS];
@@ -1574,26 +934,28 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   softmax_stage<WS>(s, pkey0 + 32 * kh, a.Skv, g, a.sl2, m, lsum, o, pf);
   __syncthreads();  // kbuf[0] is free for K(2)
 
-  auto dma = [&](auto par, int j) __attribute__((always_inline)) {
+  // Dense, stage j's fetch from the stream cursors: group A's V(j+1) into
+  // vbuf[(j+1)&1], group B's K(j+2) into kbuf[j&1].
+  auto dma_v = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;  // j & 1
-    fetch_k_cur(kbuf[P]);
-    fetch_v_cur(vbuf[P ^ 1]);
+    vdma.template issue_desc<0, kVI>(vcur.desc(), vbuf[P ^ 1]);
+    vcur.advance();
   };
-  // Sparse: the group's loads of K(j+2) and V(j+1) at the top of its softmax
-  // slot (or after its matrix cluster), and their LDS writes at the end of
-  // the softmax slot.  Entering stage j the group holds the first keys of
-  // stages j, j+1 and j+2 and the LUT entry of stage j+3.  lut_next(j),
-  // issued after a barrier, loads the entry of stage j+4 for the next
-  // stage_keys, so the scalar load's wait falls on the following barrier with
-  // a softmax cluster in between.  The softmax masks with a held key too:
-  // stage j+1's for group A (SOFT(j)), stage j's for group B (SOFT(j-1)).
+  auto dma_k = [&](auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;  // j & 1
+    kdma.template issue_desc<0, kKI>(kcur.desc(), kbuf[P]);
+    kcur.advance();
+  };
+  // Sparse: entering stage j the group holds the first keys of stages j, j+1
+  // and j+2 and the LUT entry of stage j+3.  stage_keys(j) takes stage j's
+  // keys (K(j+2), V(j+1), the softmax mask) and moves the window on;
+  // lut_next(j), issued after a barrier, loads the entry of stage j+4 for
+  // the next stage_keys, so the scalar load's wait falls on the following
+  // barrier with a softmax cluster in between.  The softmax masks with a
+  // held key too: stage j+1's for group A (SOFT(j)), stage j's for group B
+  // (SOFT(j-1)).
   int kw0 = pkey0, kw1 = pkey1, kw2 = pro_key(2), e3 = pro_entry(3);
   int soft_key = 0;
-  // stage_keys(j) takes stage j's keys (K(j+2), V(j+1), the softmax mask)
-  // and moves the window on; load_k / load_v issue the loads.  Group A calls
-  // it in stage j before SOFT(j), which masks S(j+1); group B before
-  // SOFT(j-1) (at the top of stage j, or after MFMA(j-1) when the loads go
-  // early), which masks S(j).
   int key_k = 0, key_v = 0;
   auto stage_keys = [&](int j) __attribute__((always_inline)) {
     soft_key = lead ? kw1 : kw0;
@@ -1604,168 +966,80 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     kw1 = kw2;
     kw2 = kw3;
   };
-  auto load_k = [&]() __attribute__((always_inline)) {
-    kst.start(Kb, a.kss, key_k, a.Skv, nullptr);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  auto load_v = [&]() __attribute__((always_inline)) {
-    vst.start(Vb, a.vss, key_v, a.Skv, nullptr);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  constexpr int kEarly = H3A_SPARSE_PP_EARLY;  // 0: none, 1: K and V, 2: K only, 3: in the cluster
   auto lut_next = [&](int j) __attribute__((always_inline)) { e3 = lut_entry(j + 4); };
-  auto stage_out = [&](auto par) __attribute__((always_inline)) {
-    constexpr int P = decltype(par)::value;
-    __builtin_amdgcn_sched_barrier(0);
-    kst.finish(kbuf[P]);
-    vst.finish(vbuf[P ^ 1]);
-  };
-  // Sparse with LDS DMA: stage j's fetch of K(j+2) into kbuf[j&1] and V(j+1)
-  // into vbuf[(j+1)&1], buffers the group last read in MFMA(j-1).  Issued
-  // right after the group's MFMA(j); the group waits for it before the
-  // barrier that precedes its MFMA(j+1).
-  // Where a group issues stage j's fetch: right after its MFMA(j), or at the
-  // top of its softmax slot while the other group's MFMAs run.  Of each
-  // wave's kInst loads of K (and of V), the first H3A_SPARSE_PP_KTOP
-  // (H3A_SPARSE_PP_VTOP) go at the top, the rest after the MFMAs.
-  constexpr int kKTop = kSpDma ? H3A_SPARSE_PP_KTOP : 0;
-  constexpr int kVTop = kSpDma ? H3A_SPARSE_PP_VTOP : 0;
-  static_assert(!kSpDma || (decltype(kdma)::kInstTotal % (NW / 2) == 0 &&
-                            decltype(vdma)::kInstTotal % (NW / 2) == 0),
+  static_assert(!kSparse || (decltype(kdma)::kInstTotal % (NW / 2) == 0 &&
+                             decltype(vdma)::kInstTotal % (NW / 2) == 0),
                 "every wave issues the same number of DMA loads per stage");
-  static_assert(kKTop <= decltype(kdma)::kInst && kVTop <= decltype(vdma)::kInst, "placement split");
-  // Loads a group-B wave issues at the top of a stage (waited one stage later).
-  constexpr int kDmaTop = kKTop + kVTop;
-  // top = true: the loads that go at the top of the softmax slot.
-  auto dma_k = [&](auto top, auto par) __attribute__((always_inline)) {
-    constexpr int P = decltype(par)::value;
-    constexpr int I0 = decltype(top)::value ? 0 : kKTop;
-    constexpr int I1 = decltype(top)::value ? kKTop : decltype(kdma)::kInst;
-    kdma.template issue_desc_off<I0, I1>(k_desc(key_k), kbuf[P], k_soff(key_k));
+  // The score and PV MFMAs of the cluster with the LDS operand reads issued
+  // ahead of them: kReadAhead up front, then kReadsPerMfma after each MFMA,
+  // so every read is in flight for several MFMAs.
+  auto order_reads = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_group_barrier(0x100, kReadAhead, 0);
+#pragma unroll
+    for (int i = 0; i < 16 * WS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, kReadsPerMfma, 0);
+    }
   };
-  auto dma_v = [&](auto top, auto par) __attribute__((always_inline)) {
-    constexpr int P = decltype(par)::value;
-    constexpr int I0 = decltype(top)::value ? 0 : kVTop;
-    constexpr int I1 = decltype(top)::value ? kVTop : decltype(vdma)::kInst;
-    vdma.template issue_desc_off<I0, I1>(v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
-  };
-  constexpr bool kALate = kSplitDma && !kDenseIn && H3A_PP_A_LATE && (kKA + kVA > 0);
-  // Group A's share at the top of its softmax slot: the buffers it fills were
-  // last read in MFMA(j-1), and it waits for the share before the barrier
-  // that ends the slot, as for any share.
-  constexpr bool kASoft = kSplitDma && !kDenseIn && !kALate && H3A_PP_A_SOFT && (kKA + kVA > 0);
-  // One basic block: 16*NSUB MFMAs (the last stage's scores are of
-  // the zero tile past the keys and are discarded), with the 24*NSUB LDS
-  // operand reads issued ahead of them: kReadAhead up front, then 2
-  // after each MFMA, so every read is in flight for several MFMAs.
+  // Dense matrix cluster: one basic block of 16*NSUB MFMAs (the last stage's
+  // scores are of the zero tile past the keys and are discarded).
   auto mfma = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
-    if (kPrio == 1) __builtin_amdgcn_s_setprio(1);
-#if H3A_PP_PV_FIRST
-    pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o);
+    if (kRaisePrio) __builtin_amdgcn_s_setprio(1);
     score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s);
-#else
-    if constexpr (H3A_PP_INTERLEAVE && WS == 2) {
-      qk_pv_interleaved<L>(kbuf[P ^ 1], vbuf[P], qf, k_rd, v_rd, s, pf, o);
-    } else {
-      score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s);
-      pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o);
-    }
-#endif
-    constexpr bool kLoadsIn = kSparse && kEarly == 3;
-    if constexpr (kLoadsIn) {
-      // Sparse: the group's next K/V loads (stage_keys ran before), one after
-      // each of the last 8 MFMAs, whose execution hides part of their issue.
-      kst.start(Kb, a.kss, key_k, a.Skv, nullptr);
-      vst.start(Vb, a.vss, key_v, a.Skv, nullptr);
-    }
-    if constexpr (kReadAhead > 0) {
-      __builtin_amdgcn_sched_group_barrier(0x100, kReadAhead, 0);
-#pragma unroll
-      for (int i = 0; i < 16 * WS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
-        if (kLoadsIn && i >= 16 * WS - 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      }
-    }
-    if (kPrio == 1) __builtin_amdgcn_s_setprio(0);
+    pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o);
+    order_reads();
+    if (kRaisePrio) __builtin_amdgcn_s_setprio(0);
   };
-  // The matrix cluster with this wave's fetch of K(j+2) (kseq) and V(j+1)
-  // (vseq) spread over it: the K instructions after evenly spaced score
-  // k-steps, the V ones after the PV key steps.  Each DMA instruction is
-  // volatile asm that touches memory, so it keeps its place among the LDS
-  // operand reads, which the scheduling groups interleave with the MFMAs.
-  constexpr bool kDmaPvOnly = H3A_PP_DMA_PV_ONLY;
+  // Sparse matrix cluster with this wave's fetch of K(j+2) (kseq) and V(j+1)
+  // (vseq) spread over it: all NK + NV instructions among the PV MFMAs, K
+  // first, evenly spaced.  Each DMA instruction is volatile asm that touches
+  // memory, so it keeps its place among the LDS operand reads, which the
+  // scheduling groups interleave with the MFMAs.
   auto mfma_dma = [&](auto par, auto &kseq, auto &vseq) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
     constexpr int NK = std::remove_reference_t<decltype(kseq)>::kCount;
     constexpr int NV = std::remove_reference_t<decltype(vseq)>::kCount;
-    constexpr int NKS = 2 * WS;  // PV key steps
-    static_assert(NK > 0 && 8 % NK == 0, "K instructions spread evenly over 8 score k-steps");
-    static_assert(NV > 0 && (NV % NKS == 0 || NKS % NV == 0), "V instructions spread evenly over the PV steps");
-    if (kPrio == 1) __builtin_amdgcn_s_setprio(1);
-    score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s, [&](int ks) __attribute__((always_inline)) {
-      if (!kDmaPvOnly && (ks + 1) % (8 / NK) == 0) kseq.issue();
-    });
-    pv_tile<L, NKS>(vbuf[P], pf, v_rd, o, [&](int t) __attribute__((always_inline)) {
-      if constexpr (kDmaPvOnly) {
-        // All NK + NV instructions among the PV MFMAs, K first, evenly spaced.
-        constexpr int NP = 4 * NKS, NI = NK + NV;
+    constexpr int NP = 4 * 2 * WS, NI = NK + NV;  // PV MFMAs, DMA instructions
+    if (kRaisePrio) __builtin_amdgcn_s_setprio(1);
+    score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s);
+    pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o, [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          if (t == i * NP / NI) {
-            if (i < NK) kseq.issue(); else vseq.issue();
-          }
-        }
-      } else if (t % 4 == 3) {
-        const int ks = t / 4;
-        if constexpr (NV >= NKS) {
-#pragma unroll
-          for (int u = 0; u < NV / NKS; ++u) vseq.issue();
-        } else {
-          if ((ks + 1) % (NKS / NV) == 0) vseq.issue();
+      for (int i = 0; i < NI; ++i) {
+        if (t == i * NP / NI) {
+          if (i < NK) kseq.issue(); else vseq.issue();
         }
       }
     });
-    if constexpr (kReadAhead > 0) {
-      __builtin_amdgcn_sched_group_barrier(0x100, kReadAhead, 0);
-#pragma unroll
-      for (int i = 0; i < 16 * WS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, H3A_PP_READS_PER_MFMA, 0);
-      }
-    }
-    if (kPrio == 1) __builtin_amdgcn_s_setprio(0);
+    order_reads();
+    if (kRaisePrio) __builtin_amdgcn_s_setprio(0);
   };
+  // Sparse: the cluster with the group's fetch of K(j+2) and V(j+1) (keys
+  // from stage_keys) into the buffers the group read in MFMA(j-1).
+  auto mfma_fetch = [&](auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    DmaSeq<decltype(kdma)> kseq(kdma, k_desc(key_k), kbuf[P], k_soff(key_k));
+    DmaSeq<decltype(vdma)> vseq(vdma, v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
+    mfma_dma(par, kseq, vseq);
+  };
+  // Softmax cluster.  Its results are pinned to the slot (pin), so that the
+  // compiler does not sink them past the barrier toward the MFMAs.
   auto soft = [&](int j) __attribute__((always_inline)) {
-    if (kPrio == 2) __builtin_amdgcn_s_setprio(1);
     const int key0 = (kSparse ? soft_key : key_base(j + 1)) + 32 * kh;
-#if H3A_PP_STALE_MAX
     softmax_stage_stale<WS, kSparse>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
-#else
-    softmax_stage<WS>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
-#endif
-#if H3A_PP_PIN_SOFTMAX
 #pragma unroll
     for (int i = 0; i < 2 * WS; ++i) pin(pf[i]);
     pin(lsum);
     pin(m);
-#endif
-    if (kPrio == 2) __builtin_amdgcn_s_setprio(0);
   };
 
   pc.loop_begin();
   if (lead) {
     auto stage = [&](auto par, int j) __attribute__((always_inline)) {
-      if constexpr (kSpIn) {
-        constexpr int P = decltype(par)::value;
+      if constexpr (kSparse) {
         pc.mark(0);
         stage_keys(j);
-        {
-          DmaSeq<decltype(kdma)> kseq(kdma, k_desc(key_k), kbuf[P], k_soff(key_k));
-          DmaSeq<decltype(vdma)> vseq(vdma, v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
-          mfma_dma(par, kseq, vseq);
-        }
+        mfma_fetch(par);
         pc.mark(1);
         mid_barrier<kSparse>();
         pc.mark(2);
@@ -1777,68 +1051,14 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         slot_barrier();
         pc.mark(5);
         pc.stage_done();
-        return;
-      } else if constexpr (kSpDma) {
+      } else {
         pc.mark(0);
         mfma(par);
         pc.mark(1);
-        stage_keys(j);
-        dma_k(std::false_type{}, par);
-        dma_v(std::false_type{}, par);
-        pc.mark(0);
         mid_barrier<kSparse>();
         pc.mark(2);
-        dma_k(std::true_type{}, par);
-        dma_v(std::true_type{}, par);
-        lut_next(j);
-        if (j + 1 < niter) soft(j);        pc.mark(3);
-        wait_vmem_all();
-        pc.mark(4);
-        slot_barrier();
-        pc.mark(5);
-        pc.stage_done();
-        return;
-      } else if constexpr (kSparse) {
-        pc.mark(0);
-        if constexpr (kEarly == 3) stage_keys(j);
-        mfma(par);
-        pc.mark(1);
-        if constexpr (kEarly == 1 || kEarly == 2) {
-          stage_keys(j);
-          load_k();
-          if constexpr (kEarly == 1) load_v();
-        }
-        pc.mark(0);
-        mid_barrier<kSparse>();
-        pc.mark(2);
-        if constexpr (kEarly == 0) {
-          stage_keys(j);
-          load_k();
-        }
-        if constexpr (kEarly == 0 || kEarly == 2) load_v();
-        lut_next(j);
-        if (j + 1 < niter) soft(j);
-        pc.mark(3);
-        stage_out(par);
-        pc.mark(4);
-        slot_barrier();
-        pc.mark(5);
-        pc.stage_done();
-        return;
-      }
-      if constexpr (kDenseIn) {
-        constexpr int P = decltype(par)::value;
-        pc.mark(0);
-        {
-          DmaSeq<decltype(kdma)> kseq(kdma, kcur.desc(), kbuf[P], 0u);
-          DmaSeq<decltype(vdma)> vseq(vdma, vcur.desc(), vbuf[P ^ 1], 0u);
-          mfma_dma(par, kseq, vseq);
-        }
-        kcur.advance();
-        vcur.advance();
-        pc.mark(1);
-        mid_barrier<kSparse>();
-        pc.mark(2);
+        dma_v(par);
+        __builtin_amdgcn_sched_barrier(0);
         if (j + 1 < niter) soft(j);
         pc.mark(3);
         wait_vmem_all();
@@ -1846,29 +1066,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         slot_barrier();
         pc.mark(5);
         pc.stage_done();
-        return;
       }
-      if constexpr (!kALate && !kASoft) dma(par, j);
-      pc.mark(0);
-      mfma(par);
-      if constexpr (kALate) {
-        __builtin_amdgcn_sched_barrier(0);
-        dma(par, j);
-      }
-      pc.mark(1);
-      mid_barrier<kSparse>();
-      pc.mark(2);
-      if constexpr (kASoft) {
-        dma(par, j);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (j + 1 < niter) soft(j);
-      pc.mark(3);
-      wait_vmem_all();
-      pc.mark(4);
-      slot_barrier();
-      pc.mark(5);
-      pc.stage_done();
     };
     for (int j = 0; j < niter; j += 2) {
       stage(std::integral_constant<int, 0>{}, j);
@@ -1878,8 +1076,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     // kFirst: stage 0, which has no softmax before its matrix cluster (P(0)
     // came from the prologue); peeled off so that the loop body has no branch.
     auto stage = [&](auto par, int j, auto first) __attribute__((always_inline)) {
-      if constexpr (kSpIn) {
-        constexpr int P = decltype(par)::value;
+      if constexpr (kSparse) {
         pc.mark(0);
         stage_keys(j);  // also sets the key SOFT(j-1) masks with: stage j's first
         lut_next(j);
@@ -1890,90 +1087,29 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
         pc.mark(4);
         mid_barrier<kSparse>();
         pc.mark(2);
-        {
-          DmaSeq<decltype(kdma)> kseq(kdma, k_desc(key_k), kbuf[P], k_soff(key_k));
-          DmaSeq<decltype(vdma)> vseq(vdma, v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
-          mfma_dma(par, kseq, vseq);
-        }
+        mfma_fetch(par);
         pc.mark(3);
         slot_barrier();
         pc.mark(5);
         pc.stage_done();
-        return;
-      } else if constexpr (kSpDma) {
+      } else {
+        dma_k(par);
         pc.mark(0);
-        stage_keys(j);  // also sets the key SOFT(j-1) masks with: stage j's first
-        dma_k(std::true_type{}, par);
-        dma_v(std::true_type{}, par);
-        lut_next(j);
         if constexpr (!decltype(first)::value) soft(j - 1);
         pc.mark(1);
-        // This wave's fetch of K(j+1) and V(j), issued in stage j-1; what it
-        // issued at the top of this stage may stay in flight.
-        wait_vmem_le<kDmaTop>();
-        pc.mark(4);
         mid_barrier<kSparse>();
         pc.mark(2);
         mfma(par);
         pc.mark(3);
-        dma_k(std::false_type{}, par);
-        dma_v(std::false_type{}, par);
-        pc.mark(0);
-        slot_barrier();
-        pc.mark(5);
-        pc.stage_done();
-        return;
-      } else if constexpr (kSparse) {
-        pc.mark(0);
-        if constexpr (kEarly == 0) {
-          stage_keys(j);
-          load_k();
-        }
-        if constexpr (kEarly == 0 || kEarly == 2) load_v();
-        lut_next(j);
-        if constexpr (!decltype(first)::value) soft(j - 1);
-        pc.mark(1);
-        stage_out(par);
+        wait_vmem_all();
         pc.mark(4);
-        mid_barrier<kSparse>();
-        pc.mark(2);
-        // kEarly == 3: the loads for stage j+1 go inside the matrix cluster,
-        // also after the last stage (keys past the list: nothing is read).
-        if constexpr (kEarly == 3) stage_keys(j + 1);
-        mfma(par);
-        pc.mark(3);
-        if ((kEarly == 1 || kEarly == 2) && j + 1 < niter) {
-          stage_keys(j + 1);
-          load_k();
-          if constexpr (kEarly == 1) load_v();
-        }
-        pc.mark(0);
         slot_barrier();
         pc.mark(5);
         pc.stage_done();
-        return;
       }
-      dma(par, j);
-      pc.mark(0);
-      if constexpr (!decltype(first)::value) soft(j - 1);
-      pc.mark(1);
-      mid_barrier<kSparse>();
-      pc.mark(2);
-      mfma(par);
-      pc.mark(3);
-      wait_vmem_all();
-      pc.mark(4);
-      slot_barrier();
-      pc.mark(5);
-      pc.stage_done();
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
-    if constexpr (kSparse && !kSpDma && kEarly > 0) {
-      stage_keys(0);
-      load_k();
-      if constexpr (kEarly != 2) load_v();
-    }
     stage(C0{}, 0, std::true_type{});
     for (int j = 1; j < niter; j += 2) {
       stage(C1{}, j, std::false_type{});
@@ -2047,7 +1183,6 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     return;
   }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-#if H3A_PP_STORE_LDS
   // The wave's normalised O (32 rows x 128 dims, bf16) leaves through LDS.
   // A lane holds 4-dim pieces of one row, so stored directly every
   // instruction would write 16 bytes into each of 32 rows; written into a
@@ -2090,20 +1225,6 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
       __builtin_amdgcn_raw_buffer_store_b128(val, ores, (int)((uint32_t)r * (uint32_t)a.oss * 2u + 16u * ch), 0, 0);
     }
   }
-#else
-  if (qrow < a.Sq) {
-    uint16_t *p = Ob + (int64_t)qrow * a.oss + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const u32x2 val = {pack_bf16x2(o[dt][4 * rr + 0] * inv, o[dt][4 * rr + 1] * inv),
-                           pack_bf16x2(o[dt][4 * rr + 2] * inv, o[dt][4 * rr + 3] * inv)};
-        *(u32x2 *)(p + dt * 32 + 8 * rr) = val;
-      }
-    }
-  }
-#endif
   pc.finish(wave, lane);
 }
 
@@ -2148,7 +1269,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       item = __builtin_amdgcn_readfirstlane(next_item);
       if (item < 0) break;
     }
-    pc.begin(blockIdx.x == 0, item);
+    pc.begin(blockIdx.x == 0);
     pingpong_item<L, NSUB, kSparse, kKeySplit, kWideKV>(args, item, args.sched != nullptr, lds, pc);
     KernargPtr kq = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(kq));
@@ -2274,33 +1395,17 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 }
 
 // ---------------------------------------------------------------------------
-using DenseLayout = std::conditional_t<H3A_DENSE_LAYOUT == 1, PadLayout, SwzLayout>;
-// Stage layout of the sparse ping-pong kernels: swizzled rows filled by LDS DMA,
-// or padded rows filled from VGPRs.
-using SparseLayout = std::conditional_t<H3A_SPARSE_PP_DMA != 0, SwzLayout, PadLayout>;
-constexpr int kDenseSub = H3A_DENSE_BN / 32;
-// 128-key dense stages (H3A_DENSE_BN=128) measured 22 % slower, and one
-// build of them gave wrong output when the compiler made the softmax lambda an
-// out-of-line call; that cause was never shown from the code, so the variant
-// does not build.
-static_assert(kDenseSub == 2, "dense stages are 64 keys (H3A_DENSE_BN=64)");
+// 32-key score sub-tiles per 64-key stage, in every attention kernel.
+constexpr int kStageSub = kBN / 32;
 
 int launch_attn_dense(AttnArgs a, hipStream_t s) {
-#if H3A_DENSE_PINGPONG
   constexpr int NW = 8;
-#else
-  constexpr int NW = H3A_DENSE_WAVES;
-#endif
   a.nqt = (a.Sq + 32 * NW - 1) / (32 * NW);
   const int64_t total = (int64_t)a.B * a.H * a.nqt;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
   a.total = (int)total;
-#if H3A_DENSE_PINGPONG
-  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>), dim3(a.total), dim3(64 * NW), 0, s, a);
-#else
-  hipLaunchKernelGGL((attn_fwd_kernel<NW, DenseLayout, false, false>), dim3(a.total), dim3(64 * NW), 0, s, a);
-#endif
-  return check_launch("attn_fwd_kernel<dense>");
+  hipLaunchKernelGGL((attn_fwd_pingpong_kernel<SwzLayout, kStageSub>), dim3(a.total), dim3(64 * NW), 0, s, a);
+  return check_launch("attn_fwd_pingpong_kernel<dense>");
 }
 
 // Split-tail plan.  With one workgroup per CU, N whole 256-row tiles run in
@@ -2356,8 +1461,7 @@ static int plan_tiles(int64_t tiles, int stages, bool splittable, bool queued, S
 }
 
 int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
-  return plan_tiles((int64_t)B * H * ((Sq + 255) / 256), (Skv + H3A_DENSE_BN - 1) / H3A_DENSE_BN,
-                    H3A_DENSE_PINGPONG, H3A_DENSE_PINGPONG && H3A_DENSE_QUEUES, plan);
+  return plan_tiles((int64_t)B * H * ((Sq + 255) / 256), (Skv + kBN - 1) / kBN, true, true, plan);
 }
 
 // The longest list a query block can hold (max_k_blocks key blocks) stands in
@@ -2365,9 +1469,7 @@ int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan) {
 int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k_blocks, SplitPlan *plan) {
   const int rows = sparse_sub_block_rows(blk_q);
   const int64_t nsub = (Sq + rows - 1) / rows;
-  const bool pingpong = rows == 128 ? H3A_SPARSE_PINGPONG : H3A_SPARSE64_PINGPONG;
-  return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_k_blocks * (blk_k / 64),
-                    H3A_SPARSE_PINGPONG && rows == 128, pingpong && H3A_SPARSE_QUEUES, plan);
+  return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_k_blocks * (blk_k / 64), rows == 128, true, plan);
 }
 
 // Workgroups of a persistent launch of `kernel` (512 threads): every CU
@@ -2403,7 +1505,7 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
   const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
   a.total = (int)total;
-  auto kernel = attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>;
+  auto kernel = attn_fwd_pingpong_kernel<SwzLayout, kStageSub>;
   int grid = a.total, rc;
   if (plan.dynamic) {
     rc = persistent_grid(reinterpret_cast<const void *>(kernel), 0, &grid);
@@ -2430,10 +1532,10 @@ static PingPongKernel sparse_pingpong_kernel(const AttnArgs &a, int rows) {
   const int64_t stride = a.kss > a.vss ? a.kss : a.vss;
   const bool wide = ((int64_t)a.Skv + 64) * stride * 2 >= ((int64_t)1 << 32);
   if (rows == 128)
-    return wide ? attn_fwd_pingpong_kernel<SparseLayout, 2, true, false, true>
-                : attn_fwd_pingpong_kernel<SparseLayout, 2, true, false, false>;
-  return wide ? attn_fwd_pingpong_kernel<SparseLayout, 2, true, true, true>
-              : attn_fwd_pingpong_kernel<SparseLayout, 2, true, true, false>;
+    return wide ? attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, false, true>
+                : attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, false, false>;
+  return wide ? attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true, true>
+              : attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true, false>;
 }
 
 int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s) {
@@ -2470,23 +1572,12 @@ int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan
 
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
   const int rows = sparse_sub_block_rows(blk_q);
-  if ((H3A_SPARSE_PINGPONG && rows == 128) || (H3A_SPARSE64_PINGPONG && rows == 64)) {
-    AttnArgs p = a;
-    const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
-    if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
-    p.total = (int)pairs;
-    hipLaunchKernelGGL(sparse_pingpong_kernel(p, rows), dim3(p.total), dim3(512), 0, s, p);
-    return check_launch("attn_fwd_pingpong_kernel<sparse>");
-  }
-  if (rows == 128) {
-    hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(256), 0, s, a);
-  } else if (H3A_SPARSE64_KEYSPLIT) {
-    hipLaunchKernelGGL((attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true, true>), dim3(a.total), dim3(256), 0,
-                       s, a);
-  } else {
-    hipLaunchKernelGGL((attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), dim3(a.total), dim3(128), 0, s, a);
-  }
-  return check_launch("attn_fwd_kernel<sparse>");
+  AttnArgs p = a;
+  const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
+  if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
+  p.total = (int)pairs;
+  hipLaunchKernelGGL(sparse_pingpong_kernel(p, rows), dim3(p.total), dim3(512), 0, s, p);
+  return check_launch("attn_fwd_pingpong_kernel<sparse>");
 }
 
 int launch_block_map_to_lut(const uint8_t *map, int B, int H, int nq, int nk, int32_t *lut,
@@ -2537,15 +1628,6 @@ int attn_prof_read(uint64_t *out) {
   return H3A_OK;
 }
 
-#if H3A_TIMELINE
-extern "C" int h3a_timeline_read(unsigned long long *out, int n) {
-  if (hipDeviceSynchronize() != hipSuccess) return H3A_ERR_HIP;
-  const size_t bytes = sizeof(unsigned long long) * 4 * (size_t)(n < kTimelineMax ? n : kTimelineMax);
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_timeline), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess
-             ? H3A_OK : H3A_ERR_HIP;
-}
-#endif
-
 int attn_prof_reset() {
   static const unsigned long long zeros[H3A_PROF_WAVES][kProfSlots] = {};
   if (hipDeviceSynchronize() != hipSuccess) return fail(H3A_ERR_HIP, "hipDeviceSynchronize failed");
@@ -2557,27 +1639,13 @@ int attn_prof_reset() {
 int attn_kernel_attrs(int which, double out[6]) {
   switch (which) {
     case H3A_KERNEL_ATTN_DENSE:
-#if H3A_DENSE_PINGPONG
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<DenseLayout, kDenseSub>), 512, out);
-#else
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<H3A_DENSE_WAVES, DenseLayout, false, false>),
-                        64 * H3A_DENSE_WAVES, out);
-#endif
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SwzLayout, kStageSub>), 512, out);
     case H3A_KERNEL_ATTN_SPARSE_128:
-#if H3A_SPARSE_PINGPONG
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SparseLayout, 2, true>), 512, out);
-#else
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true>), 256, out);
-#endif
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true>), 512,
+                        out);
     case H3A_KERNEL_ATTN_SPARSE_64:
-#if H3A_SPARSE64_PINGPONG
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SparseLayout, 2, true, true>), 512, out);
-#elif H3A_SPARSE64_KEYSPLIT
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<4, PadLayout, H3A_SPARSE_REGS, true, true>),
-                        256, out);
-#else
-      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_kernel<2, PadLayout, H3A_SPARSE_REGS, true>), 128, out);
-#endif
+      return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true>),
+                        512, out);
     default:
       return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
   }

@@ -18,8 +18,9 @@ __host__ __device__ __forceinline__ int block_of_stage(int t, int sub) {
 
 // The same without a branch on sub: t / sub = high 32 bits of (2t) * magic,
 // magic = ceil(2^31 / sub) for sub = 1, 2, 4 (exact powers of two) and
-// (2^32 + 1) / 6 for sub = 3 (2t * magic / 2^32 = (t / 3)(1 + 2^-32), whose
-// floor is t / 3 for 0 <= t < 2^31).  stage_magic is computed once per work
+// ceil(2^32 / 6) = (2^32 + 2) / 6 = 0x2AAAAAAB for sub = 3, where
+// 2t * magic / 2^32 = (t / 3)(1 + 2^-31), whose floor is t / 3 for
+// 0 <= t < 2^31.  stage_magic is computed once per work
 // item; block_of_stage_magic is one shift and one multiply-high.
 __host__ __device__ __forceinline__ uint32_t stage_magic(int sub) {
   return sub == 3 ? 0x2AAAAAABu : 0x80000000u >> (sub >> 1);

@@ -36,6 +36,41 @@ def _noalloc(q, k, v, o):
     _lib.check("h3a_attn_fwd_noalloc", rc)
 
 
+def test_noalloc_first_call_under_graph_capture(gpu):
+    """The process's first h3a_attn_fwd_noalloc call (no other test calls it before this one)
+    is made inside a HIP graph capture, where it sets up the device's scratch address.  Every
+    replay equals h3a_attn_fwd_ws bit for bit, with eager no-alloc calls on other inputs, which
+    overwrite the scratch, between the replays.  One captured case has a split tail, the other
+    queued dispatch."""
+    ins, want = [], []
+    for H, S, seed in ((4, 2048, 11), (56, 8192, 12)):
+        print(f"[noalloc graph] H={H} S={S}", flush=True)
+        g = torch.Generator(device=gpu).manual_seed(seed)
+        q, k, v = (torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+        ins.append((q, k, v))
+        want.append(h3attn.attn_fwd(q, k, v, split_tail=True))  # h3a_attn_fwd_ws
+    outs = [torch.full_like(q, float("nan")) for q, _, _ in ins]
+    g = torch.Generator(device=gpu).manual_seed(13)
+    other = [torch.randn(1, 8, 3000, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3)]
+    other_out = torch.empty_like(other[0])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for (q, k, v), o in zip(ins, outs):
+            _noalloc(q, k, v, o)
+    torch.cuda.synchronize()
+    for r in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, w, (q, _, _) in zip(outs, want, ins):
+            assert torch.equal(o, w), f"replay {r}, H={q.shape[1]}: differs from h3a_attn_fwd_ws"
+        _noalloc(*other, other_out)
+        torch.cuda.synchronize()
+    assert torch.equal(other_out, h3attn.attn_fwd(*other, split_tail=True))
+
+
 def test_noalloc_matches_workspace_entry_point(gpu):
     for i, (H, S, seed) in enumerate(((56, 42120, 1), (4, 2048, 2), (56, 42120, 3))):
         print(f"[noalloc] H={H} S={S}", flush=True)
