@@ -55,16 +55,23 @@ def _clock_from_rows(rows):
     return (sum(ghz) / len(ghz), min(ghz), max(ghz)) if ghz else None
 
 
-def measure_clock_sparse(item, blk):
+def measure_clock_sparse(item, blk, tiles=False):
     """As measure_clock, for the block-sparse kernel: one profiled launch of the first
-    layer's inputs (the ping-pong sparse kernels record workgroup 0's phases)."""
+    layer's inputs (the ping-pong sparse kernels record workgroup 0's phases); `tiles`:
+    the item holds a tile LUT."""
     from h3attn import ops
     try:
         q, k, v, lut, cnt, _ = item
         out = torch_empty_like(q)
-        ops.attn_fwd_blocksparse_profiled(q, k, v, lut, cnt, blk, blk, out=out)
+
+        def run():
+            if tiles:
+                ops.attn_fwd_blocksparse_tiles_profiled(q, k, v, lut, cnt, out=out)
+            else:
+                ops.attn_fwd_blocksparse_profiled(q, k, v, lut, cnt, blk, blk, out=out)
+        run()
         ops.prof_reset()
-        ops.attn_fwd_blocksparse_profiled(q, k, v, lut, cnt, blk, blk, out=out)
+        run()
         c = _clock_from_rows(ops.prof_read())
         if c is None:
             return None, "no profile rows"
@@ -190,7 +197,7 @@ def _parse():
                          "prologue + attention on the fused QKV layout at S=8192, H=56; graph: "
                          "--layers layers of prologue + attention at S=2048, H=4, eager vs one "
                          "HIP-graph replay (launch overhead)")
-    ap.add_argument("--blk", type=int, default=128, choices=[64, 128, 192, 256],
+    ap.add_argument("--blk", type=int, default=128, choices=list(range(16, 257, 16)),
                     help="sparse: query and key tile size (128: the 128x128 workload; 64: the SLA "
                          "block size default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -302,9 +309,10 @@ def run_sparse(args, torch, h3attn, dev):
     """Block-sparse (h3_sla path): blk x blk tiles (128 by default: 330 per head at S=42120),
     top floor(0.25*nk) key tiles per query tile from mean-pooled scores plus the diagonal
     (82 of 330 at 128); FLOPs counted exactly from the map."""
-    from h3attn import sla
+    from h3attn import ops, sla
     L, blk = args.layers, args.blk
     nk = (S + blk - 1) // blk
+    tiles = blk not in ops.NATIVE_BLOCKS
     items = []
     map_ms = []
     for layer in range(L):
@@ -315,6 +323,8 @@ def run_sparse(args, torch, h3attn, dev):
         a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         bmap, lut, cnt = sla.get_block_map(q, k, 0.25, blk, blk, force_diag=True, smooth_k=False)
+        if tiles:  # block sizes outside the native kernels': 64x64 tiles with sub-block masks
+            lut, cnt = ops.block_map_to_tile_lut(bmap, blk, blk, S, S)
         b_.record()
         torch.cuda.synchronize()
         map_ms.append(a.elapsed_time(b_))
@@ -331,13 +341,16 @@ def run_sparse(args, torch, h3attn, dev):
         for i, (q, k, v, lut, cnt, _) in enumerate(items):
             if events is not None:
                 events[i][0].record(stream)
-            h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk, out=out)
+            if tiles:
+                ops.attn_fwd_blocksparse_tiles(q, k, v, lut, cnt, out=out)
+            else:
+                h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk, out=out)
             if events is not None:
                 events[i][1].record(stream)
 
     wall, avg_kernel_ms = _timed(step, args.steps, args.warmup, L, torch, stream)
     _calib_copy(args, torch, dev)
-    ghz, clock_note = measure_clock_sparse(items[0], blk) if not args.no_clock else (None, "skipped")
+    ghz, clock_note = measure_clock_sparse(items[0], blk, tiles) if not args.no_clock else (None, "skipped")
     flops = sum(it[5] for it in items) / L
     value = flops * L * args.steps / wall / 1e12
     achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
@@ -355,7 +368,9 @@ def run_sparse(args, torch, h3attn, dev):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": ("attn_fwd_pingpong_kernel<SwzLayout,2,sparse> (pairs of 128-row query blocks; "
+                     "kernel": ("attn_fwd_pingpong_kernel<SwzLayout,2,sparse,key-split,tile-mask> (pairs of "
+                                "64-row query blocks over 64x64 tiles with 16x16 sub-block masks)" if tiles
+                                else "attn_fwd_pingpong_kernel<SwzLayout,2,sparse> (pairs of 128-row query blocks; "
                                 "+ split_combine_kernel for the split tail)" if blk % 128 == 0
                                 else "attn_fwd_pingpong_kernel<SwzLayout,2,sparse,key-split> (pairs of 64-row "
                                      "query blocks)"), "flop_per_launch": flops,

@@ -136,9 +136,10 @@ int h3a_attn_fwd_noalloc(const void *q, const void *k, const void *v, void *o,
  * Skipped blocks contribute nothing; a query block with no kept key block
  * gets O = 0.  LUT entries that name no key block (negative, or at or past
  * ceil(Skv/blk_k)) are skipped as well.  blk_q and blk_k each in
- * {64, 128, 192, 256} (multiples of the kernels' 64-key stage; the h3_sla
- * node's other sizes, custom_nodes/h3_sla/__init__.py:315, give
- * H3A_ERR_UNSUPPORTED).  Other arguments as h3a_attn_fwd.
+ * {64, 128, 192, 256} (multiples of the kernels' 64-key stage); the h3_sla
+ * node's other sizes (multiples of 16 from 16 to 256,
+ * custom_nodes/h3_sla/__init__.py:315) give H3A_ERR_UNSUPPORTED here and run
+ * through h3a_attn_fwd_blocksparse_tiles.  Other arguments as h3a_attn_fwd.
  */
 int h3a_attn_fwd_blocksparse(const void *q, const void *k, const void *v, void *o,
                              int B, int H, int Sq, int Skv, int D,
@@ -173,6 +174,61 @@ int h3a_attn_fwd_blocksparse_ws(const void *q, const void *k, const void *v, voi
                                 int blk_q, int blk_k, int max_k_blocks,
                                 float scale, void *workspace, size_t workspace_bytes,
                                 h3a_stream_t stream);
+
+/*
+ * Block-sparse attention over 64x64 tiles with sub-block masks: the path for
+ * block sizes h3a_attn_fwd_blocksparse does not take (the h3_sla node offers
+ * every multiple of 16 from 16 to 256, custom_nodes/h3_sla/__init__.py:315;
+ * query and key blocks may differ).  The tile LUT comes from
+ * h3a_block_map_to_tile_lut: row (b*H + h)*ceil(Sq/64) + qs of tile_lut
+ * [.., max_tiles] lists, for query rows 64*qs .. 64*qs+63, the 64-key stages
+ * to attend to, each entry stage << 16 | mask, where bit 4*i + j of the mask
+ * admits rows 64*qs + 16*i .. +15 against keys 64*stage + 16*j .. +15 (every
+ * other score of the tile is masked); tile_counts holds each row's length.
+ * Entries whose stage is negative or at or past ceil(Skv/64) load nothing.
+ * A row with no admitted key gets O = 0.  Skv <= 32767 * 64.  max_tiles in
+ * [1, ceil(Skv/64)].  Other arguments as h3a_attn_fwd; _ws and
+ * _workspace_size as for h3a_attn_fwd_blocksparse_ws (work queues, no split).
+ * No counterpart in the reference's own code: SLA's Triton kernel takes the
+ * same block maps at these sizes.
+ */
+int h3a_attn_fwd_blocksparse_tiles(const void *q, const void *k, const void *v, void *o,
+                                   int B, int H, int Sq, int Skv, int D,
+                                   const int64_t q_strides[3], const int64_t k_strides[3],
+                                   const int64_t v_strides[3], const int64_t o_strides[3],
+                                   const int32_t *tile_lut, const int32_t *tile_counts, int max_tiles,
+                                   float scale, h3a_stream_t stream);
+int h3a_attn_fwd_blocksparse_tiles_workspace_size(int B, int H, int Sq, int Skv, int D, int max_tiles,
+                                                  size_t *bytes);
+int h3a_attn_fwd_blocksparse_tiles_ws(const void *q, const void *k, const void *v, void *o,
+                                      int B, int H, int Sq, int Skv, int D,
+                                      const int64_t q_strides[3], const int64_t k_strides[3],
+                                      const int64_t v_strides[3], const int64_t o_strides[3],
+                                      const int32_t *tile_lut, const int32_t *tile_counts, int max_tiles,
+                                      float scale, void *workspace, size_t workspace_bytes,
+                                      h3a_stream_t stream);
+
+/*
+ * Convert a 0/1 block map [B,H,ceil(Sq/blk_q),ceil(Skv/blk_k)] (uint8,
+ * contiguous) at any block sizes that are multiples of 16 into the tile LUT of
+ * h3a_attn_fwd_blocksparse_tiles: tile_lut [B,H,ceil(Sq/64),max_tiles] (-1
+ * padded) and tile_counts [B,H,ceil(Sq/64)].  A row with more than max_tiles
+ * stages keeps its first max_tiles; max_tiles = ceil(Skv/64) always suffices.
+ * The SLA block map (custom_nodes/h3_sla/__init__.py:232) at the node's
+ * block sizes.
+ */
+int h3a_block_map_to_tile_lut(const uint8_t *block_map, int B, int H, int Sq, int Skv, int blk_q, int blk_k,
+                              int32_t *tile_lut, int32_t *tile_counts, int max_tiles, h3a_stream_t stream);
+
+/*
+ * The inverse of h3a_block_map_to_lut: block_map [B,H,nq,nk] (uint8) = 1 for
+ * the key blocks each LUT row lists (its first counts[row] entries; entries
+ * outside [0, nk) ignored), 0 elsewhere.  Two kernels on `stream`.  For
+ * callers that hold an h3_sla LUT at a block size that runs through
+ * h3a_attn_fwd_blocksparse_tiles.
+ */
+int h3a_lut_to_block_map(const int32_t *lut, const int32_t *counts, int B, int H, int nq, int nk,
+                         int max_k_blocks, uint8_t *block_map, h3a_stream_t stream);
 
 /*
  * Compact a boolean block map [B,H,nq,nk] (uint8, 0/1, contiguous) into the
@@ -237,6 +293,7 @@ int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D,
 #define H3A_KERNEL_ATTN_SPARSE_128 1
 #define H3A_KERNEL_ATTN_SPARSE_64  2
 #define H3A_KERNEL_QK_ROPE         3
+#define H3A_KERNEL_ATTN_SPARSE_TILES 4
 
 /*
  * out[6] = {VGPRs per thread, LDS bytes per workgroup, max resident

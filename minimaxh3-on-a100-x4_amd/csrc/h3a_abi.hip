@@ -302,6 +302,125 @@ int h3a_attn_fwd_blocksparse_ws(const void *q, const void *k, const void *v, voi
   return launch_attn_sparse_split(a, blk_q, plan, workspace, as_stream(stream));
 }
 
+namespace {
+
+// Checks shared by the tile-LUT entry points; fills `a` on success.
+int prepare_tiles(AttnArgs &a, const void *q, const void *k, const void *v, void *o, int B, int H, int Sq,
+                  int Skv, int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                  const int64_t v_strides[3], const int64_t o_strides[3], const int32_t *lut,
+                  const int32_t *counts, int max_tiles, float scale) {
+  int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
+  if (rc) return rc;
+  if (!lut || !counts) return fail(H3A_ERR_INVALID_ARG, "null tile_lut/tile_counts pointer");
+  const int64_t nstages = ((int64_t)Skv + 63) / 64;
+  if (nstages > kMaxTileStages)
+    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d stages of 64 keys", Skv, kMaxTileStages);
+  if (max_tiles <= 0 || max_tiles > nstages)
+    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)nstages);
+  const int64_t nsub = ((int64_t)Sq + 63) / 64;
+  const int64_t total = (int64_t)B * H * nsub;
+  if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
+  fill_attn_args(a, q, k, v, o, B, H, Sq, Skv, q_strides, k_strides, v_strides, o_strides, scale);
+  a.nqt = (int)nsub;
+  a.total = (int)total;
+  a.lut = lut;
+  a.counts = counts;
+  a.lut_stride = max_tiles;
+  a.blk_k = 64;
+  a.sub = 1;
+  a.nkb = (int)nstages;
+  a.nqb = (int)nsub;
+  a.qmul = 1;
+  return H3A_OK;
+}
+
+}  // namespace
+
+int h3a_attn_fwd_blocksparse_tiles(const void *q, const void *k, const void *v, void *o, int B, int H, int Sq,
+                                   int Skv, int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                                   const int64_t v_strides[3], const int64_t o_strides[3],
+                                   const int32_t *tile_lut, const int32_t *tile_counts, int max_tiles, float scale,
+                                   h3a_stream_t stream) {
+  clear_error();
+  AttnArgs a;
+  const int rc = prepare_tiles(a, q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides,
+                               tile_lut, tile_counts, max_tiles, scale);
+  if (rc) return rc;
+  return launch_attn_sparse(a, 64, as_stream(stream), true);
+}
+
+int h3a_attn_fwd_blocksparse_tiles_workspace_size(int B, int H, int Sq, int Skv, int D, int max_tiles,
+                                                  size_t *bytes) {
+  clear_error();
+  if (!bytes) return fail(H3A_ERR_INVALID_ARG, "null output pointer");
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
+  if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
+  const int64_t nstages = ((int64_t)Skv + 63) / 64;
+  if (nstages > kMaxTileStages)
+    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d stages of 64 keys", Skv, kMaxTileStages);
+  if (max_tiles <= 0 || max_tiles > nstages)
+    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)nstages);
+  SplitPlan plan;
+  const int rc = plan_attn_sparse_tiles(B, H, Sq, max_tiles, &plan);
+  if (rc) return rc;
+  *bytes = plan.bytes;
+  return H3A_OK;
+}
+
+int h3a_attn_fwd_blocksparse_tiles_ws(const void *q, const void *k, const void *v, void *o, int B, int H, int Sq,
+                                      int Skv, int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                                      const int64_t v_strides[3], const int64_t o_strides[3],
+                                      const int32_t *tile_lut, const int32_t *tile_counts, int max_tiles,
+                                      float scale, void *workspace, size_t workspace_bytes, h3a_stream_t stream) {
+  clear_error();
+  AttnArgs a;
+  int rc = prepare_tiles(a, q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, tile_lut,
+                         tile_counts, max_tiles, scale);
+  if (rc) return rc;
+  SplitPlan plan;
+  rc = plan_attn_sparse_tiles(B, H, Sq, max_tiles, &plan);
+  if (rc) return rc;
+  if (plan.bytes > 0) {
+    if (!workspace || workspace_bytes < plan.bytes)
+      return fail(H3A_ERR_INVALID_ARG, "workspace of %zu bytes needed, %zu given", plan.bytes,
+                  workspace ? workspace_bytes : (size_t)0);
+    if (!aligned16(workspace)) return fail(H3A_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+  }
+  return launch_attn_sparse_split(a, 64, plan, workspace, as_stream(stream), true);
+}
+
+int h3a_block_map_to_tile_lut(const uint8_t *block_map, int B, int H, int Sq, int Skv, int blk_q, int blk_k,
+                              int32_t *tile_lut, int32_t *tile_counts, int max_tiles, h3a_stream_t stream) {
+  clear_error();
+  if (!block_map || !tile_lut || !tile_counts) return fail(H3A_ERR_INVALID_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
+  if (!tile_block_ok(blk_q) || !tile_block_ok(blk_k))
+    return fail(H3A_ERR_UNSUPPORTED, "block sizes %d x %d: multiples of 16 only", blk_q, blk_k);
+  const int64_t nstages = ((int64_t)Skv + 63) / 64;
+  if (nstages > kMaxTileStages)
+    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d stages of 64 keys", Skv, kMaxTileStages);
+  if (max_tiles <= 0 || max_tiles > nstages)
+    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)nstages);
+  const int64_t rows = (int64_t)B * H * ((Sq + 63) / 64);
+  if ((rows + 3) / 4 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many tile LUT rows");
+  return launch_block_map_to_tile_lut(block_map, B, H, Sq, Skv, blk_q, blk_k, tile_lut, tile_counts, max_tiles,
+                                      as_stream(stream));
+}
+
+int h3a_lut_to_block_map(const int32_t *lut, const int32_t *counts, int B, int H, int nq, int nk,
+                         int max_k_blocks, uint8_t *block_map, h3a_stream_t stream) {
+  clear_error();
+  if (!lut || !counts || !block_map) return fail(H3A_ERR_INVALID_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || nq <= 0 || nk <= 0 || max_k_blocks <= 0)
+    return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d nq=%d nk=%d max_k_blocks=%d)", B, H, nq,
+                nk, max_k_blocks);
+  const int64_t rows = (int64_t)B * H * nq;
+  if ((rows + 3) / 4 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "block map too large");
+  return launch_lut_to_block_map(lut, counts, B, H, nq, nk, max_k_blocks, block_map, as_stream(stream));
+}
+
 int h3a_block_map_to_lut(const uint8_t *block_map, int B, int H, int nq, int nk, int32_t *lut,
                          int32_t *counts, int max_k_blocks, h3a_stream_t stream) {
   clear_error();
@@ -387,7 +506,7 @@ int h3a_kernel_attrs(int which, double out[6]) {
   clear_error();
   if (!out) return fail(H3A_ERR_INVALID_ARG, "null output array");
   if (which == H3A_KERNEL_QK_ROPE) return rope_kernel_attrs(out);
-  if (which < H3A_KERNEL_ATTN_DENSE || which > H3A_KERNEL_ATTN_SPARSE_64)
+  if (which != H3A_KERNEL_ATTN_SPARSE_TILES && (which < H3A_KERNEL_ATTN_DENSE || which > H3A_KERNEL_ATTN_SPARSE_64))
     return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
   return attn_kernel_attrs(which, out);
 }

@@ -404,6 +404,25 @@ __device__ __forceinline__ void mask_tail(f32x16 (&s)[NSUB], int key0, int Skv, 
   }
 }
 
+// Tile-mask sparse attention (64-row key-split pairs over 64x64 tiles, each
+// with a 16-bit mask of kept 16x16 sub-blocks): the scores of this wave's
+// key half whose sub-block bit is clear -> -inf.  Bit 4*i + j covers rows
+// 16i..16i+15 of the 64-row query block and keys 16j..16j+15 of the 64-key
+// stage.  The lane's query row is 32*rq + l32; its scores s[0][r] are keys
+// 32*kh + 8*(r/4) + 4*g + r%4, so registers 0-7 lie in key sub-block 2*kh and
+// registers 8-15 in 2*kh + 1.
+template <int NSUB>
+__device__ __forceinline__ void apply_tile_mask(f32x16 (&s)[NSUB], uint32_t mask, int rq, int l32, int kh) {
+  static_assert(NSUB == 1, "tile masks apply to the 32-key waves of the key-split kernel");
+  const uint32_t bits = mask >> (4 * (2 * rq + (l32 >> 4)) + 2 * kh);
+  const bool k0 = (bits & 1u) != 0, k1 = (bits & 2u) != 0;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    s[0][r] = k0 ? s[0][r] : kNegInf;
+    s[0][r + 8] = k1 ? s[0][r + 8] : kNegInf;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Softmax of one score stage (32*NSUB keys), in place: S -> P (bf16 pairs in
 // pf), the running max m and this lane's share of the row sum of the
@@ -676,7 +695,7 @@ struct PingPongLds {
 // range of a split tile, or (sparse) a pair of query blocks or a piece of one.
 // `remapped`: the item number is already XCD-aware (taken from the queues),
 // so whole tiles are not remapped.
-template <class L, int NSUB, bool kSparse, bool kKeySplit, bool kWideKV>
+template <class L, int NSUB, bool kSparse, bool kKeySplit, bool kWideKV, bool kTileMask>
 __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item, const bool remapped,
                                               PingPongLds<L, NSUB, kSparse> &lds, PhaseClock &pc) {
   constexpr int NW = 8;
@@ -686,6 +705,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   constexpr int kKE = PingPongLds<L, NSUB, kSparse>::kKE, kVE = PingPongLds<L, NSUB, kSparse>::kVE;
   static_assert(!kSparse || BN == kBN, "block-sparse stages are 64 keys");
   static_assert(!kKeySplit || (kSparse && NSUB == 2), "key-split pairs are block-sparse, 64-key stages");
+  static_assert(!kTileMask || kKeySplit, "tile masks run on the key-split pairs");
   auto &kbuf_all = lds.k;
   auto &vbuf_all = lds.v;
 
@@ -799,8 +819,12 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
       return 0;
     }
   };
-  auto key_of_entry = [&](int j, int kb) __attribute__((always_inline)) -> int {
+  // Tile masks: an entry is stage << 16 | mask, the stage in units of 64
+  // keys (a.blk_k = 64, a.sub = 1); an arithmetic shift keeps a negative
+  // entry negative, so it still names no key block.
+  auto key_of_entry = [&](int j, int e) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
+      const int kb = kTileMask ? (e >> 16) : e;
       // Two equivalent forms; each measured faster in one kernel (the
       // arithmetic one +0.5 % in the 128-row pairs, the select one +0.6 % in
       // the key-split pairs), through the code layout around them.
@@ -916,6 +940,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).  Dense:
   // group B fetches the K stages, group A the V stage.
   const int pkey0 = pro_key(0), pkey1 = pro_key(1);
+  const uint32_t pmask0 = kTileMask ? (uint32_t)pro_entry(0) & 0xffffu : 0u;
   if constexpr (kSparse) {
     kdma.issue(Kb, a.kss, pkey0, a.Skv, kbuf[0]);
     vdma.issue(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
@@ -931,6 +956,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   f32x16 s[WS];
   u32x4 pf[2 * WS];
   score_tile<L, WS>(kbuf[0], qf, k_rd, s);
+  if constexpr (kTileMask) apply_tile_mask<WS>(s, pmask0, rq, l32, kh);
   softmax_stage<WS>(s, pkey0 + 32 * kh, a.Skv, g, a.sl2, m, lsum, o, pf);
   __syncthreads();  // kbuf[0] is free for K(2)
 
@@ -953,10 +979,15 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // the next stage_keys, so the scalar load's wait falls on the following
   // barrier with a softmax cluster in between.  The softmax masks with a
   // held key too: stage j+1's for group A (SOFT(j)), stage j's for group B
-  // (SOFT(j-1)).
+  // (SOFT(j-1)).  Tile masks travel with the keys (mw0..mw2, soft_mask).
   int kw0 = pkey0, kw1 = pkey1, kw2 = pro_key(2), e3 = pro_entry(3);
   int soft_key = 0;
   int key_k = 0, key_v = 0;
+  uint32_t mw0 = pmask0, mw1 = 0, mw2 = 0, soft_mask = 0;
+  if constexpr (kTileMask) {
+    mw1 = (uint32_t)pro_entry(1) & 0xffffu;
+    mw2 = (uint32_t)pro_entry(2) & 0xffffu;
+  }
   auto stage_keys = [&](int j) __attribute__((always_inline)) {
     soft_key = lead ? kw1 : kw0;
     key_k = kw2;
@@ -965,6 +996,12 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     kw0 = kw1;
     kw1 = kw2;
     kw2 = kw3;
+    if constexpr (kTileMask) {
+      soft_mask = lead ? mw1 : mw0;
+      mw0 = mw1;
+      mw1 = mw2;
+      mw2 = (uint32_t)e3 & 0xffffu;
+    }
   };
   auto lut_next = [&](int j) __attribute__((always_inline)) { e3 = lut_entry(j + 4); };
   static_assert(!kSparse || (decltype(kdma)::kInstTotal % (NW / 2) == 0 &&
@@ -1026,6 +1063,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // compiler does not sink them past the barrier toward the MFMAs.
   auto soft = [&](int j) __attribute__((always_inline)) {
     const int key0 = (kSparse ? soft_key : key_base(j + 1)) + 32 * kh;
+    if constexpr (kTileMask) apply_tile_mask<WS>(s, soft_mask, rq, l32, kh);
     softmax_stage_stale<WS, kSparse>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
 #pragma unroll
     for (int i = 0; i < 2 * WS; ++i) pin(pf[i]);
@@ -1228,7 +1266,8 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   pc.finish(wave, lane);
 }
 
-template <class L, int NSUB, bool kSparse = false, bool kKeySplit = false, bool kWideKV = false>
+template <class L, int NSUB, bool kSparse = false, bool kKeySplit = false, bool kWideKV = false,
+          bool kTileMask = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_fwd_pingpong_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) PingPongLds<L, NSUB, kSparse> lds;
@@ -1270,7 +1309,7 @@ attn_fwd_pingpong_kernel(AttnArgs a) {
       if (item < 0) break;
     }
     pc.begin(blockIdx.x == 0);
-    pingpong_item<L, NSUB, kSparse, kKeySplit, kWideKV>(args, item, args.sched != nullptr, lds, pc);
+    pingpong_item<L, NSUB, kSparse, kKeySplit, kWideKV, kTileMask>(args, item, args.sched != nullptr, lds, pc);
     KernargPtr kq = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(kq));
     if (!kq->sched) break;
@@ -1472,11 +1511,19 @@ int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k
   return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_k_blocks * (blk_k / 64), rows == 128, true, plan);
 }
 
+// The same for a tile LUT (64-row sub-blocks, unsplit): max_tiles entries
+// stand in for the stage count.
+int plan_attn_sparse_tiles(int B, int H, int Sq, int max_tiles, SplitPlan *plan) {
+  const int64_t nsub = (Sq + 63) / 64;
+  return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_tiles, false, true, plan);
+}
+
 // Workgroups of a persistent launch of `kernel` (512 threads): every CU
 // filled to its occupancy, cached per device.
-// `slot` names the kernel in the cache (0 dense, 1 sparse pairs, 2 sparse key-split).
+// `slot` names the kernel in the cache (0 dense, 1 sparse pairs, 2 sparse
+// key-split, 3 sparse key-split over tile masks).
 static int persistent_grid(const void *kernel, int slot, int *grid) {
-  static std::atomic<int> grid_cache[64][3];
+  static std::atomic<int> grid_cache[64][4];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(H3A_ERR_HIP, "hipGetDevice failed");
   std::atomic<int> *cached = (dev >= 0 && dev < 64) ? &grid_cache[dev][slot] : nullptr;
@@ -1524,13 +1571,17 @@ int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStre
   return check_launch("split_combine_kernel");
 }
 
-// The block-sparse ping-pong kernel for query blocks of `rows` rows; the
+// The block-sparse ping-pong kernel for query blocks of `rows` rows (with
+// `tiles`: the key-split pairs over a tile LUT with sub-block masks); the
 // wide-K/V instantiation when stage offsets from the (b,h) slice base could
 // pass 2^32 bytes (see kWideKV).
 typedef void (*PingPongKernel)(AttnArgs);
-static PingPongKernel sparse_pingpong_kernel(const AttnArgs &a, int rows) {
+static PingPongKernel sparse_pingpong_kernel(const AttnArgs &a, int rows, bool tiles) {
   const int64_t stride = a.kss > a.vss ? a.kss : a.vss;
   const bool wide = ((int64_t)a.Skv + 64) * stride * 2 >= ((int64_t)1 << 32);
+  if (tiles)
+    return wide ? attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true, true, true>
+                : attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true, false, true>;
   if (rows == 128)
     return wide ? attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, false, true>
                 : attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, false, false>;
@@ -1538,9 +1589,10 @@ static PingPongKernel sparse_pingpong_kernel(const AttnArgs &a, int rows) {
               : attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true, false>;
 }
 
-int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s) {
-  if (plan.pieces < 2 && !plan.dynamic) return launch_attn_sparse(a, blk_q, s);
-  const int rows = sparse_sub_block_rows(blk_q);
+int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s,
+                             bool tiles) {
+  if (plan.pieces < 2 && !plan.dynamic) return launch_attn_sparse(a, blk_q, s, tiles);
+  const int rows = tiles ? 64 : sparse_sub_block_rows(blk_q);
   if (plan.pieces >= 2 && rows != 128) return fail(H3A_ERR_INVALID_ARG, "split plan for 64-row query blocks");
   AttnArgs p = a;
   if (plan.pieces >= 2) {
@@ -1551,10 +1603,10 @@ int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan
   const int64_t total = (int64_t)plan.first + (int64_t)(plan.tiles - plan.first) * plan.pieces;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many work items (%lld)", (long long)total);
   p.total = (int)total;
-  const PingPongKernel kernel = sparse_pingpong_kernel(p, rows);
+  const PingPongKernel kernel = sparse_pingpong_kernel(p, rows, tiles);
   int grid = p.total, rc;
   if (plan.dynamic) {
-    rc = persistent_grid(reinterpret_cast<const void *>(kernel), rows == 128 ? 1 : 2, &grid);
+    rc = persistent_grid(reinterpret_cast<const void *>(kernel), tiles ? 3 : (rows == 128 ? 1 : 2), &grid);
     if (rc) return rc;
     if (grid > p.total) grid = p.total;
     p.sched = reinterpret_cast<int *>(static_cast<char *>(ws) + plan.sched_off);
@@ -1570,13 +1622,13 @@ int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan
   return check_launch("split_combine_kernel<sparse>");
 }
 
-int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s) {
-  const int rows = sparse_sub_block_rows(blk_q);
+int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s, bool tiles) {
+  const int rows = tiles ? 64 : sparse_sub_block_rows(blk_q);
   AttnArgs p = a;
   const int64_t pairs = (int64_t)a.B * a.H * ((a.nqt + 1) / 2);
   if (pairs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query-block pairs (%lld)", (long long)pairs);
   p.total = (int)pairs;
-  hipLaunchKernelGGL(sparse_pingpong_kernel(p, rows), dim3(p.total), dim3(512), 0, s, p);
+  hipLaunchKernelGGL(sparse_pingpong_kernel(p, rows, tiles), dim3(p.total), dim3(512), 0, s, p);
   return check_launch("attn_fwd_pingpong_kernel<sparse>");
 }
 
@@ -1646,6 +1698,10 @@ int attn_kernel_attrs(int which, double out[6]) {
     case H3A_KERNEL_ATTN_SPARSE_64:
       return fill_attrs(reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true>),
                         512, out);
+    case H3A_KERNEL_ATTN_SPARSE_TILES:
+      return fill_attrs(
+          reinterpret_cast<const void *>(&attn_fwd_pingpong_kernel<SwzLayout, kStageSub, true, true, false, true>),
+          512, out);
     default:
       return fail(H3A_ERR_INVALID_ARG, "unknown kernel id %d", which);
   }

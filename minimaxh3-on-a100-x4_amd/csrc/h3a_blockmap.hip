@@ -311,6 +311,103 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     select_rows_lds();
 }
 
+// ---------------------------------------------------------------------------
+// Tile LUTs, for block sizes the native block-sparse kernels do not take (any
+// multiple of 16, in either dimension).  The attention then runs on 64-row
+// query sub-blocks and 64-key stages: the tile LUT row of sub-block qs lists,
+// ascending, every stage holding a kept (query block, key block) pair for some
+// row of qs, as stage << 16 | mask.  Bit 4*i + j of the mask is set when rows
+// 64*qs + 16*i .. +15 and keys 64*stage + 16*j .. +15 lie in a kept pair; both
+// block sizes are multiples of 16, so each 16x16 sub-block lies in exactly one
+// pair.  Sub-blocks past Sq or Skv get no bit.  One wave per LUT row; lane l
+// takes stages 64*c + l, and the kept ones are written in order with one
+// ballot per 64 stages.  Entries past the count are -1.
+__global__ void __launch_bounds__(256) block_map_to_tile_lut_kernel(const uint8_t *map, int64_t rows, int nsub,
+                                                                    int nq, int nk, int Sq, int Skv, int blk_q,
+                                                                    int blk_k, int nstages, int32_t *lut,
+                                                                    int32_t *counts, int max_tiles) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves leave together
+  const int qs = (int)(row % nsub);
+  const int64_t bh = row / nsub;
+  // Map row of each 16-row slice of the sub-block (null past Sq).
+  const uint8_t *mq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 64 * qs + 16 * i;
+    mq[i] = r < Sq ? map + (bh * nq + r / blk_q) * (int64_t)nk : nullptr;
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int32_t *out = lut + row * (int64_t)max_tiles;
+  int base = 0;
+  for (int c = 0; c < nstages; c += 64) {
+    const int st = c + lane;
+    uint32_t mask = 0;
+    if (st < nstages) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = 64 * st + 16 * j;
+        if (key >= Skv) break;
+        const int kb = key / blk_k;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (mq[i] && mq[i][kb]) mask |= 1u << (4 * i + j);
+      }
+    }
+    const uint64_t m = __builtin_amdgcn_ballot_w64(mask != 0);
+    const int pos = base + __builtin_popcountll(m & below);
+    if (mask != 0 && pos < max_tiles) out[pos] = (int32_t)(((uint32_t)st << 16) | mask);
+    base += __builtin_popcountll(m);
+  }
+  const int kept = base < max_tiles ? base : max_tiles;
+  for (int j = kept + lane; j < max_tiles; j += 64) out[j] = -1;
+  if (lane == 0) counts[row] = kept;
+}
+
+// A block LUT -> 0/1 block map [rows, nk]: the map is cleared by one launch,
+// and the next sets the listed blocks (entries outside [0, nk), and those past
+// a row's count, are ignored).  Two launches, so that no byte is written by
+// two threads of one kernel.
+__global__ void __launch_bounds__(256) clear_bytes_kernel(uint8_t *p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
+__global__ void __launch_bounds__(256) lut_scatter_kernel(const int32_t *lut, const int32_t *counts, int64_t rows,
+                                                          int nk, int max_k, uint8_t *map) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int cnt = counts[row];
+  const int n = cnt < 0 ? 0 : (cnt > max_k ? max_k : cnt);
+  for (int e = lane; e < n; e += 64) {
+    const int kb = lut[row * (int64_t)max_k + e];
+    if (kb >= 0 && kb < nk) map[row * (int64_t)nk + kb] = 1;
+  }
+}
+
+int launch_block_map_to_tile_lut(const uint8_t *map, int B, int H, int Sq, int Skv, int blk_q, int blk_k,
+                                 int32_t *lut, int32_t *counts, int max_tiles, hipStream_t s) {
+  const int nsub = (Sq + 63) / 64, nq = (Sq + blk_q - 1) / blk_q, nk = (Skv + blk_k - 1) / blk_k;
+  const int nstages = (Skv + 63) / 64;
+  const int64_t rows = (int64_t)B * H * nsub;
+  hipLaunchKernelGGL(block_map_to_tile_lut_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, map, rows,
+                     nsub, nq, nk, Sq, Skv, blk_q, blk_k, nstages, lut, counts, max_tiles);
+  return check_launch("block_map_to_tile_lut_kernel");
+}
+
+int launch_lut_to_block_map(const int32_t *lut, const int32_t *counts, int B, int H, int nq, int nk,
+                            int max_k_blocks, uint8_t *map, hipStream_t s) {
+  const int64_t rows = (int64_t)B * H * nq, bytes = rows * nk;
+  const int64_t clear_blocks = (bytes + 255) / 256 < 65536 ? (bytes + 255) / 256 : 65536;
+  hipLaunchKernelGGL(clear_bytes_kernel, dim3((unsigned)clear_blocks), dim3(256), 0, s, map, bytes);
+  int rc = check_launch("clear_bytes_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(lut_scatter_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, lut, counts, rows, nk,
+                     max_k_blocks, map);
+  return check_launch("lut_scatter_kernel");
+}
+
 int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int S, int blk,
                       float *out, hipStream_t s) {
   const int nb = (S + blk - 1) / blk;

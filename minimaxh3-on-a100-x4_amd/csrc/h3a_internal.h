@@ -55,6 +55,12 @@ struct AttnArgs {
 // kernel) or 64 rows (blk_q 64, 192: the key-split kernel); a key block is
 // blk_k / 64 stages.
 inline bool sparse_block_ok(int blk) { return blk == 64 || blk == 128 || blk == 192 || blk == 256; }
+// Block sizes of a block map that h3a_block_map_to_tile_lut converts: any
+// positive multiple of 16 (each 16x16 sub-block of a 64x64 tile then lies in
+// exactly one block pair).
+inline bool tile_block_ok(int blk) { return blk > 0 && blk % 16 == 0; }
+// Stages a tile LUT entry can name (16 bits): Skv <= kMaxTileStages * 64.
+constexpr int kMaxTileStages = 32767;
 inline int sparse_sub_block_rows(int blk_q) { return blk_q % 128 == 0 ? 128 : 64; }
 
 // Dense split-tail plan for a problem on the current device.
@@ -71,13 +77,21 @@ struct SplitPlan {
 int launch_attn_dense(AttnArgs a, hipStream_t s);  // sets nqt/total from its tile height
 int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan);
 int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s);
-int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s);
+// tiles: a.lut is a tile LUT (stage << 16 | sub-block mask per entry) over
+// 64-row query sub-blocks and 64-key stages; blk_q is then ignored.
+int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s, bool tiles = false);
 // Block-sparse split tail: pairs of 128-row query blocks play the part of
 // the dense tiles (no split for other block heights).
 int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k_blocks, SplitPlan *plan);
-int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s);
+int plan_attn_sparse_tiles(int B, int H, int Sq, int max_tiles, SplitPlan *plan);
+int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s,
+                             bool tiles = false);
 int launch_block_map_to_lut(const uint8_t *map, int B, int H, int nq, int nk, int32_t *lut,
                             int32_t *counts, int max_k_blocks, hipStream_t s);
+int launch_block_map_to_tile_lut(const uint8_t *map, int B, int H, int Sq, int Skv, int blk_q, int blk_k,
+                                 int32_t *lut, int32_t *counts, int max_tiles, hipStream_t s);
+int launch_lut_to_block_map(const int32_t *lut, const int32_t *counts, int B, int H, int nq, int nk,
+                            int max_k_blocks, uint8_t *map, hipStream_t s);
 int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int S, int blk,
                       float *out, hipStream_t s);
 int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, int nk, int keep,

@@ -28,6 +28,7 @@ KERNEL_ATTN_DENSE = 0
 KERNEL_ATTN_SPARSE_128 = 1
 KERNEL_ATTN_SPARSE_64 = 2
 KERNEL_QK_ROPE = 3
+KERNEL_ATTN_SPARSE_TILES = 4
 
 _c_i64_3 = ctypes.c_int64 * 3
 _vp = ctypes.c_void_p
@@ -54,6 +55,15 @@ SIGNATURES = {
     "h3a_attn_fwd_blocksparse_ws": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                          _c_i64_3, _c_i64_3, _c_i64_3, _c_i64_3,
                                          _vp, _vp, _i, _i, _i, _f, _vp, ctypes.c_size_t, _vp]),
+    "h3a_attn_fwd_blocksparse_tiles": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                            _c_i64_3, _c_i64_3, _c_i64_3, _c_i64_3, _vp, _vp, _i, _f, _vp]),
+    "h3a_attn_fwd_blocksparse_tiles_workspace_size": (_i, [_i, _i, _i, _i, _i, _i,
+                                                           ctypes.POINTER(ctypes.c_size_t)]),
+    "h3a_attn_fwd_blocksparse_tiles_ws": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                               _c_i64_3, _c_i64_3, _c_i64_3, _c_i64_3, _vp, _vp, _i, _f,
+                                               _vp, ctypes.c_size_t, _vp]),
+    "h3a_block_map_to_tile_lut": (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
+    "h3a_lut_to_block_map": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "h3a_block_map_to_lut": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
     "h3a_qk_rmsnorm_rope": (_i, [_vp, _vp, _i, _i, _i, _i, _c_i64_3, _c_i64_3,
                                  _vp, _i64, _i64, _i, _vp, _vp, _f, _vp]),

@@ -22,7 +22,8 @@ class H3SLAPatch:
                 "topk": ("FLOAT", {"default": 0.35, "min": 0.02, "max": 1.0, "step": 0.01,
                                    "tooltip": "fraction of key blocks each query block keeps (1 - sparsity)"}),
                 "blk": ("INT", {"default": 64, "min": lo, "max": hi, "step": sla.BLOCK_STEP,
-                                "tooltip": f"query and key block size, one of {sla.SUPPORTED_BLOCKS}"}),
+                                "tooltip": "query and key block size (64, 128, 192 and 256 run the "
+                                           "native kernels, the other sizes 64x64 tiles with sub-block masks)"}),
                 "enabled": ("BOOLEAN", {"default": True}),
             },
             "optional": {

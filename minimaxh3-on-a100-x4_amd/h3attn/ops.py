@@ -153,6 +153,21 @@ def attn_fwd_blocksparse_profiled(q, k, v, lut, counts, blk_q: int, blk_k: int, 
     return out
 
 
+def attn_fwd_blocksparse_tiles_profiled(q, k, v, tile_lut, tile_counts, scale: float | None = None,
+                                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """attn_fwd_blocksparse_tiles through the phase-profile build (h3a_attn_fwd_blocksparse_tiles)."""
+    q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
+    tile_lut, tile_counts = tile_lut.contiguous(), tile_counts.contiguous()
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    L = lib(profile=True)
+    with torch.cuda.device(q.device):
+        rc = L.h3a_attn_fwd_blocksparse_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq,
+                                              Skv, D, _bhs(q), _bhs(k), _bhs(v), _bhs(out), tile_lut.data_ptr(),
+                                              tile_counts.data_ptr(), int(tile_lut.shape[3]), sc, _stream(q))
+    check("h3a_attn_fwd_blocksparse_tiles (profile build)", rc, L)
+    return out
+
+
 def prof_enabled(profile: bool = True) -> bool:
     """Whether the library (profile=True: the profile build) records phases."""
     return bool(lib(profile=profile).h3a_prof_enabled())
@@ -181,6 +196,18 @@ def sparse_workspace_bytes(B: int, H: int, Sq: int, Skv: int, blk_q: int, blk_k:
     return int(n.value)
 
 
+# Block sizes h3a_attn_fwd_blocksparse runs natively (multiples of its 64-key
+# stage); every other multiple of 16 runs over tile LUTs with sub-block masks.
+NATIVE_BLOCKS = (64, 128, 192, 256)
+
+
+def _check_block_size(blk) -> int:
+    b = int(blk)
+    if b <= 0 or b % 16 != 0:
+        raise ValueError(f"block size {blk} unsupported: a positive multiple of 16")
+    return b
+
+
 def attn_fwd_blocksparse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lut: torch.Tensor,
                          counts: torch.Tensor, blk_q: int, blk_k: int, scale: float | None = None,
                          out: torch.Tensor | None = None, split_tail: bool = True) -> torch.Tensor:
@@ -188,10 +215,20 @@ def attn_fwd_blocksparse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lut:
 
     lut: int32 [B,H,ceil(Sq/blk_q),max_k_blocks] ascending key-block indices;
     counts: int32 [B,H,ceil(Sq/blk_q)] number of valid entries per row.
+    blk_q, blk_k: multiples of 16.  Sizes in NATIVE_BLOCKS run
+    h3a_attn_fwd_blocksparse; with any other size the LUT becomes a block map
+    (h3a_lut_to_block_map), then a tile LUT (h3a_block_map_to_tile_lut), run
+    by h3a_attn_fwd_blocksparse_tiles.
     split_tail: as for attn_fwd (h3a_attn_fwd_blocksparse_ws with a workspace
     from torch's allocator); False runs h3a_attn_fwd_blocksparse, which never
     splits.
     """
+    blk_q, blk_k = _check_block_size(blk_q), _check_block_size(blk_k)
+    if blk_q not in NATIVE_BLOCKS or blk_k not in NATIVE_BLOCKS:
+        Sq, Skv = q.shape[2], k.shape[2]
+        bmap = lut_to_block_map(lut, counts, -(-Skv // blk_k))
+        tlut, tcnt = block_map_to_tile_lut(bmap, blk_q, blk_k, Sq, Skv)
+        return attn_fwd_blocksparse_tiles(q, k, v, tlut, tcnt, scale=scale, out=out, queues=split_tail)
     q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
     nqb = -(-Sq // blk_q)
     if lut.dtype != torch.int32 or counts.dtype != torch.int32:
@@ -219,6 +256,89 @@ def attn_fwd_blocksparse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lut:
             rc = lib().h3a_attn_fwd_blocksparse(*args, _stream(q))
             check("h3a_attn_fwd_blocksparse", rc)
     return out
+
+
+def tiles_workspace_bytes(B: int, H: int, Sq: int, Skv: int, max_tiles: int, D: int = HEAD_DIM) -> int:
+    """Workspace bytes h3a_attn_fwd_blocksparse_tiles_ws needs on the current device (0: none)."""
+    n = ctypes.c_size_t(0)
+    check("h3a_attn_fwd_blocksparse_tiles_workspace_size",
+          lib().h3a_attn_fwd_blocksparse_tiles_workspace_size(B, H, Sq, Skv, D, int(max_tiles), ctypes.byref(n)))
+    return int(n.value)
+
+
+def attn_fwd_blocksparse_tiles(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tile_lut: torch.Tensor,
+                               tile_counts: torch.Tensor, scale: float | None = None,
+                               out: torch.Tensor | None = None, queues: bool = True) -> torch.Tensor:
+    """Block-sparse attention over 64x64 tiles with 16x16 sub-block masks (block_map_to_tile_lut).
+
+    tile_lut: int32 [B,H,ceil(Sq/64),max_tiles], entries stage << 16 | mask;
+    tile_counts: int32 [B,H,ceil(Sq/64)].  queues: run through
+    h3a_attn_fwd_blocksparse_tiles_ws (per-XCD work queues, workspace from
+    torch's allocator); False runs h3a_attn_fwd_blocksparse_tiles.
+    """
+    q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
+    nsub = -(-Sq // 64)
+    if tile_lut.dtype != torch.int32 or tile_counts.dtype != torch.int32:
+        raise ValueError("tile_lut and tile_counts must be int32")
+    if tile_lut.dim() != 4 or tuple(tile_lut.shape[:3]) != (B, H, nsub):
+        raise ValueError(f"tile_lut must be [B,H,{nsub},max_tiles], got {tuple(tile_lut.shape)}")
+    if tuple(tile_counts.shape) != (B, H, nsub):
+        raise ValueError(f"tile_counts must be [B,H,{nsub}], got {tuple(tile_counts.shape)}")
+    if tile_lut.device != q.device or tile_counts.device != q.device:
+        raise ValueError("tile_lut/tile_counts must be on q's device")
+    tile_lut, tile_counts = tile_lut.contiguous(), tile_counts.contiguous()
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    max_tiles = int(tile_lut.shape[3])
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Skv, D,
+            _bhs(q), _bhs(k), _bhs(v), _bhs(out), tile_lut.data_ptr(), tile_counts.data_ptr(), max_tiles, sc)
+    with torch.cuda.device(q.device):
+        nbytes = tiles_workspace_bytes(B, H, Sq, Skv, max_tiles, D) if queues else 0
+        if nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+            rc = lib().h3a_attn_fwd_blocksparse_tiles_ws(*args, ws.data_ptr(), nbytes, _stream(q))
+            check("h3a_attn_fwd_blocksparse_tiles_ws", rc)
+        else:
+            rc = lib().h3a_attn_fwd_blocksparse_tiles(*args, _stream(q))
+            check("h3a_attn_fwd_blocksparse_tiles", rc)
+    return out
+
+
+def block_map_to_tile_lut(block_map: torch.Tensor, blk_q: int, blk_k: int, Sq: int, Skv: int,
+                          max_tiles: int | None = None):
+    """0/1 block map [B,H,ceil(Sq/blk_q),ceil(Skv/blk_k)] at block sizes that are multiples of 16
+    -> (tile_lut int32 [B,H,ceil(Sq/64),max_tiles], tile_counts int32 [B,H,ceil(Sq/64)]) for
+    attn_fwd_blocksparse_tiles.  max_tiles defaults to ceil(Skv/64), which always suffices."""
+    blk_q, blk_k = _check_block_size(blk_q), _check_block_size(blk_k)
+    if block_map.dim() != 4 or not block_map.is_cuda:
+        raise ValueError("block_map must be a 4-D GPU tensor [B,H,nq,nk]")
+    B, H, nq, nk = block_map.shape
+    if (nq, nk) != (-(-Sq // blk_q), -(-Skv // blk_k)):
+        raise ValueError(f"block_map [.., {nq}, {nk}] does not match Sq={Sq}/blk_q={blk_q}, Skv={Skv}/blk_k={blk_k}")
+    m = block_map.to(torch.uint8).contiguous()
+    nstages = -(-Skv // 64)
+    max_tiles = nstages if max_tiles is None else int(max_tiles)
+    nsub = -(-Sq // 64)
+    lut = torch.empty((B, H, nsub, max_tiles), dtype=torch.int32, device=m.device)
+    counts = torch.empty((B, H, nsub), dtype=torch.int32, device=m.device)
+    rc = lib().h3a_block_map_to_tile_lut(m.data_ptr(), B, H, int(Sq), int(Skv), blk_q, blk_k, lut.data_ptr(),
+                                         counts.data_ptr(), max_tiles, _stream(m))
+    check("h3a_block_map_to_tile_lut", rc)
+    return lut, counts
+
+
+def lut_to_block_map(lut: torch.Tensor, counts: torch.Tensor, nk: int) -> torch.Tensor:
+    """Block LUT [B,H,nq,max_k] + counts [B,H,nq] -> 0/1 uint8 block map [B,H,nq,nk]."""
+    if lut.dtype != torch.int32 or counts.dtype != torch.int32 or not lut.is_cuda or lut.dim() != 4:
+        raise ValueError("lut must be an int32 GPU tensor [B,H,nq,max_k] with int32 counts")
+    B, H, nq, max_k = lut.shape
+    if tuple(counts.shape) != (B, H, nq) or counts.device != lut.device:
+        raise ValueError(f"counts must be [B,H,{nq}] on lut's device")
+    lut, counts = lut.contiguous(), counts.contiguous()
+    bmap = torch.empty((B, H, nq, int(nk)), dtype=torch.uint8, device=lut.device)
+    rc = lib().h3a_lut_to_block_map(lut.data_ptr(), counts.data_ptr(), B, H, nq, int(nk), int(max_k),
+                                    bmap.data_ptr(), _stream(lut))
+    check("h3a_lut_to_block_map", rc)
+    return bmap
 
 
 def block_map_to_lut(block_map: torch.Tensor, max_k_blocks: int | None = None):

@@ -126,18 +126,20 @@ def format_summary(sm: dict) -> str:
 
 
 # ---------------------------------------------------------------------------
-# Block sizes the block-sparse kernels take (query and key blocks alike):
-# multiples of their 64-key stage.  The h3_sla node offers 16..256 in steps of
-# 16 (custom_nodes/h3_sla/__init__.py:315); the others are refused up front.
-SUPPORTED_BLOCKS = (64, 128, 192, 256)
-BLOCK_STEP = 64  # spacing of SUPPORTED_BLOCKS
+# Block sizes (query and key blocks alike): those the h3_sla node offers, 16 to
+# 256 in steps of 16 (custom_nodes/h3_sla/__init__.py:315).  The multiples of
+# the kernels' 64-key stage (ops.NATIVE_BLOCKS) run the native block-sparse
+# kernels; the others run over 64x64 tiles with 16x16 sub-block masks
+# (ops.attn_fwd_blocksparse_tiles).  Anything else is refused up front.
+BLOCK_STEP = 16
+SUPPORTED_BLOCKS = tuple(range(16, 257, BLOCK_STEP))
 
 
 def check_block(blk) -> int:
     """Return blk as an int, or raise ValueError if the kernels cannot run it."""
     b = int(blk)
     if b not in SUPPORTED_BLOCKS:
-        raise ValueError(f"SLA block size {blk} unsupported by libh3attn; use one of {SUPPORTED_BLOCKS}")
+        raise ValueError(f"SLA block size {blk} unsupported by libh3attn; use a multiple of 16 from 16 to 256")
     return b
 
 
@@ -169,11 +171,20 @@ def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int
 
 def sparse_attention(q, k, v, topk_ratio: float, blk: int = 64, force_diag: bool = False,
                      smooth_k: bool = True):
-    """[1,H,S,D] -> [1,H,S,D] block-sparse attention (SLA sparse branch only; h3_sla:226-235)."""
+    """[1,H,S,D] -> [1,H,S,D] block-sparse attention (SLA sparse branch only; h3_sla:226-235).
+
+    Native block sizes run on the block LUT; the others on the tile LUT
+    built from the block map.
+    """
     blk = check_block(blk)
     out_dtype = q.dtype
     q16, k16, v16 = (t.to(torch.bfloat16) for t in (q, k, v))
-    _, lut, counts = get_block_map(q16, k16, topk_ratio, blk, blk, force_diag=force_diag,
-                                   smooth_k=smooth_k, want_map=False)
-    o = ops.attn_fwd_blocksparse(q16, k16, v16, lut, counts, blk, blk)
+    native = blk in ops.NATIVE_BLOCKS
+    bmap, lut, counts = get_block_map(q16, k16, topk_ratio, blk, blk, force_diag=force_diag,
+                                      smooth_k=smooth_k, want_map=not native)
+    if native:
+        o = ops.attn_fwd_blocksparse(q16, k16, v16, lut, counts, blk, blk)
+    else:
+        tlut, tcnt = ops.block_map_to_tile_lut(bmap, blk, blk, q16.shape[2], k16.shape[2])
+        o = ops.attn_fwd_blocksparse_tiles(q16, k16, v16, tlut, tcnt)
     return o.to(out_dtype)

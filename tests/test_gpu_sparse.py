@@ -16,7 +16,7 @@ import torch
 import h3attn
 import oracle
 from conftest import assert_close_absmax, from_dev_bf16, ramp_case, randn_bf16, to_dev_bf16
-from h3attn import ops, sla
+from h3attn import _lib, ops, sla
 
 pytestmark = pytest.mark.gpu
 
@@ -108,14 +108,23 @@ def test_sparse_batched_cross_lengths_strided_side_stream(gpu, blk_q, blk_k, Sq,
 
 
 def test_sparse_unsupported_block_sizes_raise(gpu):
+    """Block sizes that are not multiples of 16 raise ValueError before any launch; the native
+    entry point h3a_attn_fwd_blocksparse refuses sizes outside {64, 128, 192, 256} with
+    H3A_ERR_UNSUPPORTED (the Python op runs those through the tile LUT entry points)."""
     q = torch.zeros(1, 1, 256, 128, dtype=torch.bfloat16, device=gpu)
     lut = torch.zeros(1, 1, 8, 1, dtype=torch.int32, device=gpu)
     cnt = torch.ones(1, 1, 8, dtype=torch.int32, device=gpu)
-    for bq, bk in ((32, 64), (64, 96), (48, 48), (320, 64)):
-        nqb = -(-256 // bq)
+    for bq, bk in ((40, 64), (64, 24), (8, 8), (-64, 64)):
+        nqb = -(-256 // abs(bq))
         with pytest.raises(ValueError, match="unsupported"):
             h3attn.attn_fwd_blocksparse(q, q, q, lut[:, :, :1].expand(1, 1, nqb, 1).contiguous(),
                                         cnt[:, :, :1].expand(1, 1, nqb).contiguous(), bq, bk)
+    L = _lib.lib()
+    st = _lib.strides3(256 * 128, 256 * 128, 128)
+    for bq, bk in ((32, 64), (64, 96), (48, 48), (320, 64)):
+        rc = L.h3a_attn_fwd_blocksparse(q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr(), 1, 1, 256, 256, 128,
+                                        st, st, st, st, lut.data_ptr(), cnt.data_ptr(), bq, bk, 1, 0.1, None)
+        assert rc == _lib.H3A_ERR_UNSUPPORTED, (bq, bk, rc)
 
 
 @pytest.mark.parametrize("S,blk_k,blk_q", [(640, 128, 128), (1300, 64, 128), (131, 128, 128),
@@ -492,3 +501,122 @@ def test_sparse_queued_matches_one_pair_per_workgroup(gpu, blk):
     torch.cuda.synchronize()
     assert torch.equal(got, want), f"blk={blk}: queued dispatch differs from one pair per workgroup"
     assert not got[:, :, :blk].any(), "rows of empty lists must be 0"
+
+
+# ----------------------------------------------------------------------------- tile LUTs (other block sizes)
+TILE_SIZES = [16, 32, 48, 80, 96, 112, 144, 160, 176, 208, 224, 240]
+
+
+def _tile_lut_np(bmap, blk_q, blk_k, Sq, Skv):
+    """Restatement of the tile LUT on the CPU: per 64-row query sub-block, the ascending 64-key
+    stages with a kept (query block, key block) pair, as stage << 16 | mask with bit 4*i + j for
+    rows 16i.. and keys 16j.. of the tile."""
+    B, H, nq, nk = bmap.shape
+    nsub, nst = -(-Sq // 64), -(-Skv // 64)
+    rows = {}
+    for b, h, qs in np.ndindex(B, H, nsub):
+        ents = []
+        for st in range(nst):
+            mask = 0
+            for i in range(4):
+                r = 64 * qs + 16 * i
+                if r >= Sq:
+                    continue
+                for j in range(4):
+                    key = 64 * st + 16 * j
+                    if key < Skv and bmap[b, h, r // blk_q, key // blk_k]:
+                        mask |= 1 << (4 * i + j)
+            if mask:
+                ents.append((st << 16) | mask)
+        rows[(b, h, qs)] = ents
+    return rows
+
+
+def _check_tile_lut(tlut, tcnt, want):
+    tl, tc = tlut.cpu().numpy(), tcnt.cpu().numpy()
+    for idx, ents in want.items():
+        n = len(ents)
+        assert tc[idx] == n, (idx, tc[idx], n)
+        assert list(tl[idx][:n]) == ents, idx
+        assert (tl[idx][n:] == -1).all(), idx
+
+
+@pytest.mark.parametrize("blk", TILE_SIZES)
+def test_sparse_tile_sizes_vs_masked_oracle(gpu, blk):
+    """Block sizes the native kernels do not take (the h3_sla node's other sizes,
+    custom_nodes/h3_sla/__init__.py:315): the block map becomes a tile LUT, equal to the CPU
+    restatement entry for entry, and the tile kernel's output equals the masked oracle."""
+    rng = np.random.default_rng(300 + blk)
+    S, H = 700 + blk, 2
+    q, k, v = (randn_bf16(rng, (1, H, S, 128)) for _ in range(3))
+    nk = -(-S // blk)
+    bmap = oracle.block_map(q, k, blk, blk, keep=max(1, nk // 4), force_diag=True)
+    tlut, tcnt = ops.block_map_to_tile_lut(torch.from_numpy(bmap).to(gpu), blk, blk, S, S)
+    _check_tile_lut(tlut, tcnt, _tile_lut_np(bmap, blk, blk, S, S))
+    o = ops.attn_fwd_blocksparse_tiles(*(to_dev_bf16(x, gpu) for x in (q, k, v)), tlut, tcnt)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
+    assert_close_absmax(got, ref, what=f"tiles blk={blk}")
+
+
+@pytest.mark.parametrize("blk_q,blk_k,Sq,Skv", [(32, 64, 640, 900), (64, 32, 900, 640), (96, 128, 1000, 1000),
+                                                (48, 208, 777, 1300), (256, 16, 1111, 500), (16, 256, 500, 1111),
+                                                (160, 224, 1500, 1501)])
+def test_sparse_tile_mixed_sizes_from_lut(gpu, blk_q, blk_k, Sq, Skv):
+    """attn_fwd_blocksparse with a block LUT at sizes outside the native ones, query and key blocks
+    different and Sq != Skv: LUT -> block map -> tile LUT -> tile kernel, against the masked
+    oracle; the map is also compared with the LUT it came from."""
+    rng = np.random.default_rng(blk_q * 1000 + blk_k + Sq)
+    H = 2
+    q = randn_bf16(rng, (1, H, Sq, 128))
+    k, v = (randn_bf16(rng, (1, H, Skv, 128)) for _ in range(2))
+    nk = -(-Skv // blk_k)
+    bmap = oracle.block_map(q, k, blk_q, blk_k, keep=max(1, nk // 3), force_diag=False)
+    bmap[0, 1, 0] = 0  # a query block with no kept key block: its rows come out 0
+    lut, cnt = h3attn.block_map_to_lut(torch.from_numpy(bmap).to(gpu))
+    assert np.array_equal(ops.lut_to_block_map(lut, cnt, nk).cpu().numpy(), bmap)
+    o = h3attn.attn_fwd_blocksparse(*(to_dev_bf16(x, gpu) for x in (q, k, v)), lut, cnt, blk_q, blk_k)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk_q, blk_k=blk_k)
+    assert_close_absmax(got, ref, what=f"tiles blk_q={blk_q} blk_k={blk_k}")
+    assert not got[0, 1, :blk_q].any()
+
+
+@pytest.mark.parametrize("blk", [32, 96])
+def test_sla_sparse_attention_at_tile_sizes(gpu, blk):
+    """sla.sparse_attention end to end at a tile size (pool, select, tile LUT, tile kernel), with
+    the block map checked against the oracle's pooled top-k at the same keep."""
+    rng = np.random.default_rng(77 + blk)
+    S, H, keep = 1200, 3, 0.25
+    q, k, v = (randn_bf16(rng, (1, H, S, 128)) for _ in range(3))
+    nk = -(-S // blk)
+    bmap = oracle.block_map(q, k, blk, blk, keep=sla.keep_count(keep, nk), force_diag=False)
+    qd, kd, vd = (to_dev_bf16(x, gpu) for x in (q, k, v))
+    gmap, _, _ = sla.get_block_map(qd, kd, keep, blk, blk)
+    assert np.array_equal(gmap.cpu().numpy(), bmap)
+    o = sla.sparse_attention(qd, kd, vd, keep, blk)
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk, blk_k=blk)
+    assert_close_absmax(got, ref, what=f"sla blk={blk}")
+
+
+def test_sparse_tiles_queued_matches_static(gpu):
+    """The tile kernel through the per-XCD work queues (enough pairs for a persistent grid) equals
+    the statically dispatched launch bit for bit, and the masked oracle on one head."""
+    rng = np.random.default_rng(5)
+    S, H, blk = 8192, 40, 32  # 2560 pairs of 64-row sub-blocks: four rounds or more on 256 CUs
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q, k, v = (torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    nk = S // blk
+    bmap_np = (rng.random((1, H, nk, nk)) < 0.2).astype(np.uint8)
+    tlut, tcnt = ops.block_map_to_tile_lut(torch.from_numpy(bmap_np).to(gpu), blk, blk, S, S)
+    assert ops.tiles_workspace_bytes(1, H, S, S, tlut.shape[3]) > 0  # the queued path runs
+    a = ops.attn_fwd_blocksparse_tiles(q, k, v, tlut, tcnt, queues=True)
+    b = ops.attn_fwd_blocksparse_tiles(q, k, v, tlut, tcnt, queues=False)
+    assert torch.equal(a, b)
+    h, rows = 7, 128  # the oracle on the first 128 query rows of one head
+    qh = from_dev_bf16(q[:, h:h + 1, :rows])
+    kh, vh = (from_dev_bf16(t[:, h:h + 1]) for t in (k, v))
+    ref = oracle.attn_fwd(qh, kh, vh, block_map=bmap_np[:, h:h + 1, :rows // blk], blk_q=blk, blk_k=blk)
+    got = oracle.bf16_to_f32(from_dev_bf16(a[:, h:h + 1, :rows])).reshape(ref.shape)
+    assert_close_absmax(got, ref, what="tiles queued")

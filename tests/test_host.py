@@ -247,9 +247,11 @@ def test_sla_override_scope_schedule_and_fallback():
 
 
 def test_sla_block_size_checked_at_construction():
-    """Unsupported block sizes fail when the schedule/override is built (as the node fails at
-    patch time, custom_nodes/h3_sla/__init__.py:331), not by silently running dense later."""
-    for blk in (16, 32, 48, 80, 96, 112, 144, 160, 176, 208, 224, 240, 0, 512):
+    """Every size the node offers (16..256 step 16, custom_nodes/h3_sla/__init__.py:315) is accepted;
+    others fail when the schedule/override is built (as the node fails at patch time, h3_sla:331),
+    not by silently running dense later."""
+    assert sla.SUPPORTED_BLOCKS == tuple(range(16, 257, 16))
+    for blk in (0, 8, 24, 100, 272, 512, -64):
         with pytest.raises(ValueError, match="block size"):
             hooks.Schedule("custom", [0.5] * 50, blk=blk)
         with pytest.raises(ValueError, match="block size"):
@@ -398,7 +400,7 @@ def test_patch_model_disabled_and_bad_arguments(monkeypatch):
     with pytest.raises(ValueError, match="preset"):
         hooks.patch_model(mp, preset="fastest")
     with pytest.raises(ValueError, match="block size"):
-        hooks.patch_model(mp, blk=48)
+        hooks.patch_model(mp, blk=40)
     assert mp.model_options == {"transformer_options": {}}
 
 
