@@ -365,6 +365,7 @@ def run_sparse(args, torch, h3attn, dev):
         "kept_fraction": round(flops / flops_per_layer(), 4),
         "dense_equivalent_tflops": round(flops_per_layer() / (avg_kernel_ms * 1e-3) / 1e12, 1),
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
+        "block_map_pooled_in_prologue": fused_pool_cost(torch, h3attn, dev, blk),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
@@ -382,6 +383,40 @@ def run_sparse(args, torch, h3attn, dev):
         res["roofline"]["peak_at_measured_clock"] = round(peak_at_clock, 1)
         res["roofline"]["frac_at_measured_clock"] = round(achieved / peak_at_clock, 4)
     return res
+
+
+def fused_pool_cost(torch, h3attn, dev, blk, reps=10):
+    """Block-map cost when the prologue pools (h3a_qk_rmsnorm_rope_pool), at H=56, S=42120: median
+    ms of the prologue alone, of the prologue with pooling at `blk`, and of the selection from
+    those means (top 25 % + diagonal), each over `reps` launches on fused [S,3HD] views."""
+    from h3attn import ops, sla
+    qkv, qw, kw = _prologue_inputs(torch, dev, S, H, 11)
+    rope = h3attn.rope_freqs(S, 128, device=dev)
+    q = qkv[:, :H * D].view(1, S, H, D)
+    k = qkv[:, H * D:2 * H * D].view(1, S, H, D)
+    nk = (S + blk - 1) // blk
+
+    def med(fn):
+        ms = []
+        for _ in range(reps + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            out = fn()
+            b.record()
+            torch.cuda.synchronize()
+            ms.append(a.elapsed_time(b))
+        return sorted(ms[1:])[len(ms[1:]) // 2], out
+
+    plain, _ = med(lambda: ops.qk_rmsnorm_rope_(q, k, rope, qw, kw, rot_dim=128))
+    pooled, (pq, pk) = med(lambda: ops.qk_rmsnorm_rope_(q, k, rope, qw, kw, rot_dim=128, pool_blk=blk))
+    select, _ = med(lambda: ops.block_select(pq, pk, sla.keep_count(0.25, nk), blk, blk, force_diag=True,
+                                             want_map=blk not in ops.NATIVE_BLOCKS))
+    del qkv
+    return {"prologue_ms": round(plain, 3), "prologue_pool_ms": round(pooled, 3),
+            "block_select_ms": round(select, 3),
+            "block_map_fused_ms": round(pooled - plain + select, 3),
+            "note": "prologue (qk-RMSNorm+RoPE) at H=56, S=42120 alone and with the block pooling fused in; "
+                    "block_map_fused_ms = the pooling's extra prologue time + the selection"}
 
 
 def _prologue_inputs(torch, dev, s_len, heads, seed):

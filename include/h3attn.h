@@ -288,6 +288,23 @@ int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D,
                         int rot_dim, const void *qw, const void *kw, float eps,
                         h3a_stream_t stream);
 
+/*
+ * h3a_qk_rmsnorm_rope with SLA's block pooling fused in: the same in-place
+ * update of q and k, and the fp32 means of the stored (bf16) q and k over
+ * blocks of blk tokens, q_means / k_means [B,H,ceil(S/blk),128] contiguous
+ * (the last block's mean over its valid tokens), equal bit for bit to
+ * h3a_block_pool on the updated q and k.  For a layer whose attention is
+ * block-sparse: the pooling step of SLA's get_block_map
+ * (custom_nodes/h3_sla/__init__.py:232) then needs no second pass over q and
+ * k.  No counterpart in the reference's code.  blk > 0; other arguments and
+ * errors as h3a_qk_rmsnorm_rope.
+ */
+int h3a_qk_rmsnorm_rope_pool(void *q, void *k, int B, int S, int H, int D,
+                             const int64_t q_strides[3], const int64_t k_strides[3],
+                             const float *rope, int64_t rope_sb, int64_t rope_ss,
+                             int rot_dim, const void *qw, const void *kw, float eps,
+                             int blk, float *q_means, float *k_means, h3a_stream_t stream);
+
 /* Kernel identifiers for h3a_kernel_attrs. */
 #define H3A_KERNEL_ATTN_DENSE      0
 #define H3A_KERNEL_ATTN_SPARSE_128 1

@@ -465,11 +465,12 @@ int h3a_block_select(const float *pq, const float *pk, int B, int H, int nq, int
                              max_k_blocks, block_map, as_stream(stream));
 }
 
-int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D, const int64_t q_strides[3],
-                        const int64_t k_strides[3], const float *rope, int64_t rope_sb,
-                        int64_t rope_ss, int rot_dim, const void *qw, const void *kw, float eps,
-                        h3a_stream_t stream) {
-  clear_error();
+namespace {
+
+// Checks shared by the prologue entry points; fills `a` on success.
+int prepare_rope(RopeArgs &a, void *q, void *k, int B, int S, int H, int D, const int64_t q_strides[3],
+                 const int64_t k_strides[3], const float *rope, int64_t rope_sb, int64_t rope_ss, int rot_dim,
+                 const void *qw, const void *kw, float eps) {
   if (!q || !k || !qw || !kw) return fail(H3A_ERR_INVALID_ARG, "null tensor pointer");
   if (!q_strides || !k_strides) return fail(H3A_ERR_INVALID_ARG, "null stride array");
   if (B <= 0 || S <= 0 || H <= 0)
@@ -488,7 +489,6 @@ int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D, const int6
   const int64_t rows = (int64_t)B * S * H;
   const int64_t items = (int64_t)B * S * ((H + 15) / 16);  // (token, 16-head chunk) work items
   if ((items + 3) / 4 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many tokens");
-  RopeArgs a;
   a.q = static_cast<uint16_t *>(q);
   a.k = static_cast<uint16_t *>(k);
   a.qsb = q_strides[0]; a.qss = q_strides[1]; a.qsh = q_strides[2];
@@ -499,7 +499,38 @@ int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D, const int6
   a.kw = static_cast<const uint16_t *>(kw);
   a.eps = eps;
   a.rows = rows;
+  return H3A_OK;
+}
+
+}  // namespace
+
+int h3a_qk_rmsnorm_rope(void *q, void *k, int B, int S, int H, int D, const int64_t q_strides[3],
+                        const int64_t k_strides[3], const float *rope, int64_t rope_sb,
+                        int64_t rope_ss, int rot_dim, const void *qw, const void *kw, float eps,
+                        h3a_stream_t stream) {
+  clear_error();
+  RopeArgs a;
+  const int rc = prepare_rope(a, q, k, B, S, H, D, q_strides, k_strides, rope, rope_sb, rope_ss, rot_dim, qw, kw,
+                              eps);
+  if (rc) return rc;
   return launch_qk_rmsnorm_rope(a, as_stream(stream));
+}
+
+int h3a_qk_rmsnorm_rope_pool(void *q, void *k, int B, int S, int H, int D, const int64_t q_strides[3],
+                             const int64_t k_strides[3], const float *rope, int64_t rope_sb, int64_t rope_ss,
+                             int rot_dim, const void *qw, const void *kw, float eps, int blk, float *q_means,
+                             float *k_means, h3a_stream_t stream) {
+  clear_error();
+  RopeArgs a;
+  const int rc = prepare_rope(a, q, k, B, S, H, D, q_strides, k_strides, rope, rope_sb, rope_ss, rot_dim, qw, kw,
+                              eps);
+  if (rc) return rc;
+  if (!q_means || !k_means) return fail(H3A_ERR_INVALID_ARG, "null block-mean pointer");
+  if (!aligned16(q_means) || !aligned16(k_means)) return fail(H3A_ERR_ALIGNMENT, "block means must be 16-byte aligned");
+  if (blk <= 0) return fail(H3A_ERR_INVALID_ARG, "blk %d must be positive", blk);
+  const int64_t wgs = (int64_t)B * ((S + blk - 1) / blk) * ((H + 7) / 8);
+  if (wgs > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many blocks");
+  return launch_qk_rmsnorm_rope_pool(a, blk, q_means, k_means, as_stream(stream));
 }
 
 int h3a_kernel_attrs(int which, double out[6]) {

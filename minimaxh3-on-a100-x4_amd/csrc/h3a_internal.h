@@ -116,6 +116,9 @@ struct RopeArgs {
   int64_t rows;  // B*S*H
 };
 int launch_qk_rmsnorm_rope(const RopeArgs &a, hipStream_t s);
+// The same with the block means of the stored q and k (blocks of blk tokens)
+// written to pq, pk [B,H,ceil(S/blk),128] fp32.
+int launch_qk_rmsnorm_rope_pool(const RopeArgs &a, int blk, float *pq, float *pk, hipStream_t s);
 int rope_kernel_attrs(double out[6]);
 
 }  // namespace h3a

@@ -67,6 +67,8 @@ SIGNATURES = {
     "h3a_block_map_to_lut": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
     "h3a_qk_rmsnorm_rope": (_i, [_vp, _vp, _i, _i, _i, _i, _c_i64_3, _c_i64_3,
                                  _vp, _i64, _i64, _i, _vp, _vp, _f, _vp]),
+    "h3a_qk_rmsnorm_rope_pool": (_i, [_vp, _vp, _i, _i, _i, _i, _c_i64_3, _c_i64_3,
+                                      _vp, _i64, _i64, _i, _vp, _vp, _f, _i, _vp, _vp, _vp]),
     "h3a_block_pool": (_i, [_vp, _i, _i, _i, _i, _c_i64_3, _i, _vp, _vp]),
     "h3a_block_select": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp]),
     "h3a_kernel_attrs": (_i, [_i, ctypes.POINTER(ctypes.c_double)]),

@@ -200,11 +200,15 @@ class Schedule:
         """Mean sparse-attention ms per call for each layer (None where it never ran)."""
         return [round(m / n, 3) if n else None for m, n in zip(self.attn_ms, self.attn_n)]
 
-    def _sparse(self, q, k, v, keep):
-        return sla.sparse_attention(q, k, v, keep, self.blk, force_diag=self.force_diag, smooth_k=self.smooth_k)
+    def _sparse(self, q, k, v, keep, pooled=None):
+        return sla.sparse_attention(q, k, v, keep, self.blk, force_diag=self.force_diag, smooth_k=self.smooth_k,
+                                    pooled=pooled)
 
-    def run(self, layer, q, k, v, transformer_options=None):
-        """[1,H,S,D] sparse output, or None (keep >= 1: caller runs dense)."""
+    def run(self, layer, q, k, v, transformer_options=None, pooled=None):
+        """[1,H,S,D] sparse output, or None (keep >= 1: caller runs dense).
+
+        pooled: the layer's block means from the prologue, if it took them.
+        """
         if layer == 0:
             self.generation_start(transformer_options)
         keep = self.keep_for(layer)
@@ -215,11 +219,11 @@ class Schedule:
                 self.flush_timing()
             return None
         if not tracked:
-            return self._sparse(q, k, v, keep)
+            return self._sparse(q, k, v, keep, pooled)
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record()
-        o = self._sparse(q, k, v, keep)
+        o = self._sparse(q, k, v, keep, pooled)
         b.record()
         self._ev.append((layer, a, b))
         if last:
@@ -242,9 +246,14 @@ def make_sla_override(topk: float = 0.35, blk: int = 64, schedule: Schedule | No
     blk = sla.check_block(blk)
 
     def sparse(q, k, v, transformer_options):
+        pooled = _take_pooled(q, k, blk)
         if schedule is None:
-            return sla.sparse_attention(q, k, v, topk, blk)
-        return schedule.run(getattr(_state, "layer", None), q, k, v, transformer_options)
+            return sla.sparse_attention(q, k, v, topk, blk, pooled=pooled)
+        return schedule.run(getattr(_state, "layer", None), q, k, v, transformer_options, pooled=pooled)
+
+    def plan(layer):
+        """(keep, blk) this override applies to DiT layer `layer`."""
+        return (float(topk) if schedule is None else schedule.keep_for(layer)), blk
 
     def override(func, *args, **kwargs):
         if in_dit_scope() and _gate(args, kwargs):
@@ -260,7 +269,32 @@ def make_sla_override(topk: float = 0.35, blk: int = 64, schedule: Schedule | No
         return func(*args, **kwargs)
 
     override.h3sla = schedule
+    override.h3attn_plan = plan
     return override
+
+
+def _pool_blk_for(transformer_options):
+    """Block size at which the patched forward's prologue should also pool q and k: the active
+    override is an h3attn sparse override that will run this DiT layer block-sparse; else None."""
+    if not in_dit_scope():
+        return None
+    try:
+        plan = getattr((transformer_options or {}).get("optimized_attention_override"), "h3attn_plan", None)
+        if plan is None:
+            return None
+        keep, blk = plan(getattr(_state, "layer", None))
+        return blk if keep < 1.0 else None
+    except Exception:
+        return None
+
+
+def _take_pooled(q, k, blk):
+    """The block means the prologue left for this q, k and block size (consumed), or None."""
+    p = getattr(_state, "pooled", None)
+    _state.pooled = None
+    if p is None or p[0] != q.data_ptr() or p[1] != k.data_ptr() or p[2] != blk:
+        return None
+    return p[3], p[4]
 
 
 def _dit_blocks(model):
@@ -364,8 +398,15 @@ def make_attention_forward(orig_forward, prologue: Callable = ops.rms_rope_split
     With a `timer` (h3attn.profiling.OpTimer) the four sub-operations are
     timed under the reference profiler's component names
     (custom_nodes/h3_profiler/__init__.py:98-115) whenever the timer is armed.
+
+    When the HIP prologue runs and the transformer_options carry an h3attn
+    sparse override that will run this layer block-sparse, the prologue also
+    pools q and k at the override's block size (h3a_qk_rmsnorm_rope_pool) and
+    leaves the means for the override, so the block map does not read q and
+    k again.
     """
     mark = timer.mark if timer is not None else profiling.passthrough
+    fuse_pool = prologue is ops.rms_rope_split_half_
 
     def forward(self, x, rope_freqs=None, transformer_options={}):
         if rope_freqs is None:
@@ -377,8 +418,15 @@ def make_attention_forward(orig_forward, prologue: Callable = ops.rms_rope_split
         q = q.view(1, s, H, D)
         k = k.view(1, s, H, D)
         rot = rope_freqs.shape[-3] * 2
-        mark("attn.qknorm_rope", prologue, q, k, rope_freqs, _weight(self.q_norm.weight, x.device),
-             _weight(self.k_norm.weight, x.device), epsilon=self.q_norm.eps, rot_dim=rot)
+        qw, kw = _weight(self.q_norm.weight, x.device), _weight(self.k_norm.weight, x.device)
+        _state.pooled = None
+        pool_blk = _pool_blk_for(transformer_options) if fuse_pool else None
+        if pool_blk is None:
+            mark("attn.qknorm_rope", prologue, q, k, rope_freqs, qw, kw, epsilon=self.q_norm.eps, rot_dim=rot)
+        else:
+            pq, pk = mark("attn.qknorm_rope", ops.qk_rmsnorm_rope_, q, k, rope_freqs, qw, kw,
+                          eps=self.q_norm.eps, rot_dim=rot, pool_blk=pool_blk)
+            _state.pooled = (q.data_ptr(), k.data_ptr(), pool_blk, pq, pk)
         qh = q.transpose(1, 2)
         kh = k.transpose(1, 2)
         vh = v.view(1, s, H, D).transpose(1, 2)

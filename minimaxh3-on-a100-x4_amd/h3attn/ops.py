@@ -423,12 +423,16 @@ def _rope_table(rope: torch.Tensor, B: int, S: int, rot_dim: int):
 
 
 def qk_rmsnorm_rope_(q: torch.Tensor, k: torch.Tensor, rope: torch.Tensor | None, qw: torch.Tensor,
-                     kw: torch.Tensor, eps: float = 1e-6, rot_dim: int | None = None) -> None:
+                     kw: torch.Tensor, eps: float = 1e-6, rot_dim: int | None = None,
+                     pool_blk: int | None = None):
     """In-place per-head RMSNorm (weights qw/kw over head_dim) + split-half RoPE on q, k [B,S,H,128].
 
     q and k are typically strided views of the fused QKV projection output.
     The rotation for frequency i < rot_dim/2 is rope[..., s, i, :, :] applied to
-    the pair (x[i], x[i + rot_dim/2]).
+    the pair (x[i], x[i + rot_dim/2]).  Returns None; with pool_blk, also pools
+    the result in the same pass (h3a_qk_rmsnorm_rope_pool) and returns the fp32
+    block means (q_means, k_means) [B,H,ceil(S/pool_blk),128], equal to
+    block_pool of the updated q and k (as [B,H,S,128]).
     """
     for name, t in (("q", q), ("k", k)):
         if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 4 or t.shape[-1] != HEAD_DIM:
@@ -455,12 +459,20 @@ def qk_rmsnorm_rope_(q: torch.Tensor, k: torch.Tensor, rope: torch.Tensor | None
         rptr = rope.data_ptr()
     else:
         rptr, rsb, rss = None, 0, 0
-    rc = lib().h3a_qk_rmsnorm_rope(
-        q.data_ptr(), k.data_ptr(), B, S, H, D,
-        strides3(_norm_stride(q, 0), _norm_stride(q, 1), _norm_stride(q, 2)),
-        strides3(_norm_stride(k, 0), _norm_stride(k, 1), _norm_stride(k, 2)),
-        rptr, int(rsb), int(rss), rot_dim, ws[0].data_ptr(), ws[1].data_ptr(), float(eps), _stream(q))
-    check("h3a_qk_rmsnorm_rope", rc)
+    args = (q.data_ptr(), k.data_ptr(), B, S, H, D,
+            strides3(_norm_stride(q, 0), _norm_stride(q, 1), _norm_stride(q, 2)),
+            strides3(_norm_stride(k, 0), _norm_stride(k, 1), _norm_stride(k, 2)),
+            rptr, int(rsb), int(rss), rot_dim, ws[0].data_ptr(), ws[1].data_ptr(), float(eps))
+    if pool_blk is None:
+        check("h3a_qk_rmsnorm_rope", lib().h3a_qk_rmsnorm_rope(*args, _stream(q)))
+        return None
+    blk = int(pool_blk)
+    if blk <= 0:
+        raise ValueError(f"pool_blk {pool_blk} must be positive")
+    means = torch.empty((2, B, H, -(-S // blk), D), dtype=torch.float32, device=q.device)
+    check("h3a_qk_rmsnorm_rope_pool",
+          lib().h3a_qk_rmsnorm_rope_pool(*args, blk, means[0].data_ptr(), means[1].data_ptr(), _stream(q)))
+    return means[0], means[1]
 
 
 def rms_rope_split_half_(q, k, rope_freqs, qw, kw, epsilon: float = 1e-6, rot_dim: int | None = None):

@@ -149,7 +149,7 @@ def keep_count(topk_ratio: float, nk: int) -> int:
 
 
 def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int = 64, BLKK: int = 64,
-                  force_diag: bool = False, smooth_k: bool = True, want_map: bool = True):
+                  force_diag: bool = False, smooth_k: bool = True, want_map: bool = True, pooled=None):
     """Block map from mean-pooled scores -> (block_map uint8 [B,H,nq,nk] or None, lut int32, counts int32).
 
     Defaults follow SLA's get_block_map as the h3_sla node calls it
@@ -159,29 +159,40 @@ def get_block_map(q: torch.Tensor, k: torch.Tensor, topk_ratio: float, BLKQ: int
     amount and cannot change which key blocks are kept, so the selection is
     computed without it.  The H3 block-sparse workload (128x128 tiles, top 25 %) uses
     force_diag=True.  Pooling and selection run in libh3attn; ties are broken
-    towards the lower key-block index.
+    towards the lower key-block index.  `pooled`: the block means (pq, pk)
+    already taken, by the prologue that wrote q and k
+    (ops.qk_rmsnorm_rope_(..., pool_blk=...)); then q and k are not read again.
     """
     del smooth_k  # selection-invariant, see above
     BLKQ, BLKK = check_block(BLKQ), check_block(BLKK)
-    pq = ops.block_pool(q, BLKQ)
-    pk = ops.block_pool(k, BLKK)
+    if pooled is not None:
+        pq, pk = pooled
+        want_q = (q.shape[0], q.shape[1], -(-q.shape[2] // BLKQ), q.shape[3])
+        want_k = (k.shape[0], k.shape[1], -(-k.shape[2] // BLKK), k.shape[3])
+        if tuple(pq.shape) != want_q or tuple(pk.shape) != want_k:
+            raise ValueError(f"pooled means {tuple(pq.shape)}, {tuple(pk.shape)} do not match q/k at "
+                             f"blocks {BLKQ}, {BLKK}")
+    else:
+        pq = ops.block_pool(q, BLKQ)
+        pk = ops.block_pool(k, BLKK)
     kc = keep_count(topk_ratio, pk.shape[2])
     return ops.block_select(pq, pk, kc, BLKQ, BLKK, force_diag=force_diag, want_map=want_map)
 
 
 def sparse_attention(q, k, v, topk_ratio: float, blk: int = 64, force_diag: bool = False,
-                     smooth_k: bool = True):
+                     smooth_k: bool = True, pooled=None):
     """[1,H,S,D] -> [1,H,S,D] block-sparse attention (SLA sparse branch only; h3_sla:226-235).
 
     Native block sizes run on the block LUT; the others on the tile LUT
-    built from the block map.
+    built from the block map.  `pooled`: block means from the prologue (see
+    get_block_map).
     """
     blk = check_block(blk)
     out_dtype = q.dtype
     q16, k16, v16 = (t.to(torch.bfloat16) for t in (q, k, v))
     native = blk in ops.NATIVE_BLOCKS
     bmap, lut, counts = get_block_map(q16, k16, topk_ratio, blk, blk, force_diag=force_diag,
-                                      smooth_k=smooth_k, want_map=not native)
+                                      smooth_k=smooth_k, want_map=not native, pooled=pooled)
     if native:
         o = ops.attn_fwd_blocksparse(q16, k16, v16, lut, counts, blk, blk)
     else:

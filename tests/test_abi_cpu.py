@@ -134,6 +134,15 @@ def test_lut_and_prologue_argument_errors():
     assert rope(eps=-1.0) == _lib.H3A_ERR_INVALID_ARG
     assert rope(qs=(0, 3, 0)) == _lib.H3A_ERR_ALIGNMENT
     assert rope(rss=6) == _lib.H3A_ERR_ALIGNMENT
+    pool = L.h3a_qk_rmsnorm_rope_pool
+    assert pool(16, 16, 1, 4, 2, 128, z, z, 16, 0, 64, 128, 16, 16, 1e-6, 64, None, 16, None) == \
+        _lib.H3A_ERR_INVALID_ARG
+    assert pool(16, 16, 1, 4, 2, 128, z, z, 16, 0, 64, 128, 16, 16, 1e-6, 0, 16, 16, None) == \
+        _lib.H3A_ERR_INVALID_ARG
+    assert pool(16, 16, 1, 4, 2, 128, z, z, 16, 0, 64, 128, 16, 16, 1e-6, 64, 16, 20, None) == \
+        _lib.H3A_ERR_ALIGNMENT
+    assert pool(16, 16, 1, 4, 2, 64, z, z, 16, 0, 64, 128, 16, 16, 1e-6, 64, 16, 16, None) == \
+        _lib.H3A_ERR_UNSUPPORTED
     assert L.h3a_block_pool(None, 1, 1, 10, 128, z, 64, 16, None) == _lib.H3A_ERR_INVALID_ARG
     assert L.h3a_block_pool(16, 1, 1, 10, 64, z, 64, 16, None) == _lib.H3A_ERR_UNSUPPORTED
     assert L.h3a_block_pool(16, 1, 1, 10, 128, z, 0, 16, None) == _lib.H3A_ERR_INVALID_ARG

@@ -11,7 +11,7 @@ import h3attn
 import standin_dit
 import oracle
 from conftest import assert_close_absmax, from_dev_bf16
-from h3attn import hooks, sla
+from h3attn import hooks, ops, sla
 
 pytestmark = pytest.mark.gpu
 
@@ -162,3 +162,50 @@ def test_patched_model_runs_scheduled_keeps_against_masked_oracle(gpu, monkeypat
                                                                      force_diag=False), blk_q=64, blk_k=64)
         with pytest.raises(AssertionError):
             assert_close_absmax(got, wrong, what="the other layer's keep")
+
+
+def test_sparse_layers_take_block_means_from_the_prologue(gpu, monkeypatch):
+    """With the HIP forward installed and an h3attn sparse override, a sparse layer's prologue pools
+    q and k (h3a_qk_rmsnorm_rope_pool) and the override uses those means instead of pooling again;
+    dense layers (keep 1) do not pool.  The model output equals that of the same run with the
+    pooling left to the block map (the means are equal bit for bit, so is the selection)."""
+    class A(standin_dit.Attention):
+        pass
+
+    torch.manual_seed(3)
+    dm = standin_dit.MiniMaxH3Model(512, 4, depth=4, attention_cls=A, dtype=torch.bfloat16, device=gpu)
+    with torch.no_grad():
+        for blk in dm.blocks:
+            blk.attn.qkv_proj.weight.normal_(0, 512 ** -0.5)
+            blk.attn.out_proj.weight.normal_(0, 0.1 * 512 ** -0.5)
+    mp = standin_dit.ModelPatcher(dm)
+    S = 900
+    x = torch.randn(S, 512, device=gpu, dtype=torch.bfloat16)
+    rope = h3attn.rope_freqs(S, 128, device=gpu)
+    real = sla.sparse_attention
+    seen = []
+
+    def spy(q, k, v, keep, blk, pooled=None, **kw):
+        seen.append((hooks._state.layer, pooled is not None))
+        return real(q, k, v, keep, blk, pooled=pooled, **kw)
+
+    monkeypatch.setattr(sla, "sparse_attention", spy)
+    pools = []
+    real_rope = ops.qk_rmsnorm_rope_
+    monkeypatch.setattr(ops, "qk_rmsnorm_rope_",
+                        lambda *a, **kw: pools.append(kw.get("pool_blk")) or real_rope(*a, **kw))
+    try:
+        assert hooks.install(A)
+        pm = hooks.patch_model(mp, topk=0.3, blk=64, preset="custom", layer_keep="100:2", log=lambda s: None)
+        with torch.no_grad():
+            fused = pm(x, rope)
+            torch.cuda.synchronize()
+            assert seen == [(0, True), (1, True), (3, True)] and pools == [64, 64, None, 64]
+            seen.clear()
+            monkeypatch.setattr(hooks, "_pool_blk_for", lambda opts: None)
+            plain = pm(x, rope)
+            torch.cuda.synchronize()
+    finally:
+        hooks.uninstall(A)
+    assert seen == [(0, False), (1, False), (3, False)]
+    assert torch.equal(fused, plain)

@@ -84,3 +84,34 @@ def test_prologue_rejects_bad_layout(gpu):
         h3attn.qk_rmsnorm_rope_(q[..., ::2], k[..., ::2], None, w[:64], w[:64], rot_dim=0)
     with pytest.raises(ValueError):
         h3attn.qk_rmsnorm_rope_(q, k, None, w, w, rot_dim=24)
+
+
+@pytest.mark.parametrize("S,H,blk,rot", [(8192, 56, 64, 128), (1000, 5, 16, 64), (777, 56, 200, 128),
+                                         (300, 12, 128, 0), (3, 2, 64, 128), (4100, 9, 48, 128)])
+def test_pooled_prologue_equals_prologue_then_block_pool(gpu, S, H, blk, rot):
+    """h3a_qk_rmsnorm_rope_pool on fused-QKV views: q and k equal h3a_qk_rmsnorm_rope's bit for bit,
+    the v part is untouched, and the block means equal block_pool of the result bit for bit (the
+    same sums in the same order), including a partial last block, blocks of fewer than 4 tokens
+    and head counts that leave a partial head chunk."""
+    from h3attn import ops
+    g = torch.Generator(device=gpu).manual_seed(S + H + blk)
+    qkv = torch.randn(S, 3 * H * 128, generator=g, device=gpu, dtype=torch.float32)
+    qkv[:, :2 * H * 128] *= torch.empty(S, 1, device=gpu).uniform_(0.5, 4.0, generator=g)
+    qkv = qkv.to(torch.bfloat16)
+    qw = (1 + 0.05 * torch.randn(128, generator=g, device=gpu)).to(torch.bfloat16)
+    kw = (1 + 0.05 * torch.randn(128, generator=g, device=gpu)).to(torch.bfloat16)
+    rope = h3attn.rope_freqs(S, rot, device=gpu) if rot else None
+
+    def views(t):
+        return t[:, :H * 128].view(1, S, H, 128), t[:, H * 128:2 * H * 128].view(1, S, H, 128)
+
+    a, b = qkv.clone(), qkv.clone()
+    h3attn.qk_rmsnorm_rope_(*views(a), rope, qw, kw, rot_dim=rot)
+    pq, pk = h3attn.qk_rmsnorm_rope_(*views(b), rope, qw, kw, rot_dim=rot, pool_blk=blk)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), "pooled prologue changed q/k differently (or touched v)"
+    assert torch.equal(b[:, 2 * H * 128:], qkv[:, 2 * H * 128:])
+    qh, kh = (t.transpose(1, 2) for t in views(b))
+    assert tuple(pq.shape) == (1, H, -(-S // blk), 128)
+    assert torch.equal(pq, ops.block_pool(qh, blk)), "q means differ from block_pool"
+    assert torch.equal(pk, ops.block_pool(kh, blk)), "k means differ from block_pool"
