@@ -922,7 +922,10 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // LDS operand reads issued ahead of a matrix cluster's first MFMA (then 2
   // after each MFMA), and the wave priority raised (s_setprio 1) during the
   // cluster: same-box sweeps chose 4 and no raise for the dense kernel, 6
-  // and the raise for the block-sparse ones.
+  // for the block-sparse ones, whose group B raises its priority during its
+  // matrix cluster while group A's cluster runs at the default: group B's
+  // cluster, which shares its slot with group A's softmax, otherwise ran
+  // ~15 % longer than group A's and bounded the stage.
   constexpr int kReadAhead = kSparse ? 6 : 4;
   constexpr int kReadsPerMfma = 2;
   constexpr bool kRaisePrio = kSparse;
@@ -1038,7 +1041,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     constexpr int NK = std::remove_reference_t<decltype(kseq)>::kCount;
     constexpr int NV = std::remove_reference_t<decltype(vseq)>::kCount;
     constexpr int NP = 4 * 2 * WS, NI = NK + NV;  // PV MFMAs, DMA instructions
-    if (kRaisePrio) __builtin_amdgcn_s_setprio(1);
+    if (kRaisePrio && !lead) __builtin_amdgcn_s_setprio(1);
     score_tile<L, WS>(kbuf[P ^ 1], qf, k_rd, s);
     pv_tile<L, 2 * WS>(vbuf[P], pf, v_rd, o, [&](int t) __attribute__((always_inline)) {
 #pragma unroll

@@ -16,7 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("H3ATTN_LIB", os.path.join(_HERE, "libh3attn.so"))
 # The phase-profile build of the same sources (H3A_PROFILE=1): its dense kernel
 # stamps the shader clock at cluster boundaries (h3a_prof_read).
-PROF_LIB_PATH = os.path.join(_HERE, "libh3attn_prof.so")
+PROF_LIB_PATH = os.environ.get("H3ATTN_PROF_LIB", os.path.join(_HERE, "libh3attn_prof.so"))
 
 H3A_OK = 0
 H3A_ERR_INVALID_ARG = 1
