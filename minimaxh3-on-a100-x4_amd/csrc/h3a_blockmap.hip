@@ -7,8 +7,8 @@
 //   block_pool_kernel   : bf16 [B,H,S,128] (strided) -> fp32 block means
 //                         [B,H,ceil(S/blk),128], over the valid rows of each
 //                         block.  HBM-bound: reads the tensor once.
-//   block_select_kernel : up to 8 query blocks of one (b,h) per workgroup:
-//                         scores against all key blocks into LDS, rank by
+//   block_select_kernel : up to 16 query blocks of one (b,h) per workgroup:
+//                         scores against all key blocks (fp32 MFMA) into LDS, rank by
 //                         (score desc, index asc), keep rank < keep plus the
 //                         optional diagonal, and write the kept indices in
 //                         ascending order (the LUT h3a_attn_fwd_blocksparse
@@ -16,10 +16,10 @@
 // Centring k by its sequence mean (SLA's K smoothing) shifts every score of a
 // row by the same amount, so it never changes the selection and is not needed.
 #include <type_traits>
-#include <utility>
 
 #include "h3a_device.h"
 #include "h3a_internal.h"
+#include "h3a_queue.h"
 
 namespace h3a {
 
@@ -64,54 +64,28 @@ __global__ void __launch_bounds__(256) block_pool_kernel(const uint16_t *x, int6
 constexpr int kSelThreads = 256;
 constexpr int kSelRowsPerWave = 4;
 constexpr int kSelRowsMax = kSelRowsPerWave * (kSelThreads / 64);  // query blocks per workgroup
-constexpr int kSelKeyChunk = 64;         // pooled key vectors staged in LDS at a time (one per lane)
-constexpr int kSelKeyPitch = kPoolD + 4; // floats per staged key row (bank spread)
-constexpr int kSelChunkBytes = kSelKeyChunk * kSelKeyPitch * 4;
-// LDS per workgroup (two fit on a CU): the key chunk, then the score rows.
-constexpr int kSelLdsBytes = 81920;
-constexpr int kSelScoreBytes = kSelLdsBytes - kSelChunkBytes;
+// LDS per workgroup caps the score rows (R rows of nk floats, plus one spare
+// float) at 40 KiB, so that four workgroups fit on a CU: 16 rows up to
+// nk = 639, 15 at 659, 10 at 1000, 1 at the 7000 maximum.
+constexpr int kSelScoreBytes = 40960 - 4;
+constexpr int kSelKeyTile = 16;  // key blocks per score tile (one MFMA output tile)
 
-// acc += q_J * k with q_J = lane J of q's 16-lane row (DPP row_newbcast:J on
-// src0).  As inline asm because the compiler keeps the broadcast as a separate
-// v_mov_b32_dpp.  q is written by loads only (never by a VALU instruction just
-// before), so the VALU-write / DPP-read hazard does not arise.
-template <int J>
-__device__ __forceinline__ float fmac_bcast(float acc, float q, float k) {
-  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-      : "+v"(acc)
-      : "v"(q), "v"(k), "i"(J));
-  return acc;
-}
-// Four query rows' dot products with one key vector (lane l: key block
-// kc + l), advanced over dim D.  Register qv[i][m] of lane l holds
-// q_i[16m + l%16], so row_newbcast:(D%16) on qv[i][D/16] gives every lane
-// q_i[D]: one FMA per (row, dim), in the order d = 0..127.
-template <int D>
-__device__ __forceinline__ void score_dim(float (&acc)[4], const float (&qv)[4][kPoolD / 16], float k) {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Dims of step m = 4j + t of the score MFMAs, for k-slot s (lane / 16):
+// 16j + 4s + t, so each lane's operands for steps 4j..4j+3 are one 16-byte
+// load and the 32 steps cover d = 0..127 once.
+__device__ __forceinline__ void load_score_operand(f32x4 (&x)[8], const float *row, int slot) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = fmac_bcast<D & 15>(acc[i], qv[i][D >> 4], k);
-}
-template <int D4>
-__device__ __forceinline__ void score_dims(float (&acc)[4], const float (&qv)[4][kPoolD / 16],
-                                           const float *kr) {
-  const float4 k4 = *(const float4 *)(kr + 4 * D4);
-  score_dim<4 * D4 + 0>(acc, qv, k4.x);
-  score_dim<4 * D4 + 1>(acc, qv, k4.y);
-  score_dim<4 * D4 + 2>(acc, qv, k4.z);
-  score_dim<4 * D4 + 3>(acc, qv, k4.w);
-}
-template <int... D4>
-__device__ __forceinline__ void score_key(float (&acc)[4], const float (&qv)[4][kPoolD / 16],
-                                          const float *kr, std::integer_sequence<int, D4...>) {
-  (score_dims<D4>(acc, qv, kr), ...);
+  for (int j = 0; j < 8; ++j) x[j] = *(const f32x4 *)(row + 16 * j + 4 * slot);
 }
 
-// R (<= kSelRowsMax) query blocks of one (b,h) per workgroup, so each pooled
-// key vector is read from memory once per R rows.  Scores: lane l of every
-// wave takes key block kc + l of a 64-block chunk staged in LDS, and wave w
-// takes query rows w, w+4, w+8, w+12, held in registers across the DPP rows;
-// each dot product is the plain fp32 FMA chain over d = 0..127.
-// The R score rows go to LDS.  Then wave
+// R (<= kSelRowsMax = 16) query blocks of one (b,h) per workgroup, so each
+// pooled key vector is read from memory once per R rows.  Scores: the 16
+// rows x 16 key blocks of a tile are one chain of 32 v_mfma_f32_16x16x4f32
+// (fp32 products and sums); wave w takes key tiles w, w+4, ..., its pooled
+// keys loaded straight into registers one tile ahead, and writes the tile's
+// scores to LDS.  Then wave
 // w selects rows w, w+4, ..., with lane l on key blocks j = 64c + l: a bitwise
 // search over order-preserving keys finds the row's keep-th largest score in
 // 32 counting rounds (ballot + popcount), which fixes the kept set under
@@ -120,60 +94,57 @@ __device__ __forceinline__ void score_key(float (&acc)[4], const float (&qv)[4][
 __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     const float *pq, const float *pk, int nq, int nk, int rows_per_wg, int keep, int force_diag,
     int blk_q, int blk_k, int32_t *lut, int32_t *counts, int max_k, uint8_t *map) {
-  extern __shared__ float sel_lds[];
-  float *ks = sel_lds;                                   // [kSelKeyChunk][kSelKeyPitch] key chunk
-  float *sc = ks + kSelKeyChunk * kSelKeyPitch;          // [R][nk] scores
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  extern __shared__ float sc[];  // [R][nk] scores, then one spare slot
+  // The wave index as a scalar, so the loops over a wave's tiles and rows are uniform.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R = rows_per_wg;
   const int ngroups = (nq + R - 1) / R;
-  const int64_t bh = blockIdx.x / ngroups;
-  const int i0 = (int)(blockIdx.x % ngroups) * R;
+  // Consecutive row groups (those of one head) run on one XCD, so that head's
+  // pooled keys come from that XCD's L2 after the first group reads them.
+  const int g = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int64_t bh = g / ngroups;
+  const int i0 = (g % ngroups) * R;
   const int nrows = nq - i0 < R ? nq - i0 : R;
-  // This wave's query rows, clamped to a valid row (results past nrows are
-  // not stored), as score_dims wants them.
-  static_assert(kSelRowsPerWave == 4, "score_dims takes four rows");
-  float qv[kSelRowsPerWave][kPoolD / 16];
-#pragma unroll
-  for (int i = 0; i < kSelRowsPerWave; ++i) {
-    const int r = wave + 4 * i < nrows ? wave + 4 * i : nrows - 1;
-    const float *qp = pq + (bh * nq + i0 + r) * kPoolD + (lane & 15);
-#pragma unroll
-    for (int m = 0; m < kPoolD / 16; ++m) qv[i][m] = qp[16 * m];
-  }
-  // Key chunks go through registers with coalesced 16-byte loads, the next
-  // chunk's loads in flight while the current one is scored.  Rows past nk
-  // repeat the last key block (the chunk after the last one too); their
-  // scores are never stored.
+  // MFMA operands: lane l supplies A[row l%16][slot l/16] (query rows, past
+  // nrows clamped to the last one; their scores are not stored) and
+  // B[slot l/16][key l%16]; lane l's results are rows 4*(l/16) + v, v = 0..3,
+  // of key l%16.
+  static_assert(kSelRowsMax == 16, "one MFMA tile spans the workgroup's rows");
+  const int lr = lane & 15, slot = lane >> 4;
+  f32x4 qa[8];
+  load_score_operand(qa, pq + (bh * nq + i0 + (lr < nrows ? lr : nrows - 1)) * kPoolD, slot);
   const float *pkh = pk + bh * (int64_t)nk * kPoolD;
-  constexpr int kStage = kSelKeyChunk * (kPoolD / 4) / kSelThreads;  // float4 per thread per chunk
-  const int st_kk = tid / (kPoolD / 4), st_f4 = tid % (kPoolD / 4);
-  constexpr int kRowsPerPass = kSelThreads / (kPoolD / 4);
-  typedef float f32x4 __attribute__((ext_vector_type(4)));  // (HIP's float4 struct stays in scratch here)
-  f32x4 pre[kStage];
+  const int ntiles = (nk + kSelKeyTile - 1) / kSelKeyTile;
+  // Key rows past nk repeat the last key block (the tile after a wave's last
+  // one too); their scores are not stored.
+  auto key_row = [&](int t) __attribute__((always_inline)) {
+    const int j = t * kSelKeyTile + lr;
+    return pkh + (int64_t)(j < nk ? j : nk - 1) * kPoolD;
+  };
+  auto score_tile = [&](int t, const f32x4(&kb)[8]) __attribute__((always_inline)) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int u = 0; u < kStage; ++u) {
-    const int j = st_kk + u * kRowsPerPass < nk ? st_kk + u * kRowsPerPass : nk - 1;
-    pre[u] = *(const f32x4 *)(pkh + (int64_t)j * kPoolD + 4 * st_f4);
-  }
-  for (int kc = 0; kc < nk; kc += kSelKeyChunk) {
-    __syncthreads();  // previous chunk consumed
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int u = 0; u < kStage; ++u)
-      *(f32x4 *)(ks + (st_kk + u * kRowsPerPass) * kSelKeyPitch + 4 * st_f4) = pre[u];
-    __syncthreads();
+      for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[j][u], kb[j][u], acc, 0, 0, 0);
+    // Scores of rows past nrows or keys past nk go to the spare slot sc[R*nk]
+    // (no branches around the stores).
+    const int key = t * kSelKeyTile + lr;
 #pragma unroll
-    for (int u = 0; u < kStage; ++u) {
-      const int jn = kc + kSelKeyChunk + st_kk + u * kRowsPerPass;
-      pre[u] = *(const f32x4 *)(pkh + (int64_t)(jn < nk ? jn : nk - 1) * kPoolD + 4 * st_f4);
-    }
-    const float *kr = ks + lane * kSelKeyPitch;
-    float acc[kSelRowsPerWave];
-#pragma unroll
-    for (int i = 0; i < kSelRowsPerWave; ++i) acc[i] = 0.f;
-    score_key(acc, qv, kr, std::make_integer_sequence<int, kPoolD / 4>{});
-#pragma unroll
-    for (int i = 0; i < kSelRowsPerWave; ++i)
-      if (wave + 4 * i < nrows && kc + lane < nk) sc[(wave + 4 * i) * nk + kc + lane] = acc[i];
+    for (int v = 0; v < 4; ++v)
+      sc[4 * slot + v < nrows && key < nk ? (4 * slot + v) * nk + key : R * nk] = acc[v];
+  };
+  // Two key buffers, each loaded while the other one's tile is scored (the
+  // scheduling barriers keep the loads ahead of the MFMA chain they overlap).
+  f32x4 k0[8], k1[8];
+  load_score_operand(k0, key_row(wave < ntiles ? wave : ntiles - 1), slot);
+  for (int t = wave; t < ntiles; t += 8) {
+    load_score_operand(k1, key_row(t + 4 < ntiles ? t + 4 : ntiles - 1), slot);
+    __builtin_amdgcn_sched_barrier(0);
+    score_tile(t, k0);
+    load_score_operand(k0, key_row(t + 8 < ntiles ? t + 8 : ntiles - 1), slot);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t + 4 < ntiles) score_tile(t + 4, k1);
   }
   __syncthreads();
 
@@ -422,15 +393,7 @@ int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, 
                         int max_k, uint8_t *map, hipStream_t s) {
   int rows = kSelScoreBytes / (nk * (int)sizeof(float));
   rows = rows < 1 ? 1 : (rows > kSelRowsMax ? kSelRowsMax : rows);
-  const size_t lds = (size_t)kSelChunkBytes + (size_t)rows * nk * sizeof(float);
-  // Above 64 KiB of dynamic LDS the kernel is allowed the larger size first
-  // (on the current device; a host-side setting, no stream work).
-  if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&block_select_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kSelLdsBytes);
-    if (e != hipSuccess)
-      return fail(H3A_ERR_HIP, "block_select_kernel: %zu bytes of LDS refused: %s", lds, hipGetErrorString(e));
-  }
+  const size_t lds = ((size_t)rows * nk + 1) * sizeof(float);
   const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
   hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)groups), dim3(kSelThreads), lds, s, pq, pk, nq,
                      nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);

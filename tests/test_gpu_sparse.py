@@ -432,9 +432,10 @@ def test_block_select_exact_ties(gpu, nq, nk, keep, diag, max_k):
     """Integer pooled vectors make every score an exact fp32 integer, with many ties:
     the kept set, its order and the truncation to max_k_blocks must match exactly.
     Covers row groups of up to 16 query blocks per workgroup (fewer where the score
-    rows fill LDS: 15 at nk 769, 12 at nk 1000, 2 at nk 5000, 1 at the 7000 maximum)
-    and all three counting paths: keys held in 6 registers (nk <= 384), in 12
-    (nk <= 768), and re-read from LDS (769 and above)."""
+    rows fill LDS: 14 at nk 700, 13 at nk 769, 10 at nk 1000, 2 at nk 5000, 1 at the
+    7000 maximum; the score MFMAs' rows past a group's end are computed and dropped),
+    key tiles past nk (nk 65, 1, 769, 1000), and all three counting paths: keys held
+    in 6 registers (nk <= 384), in 12 (nk <= 768), and re-read from LDS (769 and above)."""
     rng = np.random.default_rng(50 + nq + nk)
     pq = rng.integers(-2, 3, (1, 2, nq, 128)).astype(np.float32)
     pk = rng.integers(-2, 3, (1, 2, nk, 128)).astype(np.float32)
