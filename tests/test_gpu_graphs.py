@@ -58,9 +58,9 @@ def test_graph_replay_matches_eager(gpu):
 
 
 def test_graph_capture_of_wide_block_select(gpu):
-    """Block select over 700 key blocks per row, where the kernel takes more than 64 KiB
-    of LDS and each call first raises its dynamic-LDS limit (a host-side setting):
-    captured into a graph, every replay equals the eager call."""
+    """Block select over 700 key blocks per row (44 score tiles per row, 14 query blocks
+    per workgroup, keys counted in 12 registers per lane): captured into a graph, every
+    replay equals the eager call."""
     g = torch.Generator(device=gpu).manual_seed(41)
     pq = torch.randn(1, 2, 20, 128, generator=g, device=gpu)
     pk = torch.randn(1, 2, 700, 128, generator=g, device=gpu)
