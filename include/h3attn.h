@@ -66,6 +66,9 @@ const char *h3a_last_error(void);
  * attn_sm80/fa3_sm80_h3.cu:405-420).  Sq != Skv is allowed (pad path,
  * harness/sp_runtime.py:106-109).  scale > 0 (1/sqrt(128) for the DiT).
  * The seq strides of k and v must be < 2^24 elements (H3A_ERR_UNSUPPORTED).
+ * With Sq > 1 the seq stride of o must be at least D, so that rows do not
+ * overlap (H3A_ERR_INVALID_ARG).  The seq stride of a length-1 sequence
+ * (Sq or Skv == 1) is ignored, as for any size-1 dimension: 0 is fine.
  * Range: the softmax runs against a stale reference max that is refreshed
  * once a stage's p values would exceed 2^16, so the unnormalised fp32 O is
  * bounded by 2^17 * ceil(Skv/64) * max|v|; results are finite for

@@ -39,6 +39,7 @@ int check_launch(const char *what) {
 namespace {
 
 constexpr int64_t kMaxSeqStride = int64_t(1) << 24;
+constexpr int64_t kRowElems = 128;  // elements of one q/k/v/o row (head_dim)
 
 bool strides_ok(const int64_t s[3]) {
   for (int i = 0; i < 3; ++i)
@@ -67,6 +68,11 @@ int check_attn(const void *q, const void *k, const void *v, void *o, int B, int 
   // less than 2 GiB.
   if (ks[2] >= kMaxSeqStride || vs[2] >= kMaxSeqStride)
     return fail(H3A_ERR_UNSUPPORTED, "k/v sequence stride must be < %lld elements", (long long)kMaxSeqStride);
+  // Output rows closer than one row apart would overlap.  (A length-1
+  // sequence has no second row: its stride is free, see fill_attn_args.)
+  if (Sq > 1 && os[2] < kRowElems)
+    return fail(H3A_ERR_INVALID_ARG, "o sequence stride %lld is less than a row (%lld elements): rows overlap",
+                (long long)os[2], (long long)kRowElems);
   return H3A_OK;
 }
 
@@ -118,6 +124,13 @@ void fill_attn_args(AttnArgs &a, const void *q, const void *k, const void *v, vo
   a.ksb = ks[0]; a.ksh = ks[1]; a.kss = ks[2];
   a.vsb = vs[0]; a.vsh = vs[1]; a.vss = vs[2];
   a.osb = os[0]; a.osh = os[1]; a.oss = os[2];
+  // The kernels step along the sequence past its end (whole 32-row O tiles,
+  // 64-row K/V stages) and rely on a buffer range to drop those rows, which
+  // takes a stride of at least one row.  A length-1 sequence's stride never
+  // reaches a valid row, so callers may pass anything there (0 for a size-1
+  // dimension, as torch views do): give it one row.
+  if (Sq == 1) a.qss = a.oss = kRowElems;
+  if (Skv == 1) a.kss = a.vss = kRowElems;
   a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv;
   a.sl2 = scale * 1.4426950408889634f;
   a.lut = nullptr; a.counts = nullptr; a.lut_stride = 0; a.sub = 1; a.blk_k = 64;

@@ -15,6 +15,7 @@ from h3attn import _lib
 
 HEADER = os.path.join(ROOT, "include", "h3attn.h")
 S3 = _lib.strides3
+ROW = S3(0, 0, 128)  # output strides with one row per step (o rows must not overlap)
 
 
 def header_symbols():
@@ -60,6 +61,11 @@ def test_attn_argument_errors():
     assert L.h3a_attn_fwd(16, 16, 16, 16, 1, 1, 4, 4, 128, z, big, z, z, 0.1, None) == _lib.H3A_ERR_UNSUPPORTED
     assert b"sequence stride" in L.h3a_last_error()
     assert L.h3a_attn_fwd(16, 16, 16, 16, 1, 1, 4, 4, 128, z, z, big, z, 0.1, None) == _lib.H3A_ERR_UNSUPPORTED
+    # Output rows less than one row apart overlap (a length-1 sequence's stride is free).
+    for oss in (0, 64, 120):
+        assert L.h3a_attn_fwd(16, 16, 16, 16, 1, 1, 4, 4, 128, z, z, z, S3(0, 0, oss), 0.1, None) == \
+            _lib.H3A_ERR_INVALID_ARG
+        assert b"rows overlap" in L.h3a_last_error()
 
 
 def test_blocksparse_argument_errors():
@@ -67,7 +73,7 @@ def test_blocksparse_argument_errors():
     z = S3(0, 0, 0)
 
     def call(lut=16, counts=16, bq=128, bk=128, maxk=1, Skv=300):
-        return L.h3a_attn_fwd_blocksparse(16, 16, 16, 16, 1, 1, 300, Skv, 128, z, z, z, z, lut, counts,
+        return L.h3a_attn_fwd_blocksparse(16, 16, 16, 16, 1, 1, 300, Skv, 128, z, z, z, ROW, lut, counts,
                                           bq, bk, maxk, 0.1, None)
 
     assert call(lut=None) == _lib.H3A_ERR_INVALID_ARG
@@ -87,7 +93,7 @@ def test_tile_entry_argument_errors():
     z = S3(0, 0, 0)
 
     def tiles(lut=16, counts=16, maxt=1, Skv=300, D=128):
-        return L.h3a_attn_fwd_blocksparse_tiles(16, 16, 16, 16, 1, 1, 300, Skv, D, z, z, z, z, lut, counts,
+        return L.h3a_attn_fwd_blocksparse_tiles(16, 16, 16, 16, 1, 1, 300, Skv, D, z, z, z, ROW, lut, counts,
                                                 maxt, 0.1, None)
 
     assert tiles(lut=None) == _lib.H3A_ERR_INVALID_ARG
@@ -97,7 +103,7 @@ def test_tile_entry_argument_errors():
     assert b"max_tiles" in L.h3a_last_error()
     assert tiles(Skv=32768 * 64, maxt=1) == _lib.H3A_ERR_UNSUPPORTED  # past 16-bit stage numbers
     ws = L.h3a_attn_fwd_blocksparse_tiles_ws
-    assert ws(16, 16, 16, 16, 1, 1, 300, 300, 128, z, z, z, z, None, 16, 1, 0.1, None, 0, None) == \
+    assert ws(16, 16, 16, 16, 1, 1, 300, 300, 128, z, z, z, ROW, None, 16, 1, 0.1, None, 0, None) == \
         _lib.H3A_ERR_INVALID_ARG
     n = ctypes.c_size_t(7)
     assert L.h3a_attn_fwd_blocksparse_tiles_workspace_size(1, 1, 300, 300, 64, 1, ctypes.byref(n)) == \

@@ -57,6 +57,7 @@ def test_fragment_pv(gpu):
 @pytest.mark.parametrize("B,H,Sq,Skv", [
     (1, 1, 1, 1), (1, 2, 7, 7), (1, 2, 64, 64), (1, 2, 65, 65), (1, 1, 129, 129),
     (1, 2, 200, 200), (2, 3, 128, 136), (1, 2, 64, 300), (1, 1, 300, 64), (1, 2, 1000, 1000),
+    (1, 2, 1, 300), (2, 1, 1, 77), (2, 2, 300, 1),  # length-1 sequences (their stride reaches the ABI as 0)
 ])
 def test_dense_vs_oracle(gpu, B, H, Sq, Skv):
     rng = np.random.default_rng(1000 + Sq * 7 + Skv)

@@ -339,6 +339,36 @@ def test_lut_leading_invalid_entry_changes_nothing(gpu, bad, blk):
     assert torch.equal(o_a, o_b)
 
 
+@pytest.mark.parametrize("blk_q,blk_k,Sq,Skv", [(64, 64, 1, 973), (192, 128, 1, 973), (128, 128, 1, 300),
+                                               (256, 64, 1, 500), (96, 96, 1, 700), (32, 48, 1, 333),
+                                               (64, 64, 300, 1), (128, 128, 130, 1), (96, 32, 200, 1)])
+def test_length_one_sequences(gpu, blk_q, blk_k, Sq, Skv):
+    """One query row or one key, B=2, H=2, against the masked oracle, on the native kernels
+    (64/128/192/256) and the tile path (other sizes).  A size-1 dimension's stride reaches the
+    library as 0; the kernels step past the end of the sequence (whole O tiles, whole K/V
+    stages) and those rows must still be dropped, not land on row 0."""
+    rng = np.random.default_rng(blk_q + 7 * blk_k + Sq + Skv)
+    B, H = 2, 2
+    q = randn_bf16(rng, (B, H, Sq, 128))
+    k = randn_bf16(rng, (B, H, Skv, 128))
+    v = randn_bf16(rng, (B, H, Skv, 128), scale=4.0)
+    nq, nk = -(-Sq // blk_q), -(-Skv // blk_k)
+    bmap = (rng.random((B, H, nq, nk)) < 0.6).astype(np.uint8)
+    bmap[..., 0] = 1
+    qd, kd, vd = (to_dev_bf16(x, gpu) for x in (q, k, v))
+    bt = torch.from_numpy(bmap).to(gpu)
+    if blk_q in ops.NATIVE_BLOCKS and blk_k in ops.NATIVE_BLOCKS:
+        lut, cnt = h3attn.block_map_to_lut(bt)
+        o = h3attn.attn_fwd_blocksparse(qd, kd, vd, lut, cnt, blk_q, blk_k)
+    else:
+        tl, tc = ops.block_map_to_tile_lut(bt, blk_q, blk_k, Sq, Skv)
+        o = ops.attn_fwd_blocksparse_tiles(qd, kd, vd, tl, tc)
+    torch.cuda.synchronize()
+    got = oracle.bf16_to_f32(from_dev_bf16(o)).reshape(o.shape)
+    ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=blk_q, blk_k=blk_k)
+    assert_close_absmax(got, ref, what=f"blk=({blk_q},{blk_k}) Sq={Sq} Skv={Skv}")
+
+
 def test_empty_rows_give_zero(gpu):
     rng = np.random.default_rng(22)
     q, k, v = (to_dev_bf16(randn_bf16(rng, (1, 1, 256, 128)), gpu) for _ in range(3))
