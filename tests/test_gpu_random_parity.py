@@ -1,7 +1,10 @@
 """Randomized parity over the attention paths: dense, native block-sparse (blocks 64/128/192/256,
 square or mixed), the tile-LUT path (every other multiple of 16) and the SLA route
 (sla.sparse_attention with its own block map), each against the oracle at the attention
-tolerance (max error <= 1e-2 * absmax, mean error <= 1e-3 * absmax).
+tolerance (max error <= 1e-2 * absmax, mean error <= 1e-3 * absmax).  Also the prologue
+(qk-RMSNorm + RoPE, plain and with the block pooling; within one bf16 ulp of the oracle,
+>= 99 % bit-identical, means equal to block_pool's) and the GPU block map (equal to the
+oracle's fp64 selection except at near-ties; LUT and counts consistent with the map).
 
 Shapes are drawn per case from a fixed seed: B 1-2, H 1-3, Sq and Skv 1-1399 (equal or not),
 inputs contiguous or read through [B,S,H,D] buffers, block maps of random density with
@@ -19,7 +22,7 @@ import torch
 
 import h3attn
 import oracle
-from conftest import assert_close_absmax, from_dev_bf16, randn_bf16, to_dev_bf16
+from conftest import assert_close_absmax, assert_prologue_close, from_dev_bf16, randn_bf16, to_dev_bf16
 from h3attn import ops, sla
 
 pytestmark = pytest.mark.gpu
@@ -91,3 +94,65 @@ def test_random_case_against_oracle(gpu, seed):
     torch.cuda.synchronize()
     got = oracle.bf16_to_f32(from_dev_bf16(o.contiguous())).reshape(o.shape)
     assert_close_absmax(got, ref, what=what)
+
+
+@pytest.mark.parametrize("seed", range(3000, 3030))
+def test_random_prologue_case(gpu, seed):
+    """Reference: harness/sp_runtime.py:93-99 (rms_rope_split_half_ on fused-QKV views)."""
+    rng = np.random.default_rng(seed)
+    S, H, rot = int(rng.integers(1, 700)), int(rng.integers(1, 90)), 16 * int(rng.integers(0, 9))
+    fused = bool(rng.random() < 0.5)
+    B = 1 if fused else int(rng.integers(1, 3))
+    pool = int(16 * rng.integers(1, 17)) if rng.random() < 0.5 else None
+    what = f"seed {seed}: B={B} S={S} H={H} rot={rot} fused={fused} pool={pool}"
+    x = rng.standard_normal((2, B, S, H, 128)).astype(np.float32)
+    x *= rng.uniform(0.5, 4.0, size=(2, B, S, 1, 1)).astype(np.float32)
+    w = (1.0 + 0.05 * rng.standard_normal((2, 128))).astype(np.float32)
+    xb, wb = oracle.f32_to_bf16(x), oracle.f32_to_bf16(w)
+    if fused:
+        qkv = torch.zeros(S, 3 * H * 128, dtype=torch.bfloat16, device=gpu)
+        q = qkv[:, :H * 128].view(1, S, H, 128)
+        k = qkv[:, H * 128:2 * H * 128].view(1, S, H, 128)
+        q.copy_(to_dev_bf16(xb[0], gpu))
+        k.copy_(to_dev_bf16(xb[1], gpu))
+    else:
+        q, k = to_dev_bf16(xb[0], gpu).clone(), to_dev_bf16(xb[1], gpu).clone()
+    rope = oracle.rope_table(S, rot) if rot else None
+    rope_t = None if rope is None else torch.from_numpy(rope).view(1, S, 1, rot // 2, 2, 2).to(gpu)
+    qw, kw = to_dev_bf16(wb[0], gpu), to_dev_bf16(wb[1], gpu)
+    if pool:
+        pq, pk = ops.qk_rmsnorm_rope_(q, k, rope_t, qw, kw, eps=1e-6, rot_dim=rot, pool_blk=pool)
+    else:
+        h3attn.rms_rope_split_half_(q, k, rope_t, qw, kw, epsilon=1e-6, rot_dim=rot)
+    torch.cuda.synchronize()
+    rq, rk = oracle.qk_rmsnorm_rope(xb[0], xb[1], rope, wb[0], wb[1], eps=1e-6, rot_dim=rot)
+    assert_prologue_close(from_dev_bf16(q).reshape(rq.shape), rq, what + " q")
+    assert_prologue_close(from_dev_bf16(k).reshape(rk.shape), rk, what + " k")
+    if pool:
+        assert torch.equal(pq, ops.block_pool(q.transpose(1, 2), pool)), what + ": q means"
+        assert torch.equal(pk, ops.block_pool(k.transpose(1, 2), pool)), what + ": k means"
+
+
+@pytest.mark.parametrize("seed", range(5000, 5030))
+def test_random_block_map_case(gpu, seed):
+    """Reference: custom_nodes/h3_sla/__init__.py:232 (SLA get_block_map at the node's sizes)."""
+    rng = np.random.default_rng(seed)
+    B, H, S = int(rng.integers(1, 3)), int(rng.integers(1, 4)), int(rng.integers(1, 3000))
+    bq = 16 * int(rng.integers(1, 17))
+    bk = bq if rng.random() < 0.6 else 16 * int(rng.integers(1, 17))
+    ratio, diag = float(rng.uniform(0.01, 1.0)), bool(rng.random() < 0.5)
+    what = f"seed {seed}: B={B} H={H} S={S} blk=({bq},{bk}) ratio={ratio:.3f} diag={diag}"
+    q, k = randn_bf16(rng, (B, H, S, 128)), randn_bf16(rng, (B, H, S, 128))
+    keep = sla.keep_count(ratio, -(-S // bk))
+    ref, scores = oracle.block_map(q, k, bq, bk, keep=keep, force_diag=diag, return_scores=True)
+    bmap, lut, cnt = sla.get_block_map(to_dev_bf16(q, gpu), to_dev_bf16(k, gpu), ratio, bq, bk,
+                                       force_diag=diag, want_map=True)
+    got = bmap.cpu().numpy()
+    for b, h, i, j in np.argwhere(got != ref):  # only fp32-vs-fp64 near-ties may differ
+        thr = np.sort(scores[b, h, i])[::-1][keep - 1]
+        assert abs(scores[b, h, i, j] - thr) <= 1e-4 * max(1.0, abs(thr)), what
+    cn, ln = cnt.cpu().numpy(), lut.cpu().numpy()
+    assert np.array_equal(cn, np.minimum(got.sum(-1), ln.shape[-1])), what + ": counts"
+    for idx in np.ndindex(*got.shape[:3]):
+        nz = np.flatnonzero(got[idx])[:ln.shape[-1]]
+        assert np.array_equal(ln[idx][:len(nz)], nz) and np.all(ln[idx][len(nz):] == -1), what
