@@ -86,6 +86,33 @@ def test_prologue_rejects_bad_layout(gpu):
         h3attn.qk_rmsnorm_rope_(q, k, None, w, w, rot_dim=24)
 
 
+@pytest.mark.parametrize("B,S,H,rot,pool", [(1, 1, 1, 128, None), (2, 1, 3, 64, 16), (1, 1, 56, 128, 64),
+                                           (2, 5, 1, 0, 48), (1, 300, 1, 128, 256)])
+def test_size_one_dimensions(gpu, B, S, H, rot, pool):
+    """One token and/or one head: a size-1 dimension's stride reaches the library as 0.  q/k
+    within one bf16 ulp of the oracle; the pooled means equal block_pool's."""
+    from h3attn import ops
+    rng = np.random.default_rng(B * 1000 + S * 10 + H)
+    x = rng.standard_normal((2, B, S, H, 128)).astype(np.float32)
+    w = (1.0 + 0.05 * rng.standard_normal((2, 128))).astype(np.float32)
+    xb, wb = oracle.f32_to_bf16(x), oracle.f32_to_bf16(w)
+    q, k = to_dev_bf16(xb[0], gpu).clone(), to_dev_bf16(xb[1], gpu).clone()
+    rope = oracle.rope_table(S, rot) if rot else None
+    rope_t = None if rope is None else torch.from_numpy(rope).view(1, S, 1, rot // 2, 2, 2).to(gpu)
+    qw, kw = to_dev_bf16(wb[0], gpu), to_dev_bf16(wb[1], gpu)
+    if pool:
+        pq, pk = ops.qk_rmsnorm_rope_(q, k, rope_t, qw, kw, eps=1e-6, rot_dim=rot, pool_blk=pool)
+    else:
+        h3attn.rms_rope_split_half_(q, k, rope_t, qw, kw, epsilon=1e-6, rot_dim=rot)
+    torch.cuda.synchronize()
+    rq, rk = oracle.qk_rmsnorm_rope(xb[0], xb[1], rope, wb[0], wb[1], eps=1e-6, rot_dim=rot)
+    assert_prologue_close(from_dev_bf16(q).reshape(rq.shape), rq, "q")
+    assert_prologue_close(from_dev_bf16(k).reshape(rk.shape), rk, "k")
+    if pool:
+        assert torch.equal(pq, ops.block_pool(q.transpose(1, 2), pool))
+        assert torch.equal(pk, ops.block_pool(k.transpose(1, 2), pool))
+
+
 @pytest.mark.parametrize("S,H,blk,rot", [(8192, 56, 64, 128), (1000, 5, 16, 64), (777, 56, 200, 128),
                                          (300, 12, 128, 0), (3, 2, 64, 128), (4100, 9, 48, 128)])
 def test_pooled_prologue_equals_prologue_then_block_pool(gpu, S, H, blk, rot):
