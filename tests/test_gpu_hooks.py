@@ -46,6 +46,28 @@ def test_patched_forward_matches_stock(gpu):
     assert torch.equal(no_rope, want_no_rope)
 
 
+@pytest.mark.parametrize("S,heads,rot", [(1, 4, 128), (2, 1, 64), (63, 3, 128), (65, 2, 32), (777, 5, 128),
+                                         (2048, 8, 96)])
+def test_patched_forward_matches_stock_shapes(gpu, S, heads, rot):
+    """The patched forward against the stock one over sequence lengths (one token
+    included, where the kernels see a length-1 sequence), head counts and rot dims."""
+    class A(standin_dit.Attention):
+        pass
+
+    dim = 128 * heads
+    m = _module(A, gpu, dim=dim, heads=heads, seed=S)
+    x = torch.randn(S, dim, device=gpu, dtype=torch.bfloat16)
+    rope = h3attn.rope_freqs(S, rot, device=gpu)
+    with torch.no_grad():
+        want = m(x, rope_freqs=rope).float()
+        assert hooks.install(A)
+        try:
+            got = m(x, rope_freqs=rope).float()
+        finally:
+            hooks.uninstall(A)
+    assert_close_absmax(got.cpu().numpy(), want.cpu().numpy(), what=f"patched forward S={S} H={heads}")
+
+
 def test_patched_optimized_attention(gpu):
     q, k, v = (torch.randn(1, 4, 300, 128, device=gpu, dtype=torch.bfloat16) for _ in range(3))
     want = standin_dit.optimized_attention(q, k, v, 4, skip_reshape=True).float()
