@@ -4,7 +4,8 @@ square or mixed), the tile-LUT path (every other multiple of 16) and the SLA rou
 tolerance (max error <= 1e-2 * absmax, mean error <= 1e-3 * absmax).  Also the prologue
 (qk-RMSNorm + RoPE, plain and with the block pooling; within one bf16 ulp of the oracle,
 >= 99 % bit-identical, means equal to block_pool's) and the GPU block map (equal to the
-oracle's fp64 selection except at near-ties; LUT and counts consistent with the map).
+oracle's fp64 selection except at near-ties; LUT and counts consistent with the map), and
+shapes large enough for the work queues and split tails, against fp32 attention on the GPU.
 
 Shapes are drawn per case from a fixed seed: B 1-2, H 1-3, Sq and Skv 1-1399 (equal or not),
 inputs contiguous or read through [B,S,H,D] buffers, block maps of random density with
@@ -156,3 +157,44 @@ def test_random_block_map_case(gpu, seed):
     for idx in np.ndindex(*got.shape[:3]):
         nz = np.flatnonzero(got[idx])[:ln.shape[-1]]
         assert np.array_equal(ln[idx][:len(nz)], nz) and np.all(ln[idx][len(nz):] == -1), what
+
+
+def _ref_head(q, k, v, mask=None):
+    """fp32 attention of one head from contiguous operands (plain matmuls, no batched bf16 products)."""
+    s = (q.float() @ k.float().t().contiguous()) / 128 ** 0.5
+    if mask is not None:
+        s = s.masked_fill(~mask, float("-inf"))
+    p = torch.nan_to_num(torch.softmax(s, -1), nan=0.0)
+    return p @ v.float()
+
+
+@pytest.mark.parametrize("seed", [8000, 8001, 8002, 8003, 8005, 8006])
+def test_random_large_case(gpu, seed):
+    """Shapes large enough for the persistent grid with per-XCD work queues and split last
+    rounds (H 4-24, Sq and Skv 2048-16384): dense, and native block-sparse at a random block
+    size, against fp32 attention per head on the GPU."""
+    rng = np.random.default_rng(seed)
+    mode = ("dense", "sparse")[seed % 2]
+    H, Sq = int(rng.integers(4, 25)), int(rng.integers(2048, 16385))
+    Skv = Sq if rng.random() < 0.7 else int(rng.integers(2048, 16385))
+    blk = int(rng.choice(NATIVE))
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    q = torch.randn(1, H, Sq, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+    k = torch.randn(1, H, Skv, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+    v = torch.randn(1, H, Skv, 128, generator=g, device=gpu, dtype=torch.bfloat16) * 4
+    bm = None
+    if mode == "dense":
+        o = h3attn.attn_fwd(q, k, v)
+    else:
+        nq, nk = -(-Sq // blk), -(-Skv // blk)
+        bm = (torch.rand(1, H, nq, nk, generator=g, device=gpu) < float(rng.uniform(0.05, 0.5))).to(torch.uint8)
+        lut, cnt = h3attn.block_map_to_lut(bm)
+        o = h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk)
+    torch.cuda.synchronize()
+    for h in range(H):
+        mask = None
+        if bm is not None:
+            mask = bm[0, h].bool().repeat_interleave(blk, 0)[:Sq].repeat_interleave(blk, 1)[:, :Skv]
+        ref = _ref_head(q[0, h], k[0, h], v[0, h], mask)
+        assert_close_absmax(o[0, h].float().cpu().numpy(), ref.cpu().numpy(),
+                            what=f"seed {seed}: {mode} H={H} Sq={Sq} Skv={Skv} blk={blk} head {h}")
