@@ -120,6 +120,45 @@ def test_graph_replay_of_queued_launches(gpu):
             assert torch.equal(o, w), f"replay {r}: {name} differs from the eager call"
 
 
+def test_graph_replay_of_key_split_and_tile_launches(gpu):
+    """The 64-row key-split pairs (64x64 blocks) and the tile path (96x96 blocks over 64x64
+    tiles) at H=9, S=32768, both through the queued entry points (a kernel zeroes the
+    counters before each launch): captured in one graph, every replay, with eager work and
+    cleared outputs in between, equals the eager calls bit for bit."""
+    g = torch.Generator(device=gpu).manual_seed(44)
+    B, H, S = 1, 9, 32768
+    q, k, v = (torch.randn(B, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    maps = {}
+    for blk in (64, 96):
+        nb = -(-S // blk)
+        m = torch.rand(B, H, nb, nb, generator=g, device=gpu) < 0.25
+        d = torch.arange(nb, device=gpu)
+        m[..., d, d] = True
+        maps[blk] = m.to(torch.uint8)
+    lut, cnt = h3attn.block_map_to_lut(maps[64])
+    tl, tc = ops.block_map_to_tile_lut(maps[96], 96, 96, S, S)
+    assert ops.sparse_workspace_bytes(B, H, S, S, 64, 64, lut.shape[3]) > 0  # queued
+    assert ops.tiles_workspace_bytes(B, H, S, S, tl.shape[3]) > 0
+
+    def fn():
+        return (h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, 64, 64),
+                ops.attn_fwd_blocksparse_tiles(q, k, v, tl, tc, queues=True))
+
+    want = [t.clone() for t in fn()]
+    torch.cuda.synchronize()
+    graph, outs = graphs.capture(fn, warmup=1)
+    other = torch.randn(1, 2, 300, 128, device=gpu, dtype=torch.bfloat16)
+    for r in range(3):
+        h3attn.attn_fwd(other, other, other)  # unrelated eager work between replays
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, o, w in zip(("64x64 key-split", "96x96 tiles"), outs, want):
+            assert torch.equal(o, w), f"replay {r}: {name} differs from the eager call"
+
+
 def test_graph_capture_requires_capture_before_replay(gpu):
     layers, _ = _layers(gpu, n=1)
     with pytest.raises(RuntimeError):
