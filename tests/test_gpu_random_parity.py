@@ -8,8 +8,8 @@ oracle's fp64 selection except at near-ties; LUT and counts consistent with the 
 shapes large enough for the work queues and split tails, against fp32 attention on the GPU.
 
 Shapes are drawn per case from a fixed seed: B 1-2, H 1-3, Sq and Skv 1-1399 (equal or not),
-inputs contiguous or read through [B,S,H,D] buffers, block maps of random density with
-empty rows.  Such a sweep found that a length-1 query sequence (its stride 0, as for any
+q, k, v and O each contiguous, sequence-major, with padded rows or with padded batches,
+block maps of random density with empty rows.  Such a sweep found that a length-1 query sequence (its stride 0, as for any
 size-1 dimension) sent the kernels' padding rows onto row 0.
 
 Reference: custom_nodes/h3_sla/__init__.py:226-235 (block map + sparse attention);
@@ -32,14 +32,37 @@ NATIVE = (64, 128, 192, 256)
 MODES = ("dense", "native", "tiles", "sla")
 
 
-def _device(bits, gpu, strided):
-    t = to_dev_bf16(bits, gpu)  # [B,H,S,D] contiguous
-    if strided:  # the same values read through a [B,S,H,D] buffer
-        B, H, S, D = bits.shape
+LAYOUTS = ("bhsd", "bshd", "padrow", "padbatch")
+
+
+def _device(bits, gpu, layout):
+    """The values of [B,H,S,D] `bits` on the GPU in one of four memory layouts: contiguous,
+    sequence-major ([B,S,H,D] buffer), rows padded to 192 elements, or batches padded apart."""
+    t = to_dev_bf16(bits, gpu)
+    B, H, S, D = bits.shape
+    if layout == "bshd":
         buf = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=gpu)
         buf.copy_(t.transpose(1, 2))
-        t = buf.transpose(1, 2)
+        return buf.transpose(1, 2)
+    if layout == "padrow":
+        buf = torch.full((B, H, S, D + 64), 7.0, dtype=torch.bfloat16, device=gpu)
+        buf[..., :D] = t
+        return buf[..., :D]
+    if layout == "padbatch":
+        buf = torch.full((B, H + 1, S, D), 7.0, dtype=torch.bfloat16, device=gpu)
+        buf[:, :H] = t
+        return buf[:, :H]
     return t
+
+
+def _out_like(q, gpu, layout):
+    """None (the library allocates O) or a preallocated O in a sequence-major or padded layout."""
+    B, H, Sq, D = q.shape
+    if layout == "bshd":
+        return torch.empty(B, Sq, H, D, dtype=torch.bfloat16, device=gpu).transpose(1, 2)
+    if layout == "padrow":
+        return torch.empty(B, H, Sq, D + 64, dtype=torch.bfloat16, device=gpu)[..., :D]
+    return None
 
 
 def _case(seed):
@@ -66,13 +89,17 @@ def _case(seed):
 @pytest.mark.parametrize("seed", list(range(7000, 7120)) + [50297])
 def test_random_case_against_oracle(gpu, seed):
     rng, mode, B, H, Sq, Skv, strided, bq, bk = _case(seed)
-    what = f"seed {seed}: {mode} B={B} H={H} Sq={Sq} Skv={Skv} strided={strided} blk=({bq},{bk})"
     q = randn_bf16(rng, (B, H, Sq, 128))
     k = randn_bf16(rng, (B, H, Skv, 128))
     v = randn_bf16(rng, (B, H, Skv, 128), scale=4.0)
-    qd, kd, vd = (_device(x, gpu, strided) for x in (q, k, v))
+    lay = [("bshd" if strided else "bhsd") if rng.random() < 0.5 else LAYOUTS[int(rng.integers(0, 4))]
+           for _ in range(3)]
+    out_lay = LAYOUTS[int(rng.integers(0, 4))]
+    what = f"seed {seed}: {mode} B={B} H={H} Sq={Sq} Skv={Skv} layouts={lay} out={out_lay} blk=({bq},{bk})"
+    qd, kd, vd = (_device(x, gpu, lt) for x, lt in zip((q, k, v), lay))
+    out = _out_like(qd, gpu, out_lay)
     if mode == "dense":
-        o = h3attn.attn_fwd(qd, kd, vd)
+        o = h3attn.attn_fwd(qd, kd, vd, out=out)
         ref = oracle.attn_fwd(q, k, v)
     elif mode == "sla":
         keep, diag = float(rng.uniform(0.05, 0.9)), bool(rng.random() < 0.5)
@@ -87,10 +114,10 @@ def test_random_case_against_oracle(gpu, seed):
         bt = torch.from_numpy(bmap).to(gpu)
         if mode == "native":
             lut, cnt = h3attn.block_map_to_lut(bt)
-            o = h3attn.attn_fwd_blocksparse(qd, kd, vd, lut, cnt, bq, bk)
+            o = h3attn.attn_fwd_blocksparse(qd, kd, vd, lut, cnt, bq, bk, out=out)
         else:
             lut, cnt = ops.block_map_to_tile_lut(bt, bq, bk, Sq, Skv)
-            o = ops.attn_fwd_blocksparse_tiles(qd, kd, vd, lut, cnt, queues=bool(rng.random() < 0.5))
+            o = ops.attn_fwd_blocksparse_tiles(qd, kd, vd, lut, cnt, out=out, queues=bool(rng.random() < 0.5))
         ref = oracle.attn_fwd(q, k, v, block_map=bmap, blk_q=bq, blk_k=bk)
     torch.cuda.synchronize()
     got = oracle.bf16_to_f32(from_dev_bf16(o.contiguous())).reshape(o.shape)
