@@ -263,6 +263,10 @@ int h3a_block_pool(const void *x, int B, int H, int S, int D, const int64_t stri
  * kept indices ascending into lut [B,H,nq,max_k_blocks] (-1 padded), their
  * number into counts [B,H,nq], and, if block_map is not NULL, the 0/1 map
  * [B,H,nq,nk].  pq: fp32 [B,H,nq,128], pk: fp32 [B,H,nk,128], contiguous.
+ * Scores are fp32 products and sums in the order of the fp32 matrix-core
+ * instruction (not a sequential dot product), so a key block whose score ties
+ * the keep-th one to the last bits may go either way; exact ties keep the
+ * lower index.  nk <= 7000 (H3A_ERR_UNSUPPORTED beyond).
  * The selection step of SLA's get_block_map (custom_nodes/h3_sla/__init__.py:232).
  */
 int h3a_block_select(const float *pq, const float *pk, int B, int H, int nq, int nk, int keep,
