@@ -921,12 +921,13 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   };
   // LDS operand reads issued ahead of a matrix cluster's first MFMA (then 2
   // after each MFMA), and the wave priority raised (s_setprio 1) during the
-  // cluster: same-box sweeps chose 4 and no raise for the dense kernel, 6
-  // for the block-sparse ones, whose group B raises its priority during its
-  // matrix cluster while group A's cluster runs at the default: group B's
-  // cluster, which shares its slot with group A's softmax, otherwise ran
-  // ~15 % longer than group A's and bounded the stage.
-  constexpr int kReadAhead = kSparse ? 6 : 4;
+  // cluster: same-box sweeps chose 4 reads ahead for the dense kernel and the
+  // 128-row pairs, 5 for the key-split pairs (16 MFMAs per cluster), and no
+  // raise for the dense kernel.  In the block-sparse kernels group B raises
+  // its priority during its matrix cluster while group A's cluster runs at
+  // the default: group B's cluster, which shares its slot with group A's
+  // softmax, otherwise ran ~15 % longer than group A's and bounded the stage.
+  constexpr int kReadAhead = kKeySplit ? 5 : 4;
   constexpr int kReadsPerMfma = 2;
   constexpr bool kRaisePrio = kSparse;
 
