@@ -516,8 +516,11 @@ __device__ __forceinline__ void softmax_stage_stale(f32x16 (&s)[NSUB], int key0,
   if (kHint ? __builtin_expect(past, 0) : past) mask_tail<NSUB>(s, key0, Skv, g);
   float ps;
   exp_pack_sum<NSUB>(s, sl2, kMaybeEmpty && m == kNegInf ? 0.f : m, pf, ps);
-  const bool refresh =
-      __builtin_amdgcn_ballot_w64(stage_sum_needs_refresh(ps) || (kMaybeEmpty && m == kNegInf)) != 0;
+  // Two ballots OR'd on the scalar unit: one ballot of the lane-wise OR
+  // compiles to a mask -> 0/1 -> compare round trip through VALU.
+  uint64_t need = __builtin_amdgcn_ballot_w64(stage_sum_needs_refresh(ps));
+  if constexpr (kMaybeEmpty) need |= __builtin_amdgcn_ballot_w64(m == kNegInf);
+  const bool refresh = need != 0;
   if (kHint ? __builtin_expect(refresh, 0) : refresh) {
     const float mnew = fmaxf(m, tile_max<NSUB>(s, sl2));
     const float alpha = fast_exp2(m - (kMaybeEmpty && mnew == kNegInf ? 0.f : mnew));
