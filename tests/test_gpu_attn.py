@@ -240,3 +240,59 @@ def test_full_h3_shape(gpu, H):
     got = o[0, heads].float()
     assert_close_absmax(got.cpu().numpy(), ref.cpu().numpy(), what=f"H={H} S={S}")
     assert_close_absmax(got[:, -8:].cpu().numpy(), ref[:, -8:].cpu().numpy(), what="tail tile")
+
+
+def test_concurrent_host_threads_on_separate_streams(gpu):
+    """Two host threads, each on its own stream, run queued dense and block-sparse
+    launches at once (each call has its own workspace from torch's allocator on its
+    stream, so its own queue counters and split partials).  Every result equals the
+    same call made alone, bit for bit."""
+    import threading
+
+    from h3attn import sla
+
+    g = torch.Generator(device=gpu).manual_seed(21)
+    H, S = 16, 16384  # 16 x 64 = 1024 dense tiles: a queued persistent launch
+    inputs = [tuple(torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+              for _ in range(2)]
+    maps = [{blk: sla.get_block_map(q, k, 0.25, blk, blk, force_diag=True, want_map=False)[1:]
+             for blk in (128, 64)} for q, k, _ in inputs]
+
+    def calls(i):
+        q, k, v = inputs[i]
+        outs = [h3attn.attn_fwd(q, k, v)]
+        for blk in (128, 64):
+            lut, cnt = maps[i][blk]
+            outs.append(h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk))
+        return outs
+
+    alone = []
+    for i in range(2):
+        alone.append([o.clone() for o in calls(i)])
+        torch.cuda.synchronize()
+
+    results, errors = [None, None], []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream(device=gpu)
+            with torch.cuda.stream(s):
+                got = []
+                for _ in range(3):
+                    got.append(calls(i))
+            s.synchronize()
+            results[i] = got
+        except Exception as e:  # surfaced in the main thread below
+            errors.append(e)
+
+    print("[threads] 2 host threads x 3 rounds of dense + sparse 128/64 at H=16 S=16384", flush=True)
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        for rnd in results[i]:
+            for got, ref in zip(rnd, alone[i]):
+                assert torch.equal(got, ref)
