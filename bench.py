@@ -323,7 +323,7 @@ def run_sparse(args, torch, h3attn, dev):
         a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         bmap, lut, cnt = sla.get_block_map(q, k, 0.25, blk, blk, force_diag=True, smooth_k=False)
-        if tiles:  # block sizes outside the native kernels': 64x64 tiles with sub-block masks
+        if tiles:  # block sizes outside the native kernels': 32-key columns with sub-block masks
             lut, cnt = ops.block_map_to_tile_lut(bmap, blk, blk, S, S)
         b_.record()
         torch.cuda.synchronize()
@@ -370,7 +370,7 @@ def run_sparse(args, torch, h3attn, dev):
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
                      "kernel": ("attn_fwd_pingpong_kernel<SwzLayout,2,sparse,key-split,tile-mask> (pairs of "
-                                "64-row query blocks over 64x64 tiles with 16x16 sub-block masks)" if tiles
+                                "64-row query blocks over 32-key columns with 16x16 sub-block masks)" if tiles
                                 else "attn_fwd_pingpong_kernel<SwzLayout,2,sparse> (pairs of 128-row query blocks; "
                                 "+ split_combine_kernel for the split tail)" if blk % 128 == 0
                                 else "attn_fwd_pingpong_kernel<SwzLayout,2,sparse,key-split> (pairs of 64-row "

@@ -179,18 +179,19 @@ int h3a_attn_fwd_blocksparse_ws(const void *q, const void *k, const void *v, voi
                                 h3a_stream_t stream);
 
 /*
- * Block-sparse attention over 64x64 tiles with sub-block masks: the path for
- * block sizes h3a_attn_fwd_blocksparse does not take (the h3_sla node offers
- * every multiple of 16 from 16 to 256, custom_nodes/h3_sla/__init__.py:315;
+ * Block-sparse attention over 32-key columns with sub-block masks: the path
+ * for block sizes h3a_attn_fwd_blocksparse does not take (the h3_sla node
+ * offers every multiple of 16 from 16 to 256, custom_nodes/h3_sla/__init__.py:315;
  * query and key blocks may differ).  The tile LUT comes from
  * h3a_block_map_to_tile_lut: row (b*H + h)*ceil(Sq/64) + qs of tile_lut
- * [.., max_tiles] lists, for query rows 64*qs .. 64*qs+63, the 64-key stages
- * to attend to, each entry stage << 16 | mask, where bit 4*i + j of the mask
- * admits rows 64*qs + 16*i .. +15 against keys 64*stage + 16*j .. +15 (every
- * other score of the tile is masked); tile_counts holds each row's length.
- * Entries whose stage is negative or at or past ceil(Skv/64) load nothing.
- * A row with no admitted key gets O = 0.  Skv <= 32767 * 64.  max_tiles in
- * [1, ceil(Skv/64)].  Other arguments as h3a_attn_fwd; _ws and
+ * [.., max_tiles] lists, for query rows 64*qs .. 64*qs+63, the 32-key columns
+ * to attend to, ascending, each entry column << 8 | mask, where bit 2*i + j of
+ * the mask admits rows 64*qs + 16*i .. +15 against keys 32*column + 16*j .. +15
+ * (every other score of the column is masked); tile_counts holds each row's
+ * length.  The kernel takes a row's columns two at a time.  Entries whose
+ * column is negative or at or past ceil(Skv/32) load nothing.  A row with no
+ * admitted key gets O = 0.  Skv <= 65534 * 32.  max_tiles in
+ * [1, ceil(Skv/32)].  Other arguments as h3a_attn_fwd; _ws and
  * _workspace_size as for h3a_attn_fwd_blocksparse_ws (work queues, no split).
  * No counterpart in the reference's own code: SLA's Triton kernel takes the
  * same block maps at these sizes.
@@ -216,7 +217,7 @@ int h3a_attn_fwd_blocksparse_tiles_ws(const void *q, const void *k, const void *
  * contiguous) at any block sizes that are multiples of 16 into the tile LUT of
  * h3a_attn_fwd_blocksparse_tiles: tile_lut [B,H,ceil(Sq/64),max_tiles] (-1
  * padded) and tile_counts [B,H,ceil(Sq/64)].  A row with more than max_tiles
- * stages keeps its first max_tiles; max_tiles = ceil(Skv/64) always suffices.
+ * columns keeps its first max_tiles; max_tiles = ceil(Skv/32) always suffices.
  * The SLA block map (custom_nodes/h3_sla/__init__.py:232) at the node's
  * block sizes.
  */

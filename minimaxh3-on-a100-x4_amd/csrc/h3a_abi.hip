@@ -325,11 +325,11 @@ int prepare_tiles(AttnArgs &a, const void *q, const void *k, const void *v, void
   int rc = check_attn(q, k, v, o, B, H, Sq, Skv, D, q_strides, k_strides, v_strides, o_strides, scale);
   if (rc) return rc;
   if (!lut || !counts) return fail(H3A_ERR_INVALID_ARG, "null tile_lut/tile_counts pointer");
-  const int64_t nstages = ((int64_t)Skv + 63) / 64;
-  if (nstages > kMaxTileStages)
-    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d stages of 64 keys", Skv, kMaxTileStages);
-  if (max_tiles <= 0 || max_tiles > nstages)
-    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)nstages);
+  const int64_t ncols = ((int64_t)Skv + 31) / 32;
+  if (ncols > kMaxTileColumns)
+    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d columns of 32 keys", Skv, kMaxTileColumns);
+  if (max_tiles <= 0 || max_tiles > ncols)
+    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)ncols);
   const int64_t nsub = ((int64_t)Sq + 63) / 64;
   const int64_t total = (int64_t)B * H * nsub;
   if (total > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many query tiles (%lld)", (long long)total);
@@ -339,9 +339,9 @@ int prepare_tiles(AttnArgs &a, const void *q, const void *k, const void *v, void
   a.lut = lut;
   a.counts = counts;
   a.lut_stride = max_tiles;
-  a.blk_k = 64;
+  a.blk_k = 32;  // a LUT entry names one 32-key column
   a.sub = 1;
-  a.nkb = (int)nstages;
+  a.nkb = (int)ncols;
   a.nqb = (int)nsub;
   a.qmul = 1;
   return H3A_OK;
@@ -369,11 +369,11 @@ int h3a_attn_fwd_blocksparse_tiles_workspace_size(int B, int H, int Sq, int Skv,
   if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0)
     return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
   if (D != 128) return fail(H3A_ERR_UNSUPPORTED, "head_dim %d unsupported (only 128)", D);
-  const int64_t nstages = ((int64_t)Skv + 63) / 64;
-  if (nstages > kMaxTileStages)
-    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d stages of 64 keys", Skv, kMaxTileStages);
-  if (max_tiles <= 0 || max_tiles > nstages)
-    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)nstages);
+  const int64_t ncols = ((int64_t)Skv + 31) / 32;
+  if (ncols > kMaxTileColumns)
+    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d columns of 32 keys", Skv, kMaxTileColumns);
+  if (max_tiles <= 0 || max_tiles > ncols)
+    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)ncols);
   SplitPlan plan;
   const int rc = plan_attn_sparse_tiles(B, H, Sq, max_tiles, &plan);
   if (rc) return rc;
@@ -411,11 +411,11 @@ int h3a_block_map_to_tile_lut(const uint8_t *block_map, int B, int H, int Sq, in
     return fail(H3A_ERR_INVALID_ARG, "sizes must be positive (B=%d H=%d Sq=%d Skv=%d)", B, H, Sq, Skv);
   if (!tile_block_ok(blk_q) || !tile_block_ok(blk_k))
     return fail(H3A_ERR_UNSUPPORTED, "block sizes %d x %d: multiples of 16 only", blk_q, blk_k);
-  const int64_t nstages = ((int64_t)Skv + 63) / 64;
-  if (nstages > kMaxTileStages)
-    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d stages of 64 keys", Skv, kMaxTileStages);
-  if (max_tiles <= 0 || max_tiles > nstages)
-    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)nstages);
+  const int64_t ncols = ((int64_t)Skv + 31) / 32;
+  if (ncols > kMaxTileColumns)
+    return fail(H3A_ERR_UNSUPPORTED, "Skv %d past the tile LUT's %d columns of 32 keys", Skv, kMaxTileColumns);
+  if (max_tiles <= 0 || max_tiles > ncols)
+    return fail(H3A_ERR_INVALID_ARG, "max_tiles %d outside [1, %lld]", max_tiles, (long long)ncols);
   const int64_t rows = (int64_t)B * H * ((Sq + 63) / 64);
   if ((rows + 3) / 4 > INT_MAX) return fail(H3A_ERR_INVALID_ARG, "too many tile LUT rows");
   return launch_block_map_to_tile_lut(block_map, B, H, Sq, Skv, blk_q, blk_k, tile_lut, tile_counts, max_tiles,

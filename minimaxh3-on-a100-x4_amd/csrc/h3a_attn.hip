@@ -142,7 +142,9 @@ struct TileDma {
   // Offsets of instructions 0, 1, ... in issue order: `cur` starts at
   // first() and next() moves it on.  The add is opaque to the compiler, which
   // would otherwise hoist all kInst offsets out of the stage loop and keep
-  // them in registers.  Without kAffine the cursor is the instruction index.
+  // them in registers.  Without kAffine the cursor is the byte offset added
+  // to every instruction's own offset (the stage's, for a descriptor of the
+  // whole (b,h) slice).
   __device__ __forceinline__ uint32_t first() const { return kAffine ? off[0] : 0u; }
   __device__ __forceinline__ uint32_t next(uint32_t cur) const {
     if constexpr (kAffine) {
@@ -150,7 +152,7 @@ struct TileDma {
       asm volatile("v_add_u32 %0, %1, %2" : "=v"(r) : "v"(cur), "s"(step));
       return r;
     } else {
-      return cur + 1;
+      return cur;
     }
   }
   // Buffer descriptor of the stage that starts at key0 (valid rows only).
@@ -166,7 +168,7 @@ struct TileDma {
   // instruction's address of both buffers live in SGPRs.
   __device__ __forceinline__ void issue_one(u32x4 d, int i, uint32_t cur, uint32_t m0) const {
     if (kInstTotal % NW == 0 || wave + i * NW < kInstTotal)
-      buffer_load_lds_b128(d, kAffine ? cur : off[i], m0);
+      buffer_load_lds_b128(d, kAffine ? cur : off[i] + cur, m0);
   }
   __device__ __forceinline__ void issue(const uint16_t *base, int64_t ss, int key0, int Skv,
                                         uint16_t *tile) const {
@@ -404,17 +406,17 @@ __device__ __forceinline__ void mask_tail(f32x16 (&s)[NSUB], int key0, int Skv, 
   }
 }
 
-// Tile-mask sparse attention (64-row key-split pairs over 64x64 tiles, each
-// with a 16-bit mask of kept 16x16 sub-blocks): the scores of this wave's
-// key half whose sub-block bit is clear -> -inf.  Bit 4*i + j covers rows
-// 16i..16i+15 of the 64-row query block and keys 16j..16j+15 of the 64-key
-// stage.  The lane's query row is 32*rq + l32; its scores s[0][r] are keys
-// 32*kh + 8*(r/4) + 4*g + r%4, so registers 0-7 lie in key sub-block 2*kh and
-// registers 8-15 in 2*kh + 1.
+// Tile-mask sparse attention (64-row key-split pairs over 32-key columns,
+// each with an 8-bit mask of kept 16x16 sub-blocks): the scores of this
+// wave's column whose sub-block bit is clear -> -inf.  Bit 2*i + j covers
+// rows 16i..16i+15 of the 64-row query block and keys 16j..16j+15 of the
+// column.  The lane's query row is 32*rq + l32; its scores s[0][r] are keys
+// 8*(r/4) + 4*g + r%4 of the column, so registers 0-7 lie in key sub-block 0
+// and registers 8-15 in 1.
 template <int NSUB>
-__device__ __forceinline__ void apply_tile_mask(f32x16 (&s)[NSUB], uint32_t mask, int rq, int l32, int kh) {
+__device__ __forceinline__ void apply_tile_mask(f32x16 (&s)[NSUB], uint32_t mask, int rq, int l32) {
   static_assert(NSUB == 1, "tile masks apply to the 32-key waves of the key-split kernel");
-  const uint32_t bits = mask >> (4 * (2 * rq + (l32 >> 4)) + 2 * kh);
+  const uint32_t bits = mask >> (2 * (2 * rq + (l32 >> 4)));
   const bool k0 = (bits & 1u) != 0, k1 = (bits & 2u) != 0;
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -764,6 +766,10 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   int ngrp = niter, gj0 = 0;
   const int32_t *lut_row = nullptr;
   int e_pre[4] = {0, 0, 0, 0};
+  // Tile masks: stage j of a group is entries 2j and 2j+1 of its LUT row,
+  // two 32-key columns; the waves of key half kh take entry 2j + kh (their
+  // own column: its fetch, scores and mask).  ntile is the row's entry count.
+  int ntile = 0;
   const uint32_t smag = stage_magic(a.sub);  // block_of_stage_magic(t, smag) = t / a.sub
   if constexpr (kSparse) {
     // Query sub-block qb reads LUT row qb / a.qmul (blk_q = 256: the two
@@ -784,13 +790,16 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     lut_row = a.lut + ((int64_t)bh * a.nqb + (qb < a.nqt ? qb : 0) / a.qmul) * a.lut_stride;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int e = block_of_stage_magic(j, smag);
+      const int e = kTileMask ? 2 * j + kh : block_of_stage_magic(j, smag);
       e_pre[j] = ((ConstInts)lut_row)[e < a.lut_stride ? e : a.lut_stride - 1];
     }
     auto stages_of = [&](int qb, int cnt) __attribute__((always_inline)) -> int {
       if (qb >= a.nqt) return 0;
-      return (cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt)) * a.sub;
+      const int n = cnt < 0 ? 0 : (cnt > a.lut_stride ? a.lut_stride : cnt);
+      return kTileMask ? (n + 1) / 2 : n * a.sub;
     };
+    if constexpr (kTileMask)
+      ntile = qb >= a.nqt ? 0 : (cnt_own < 0 ? 0 : (cnt_own > a.lut_stride ? a.lut_stride : cnt_own));
     auto part_of = [&](int n, int &first) __attribute__((always_inline)) -> int {
       if (split_part < 0) {
         first = 0;
@@ -817,23 +826,30 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
       const __attribute__((address_space(4))) int32_t *row =
           (const __attribute__((address_space(4))) int32_t *)lut_row;
       const int jc = j < ngrp ? j : ngrp - 1;
-      return row[block_of_stage_magic(gj0 + (jc > 0 ? jc : 0), smag)];
+      if constexpr (kTileMask) {
+        const int i = 2 * (jc > 0 ? jc : 0) + kh;
+        return row[i < a.lut_stride ? i : a.lut_stride - 1];
+      } else {
+        return row[block_of_stage_magic(gj0 + (jc > 0 ? jc : 0), smag)];
+      }
     } else {
       return 0;
     }
   };
-  // Tile masks: an entry is stage << 16 | mask, the stage in units of 64
-  // keys (a.blk_k = 64, a.sub = 1); an arithmetic shift keeps a negative
-  // entry negative, so it still names no key block.
+  // Tile masks: an entry is column << 8 | mask, the column in units of 32
+  // keys (a.blk_k = 32, a.sub = 1); an arithmetic shift keeps a negative
+  // entry negative, so it still names no key block.  Past the row's entries
+  // (the last stage can hold one column) the key is Skv.
   auto key_of_entry = [&](int j, int e) __attribute__((always_inline)) -> int {
     if constexpr (kSparse) {
-      const int kb = kTileMask ? (e >> 16) : e;
+      const int kb = kTileMask ? (e >> 8) : e;
       // Two equivalent forms; each measured faster in one kernel (the
       // arithmetic one +0.5 % in the 128-row pairs, the select one +0.6 % in
       // the key-split pairs), through the code layout around them.
       const int key0 = kKeySplit ? lut_stage_key0_sel(gj0 + j, kb, a.nkb, a.blk_k, a.sub, smag, a.Skv)
                                  : lut_stage_key0_magic(gj0 + j, kb, a.nkb, a.blk_k, a.sub, smag, a.Skv);
-      return j < ngrp ? key0 : a.Skv;
+      if constexpr (kTileMask) return j < ngrp && 2 * j + kh < ntile ? key0 : a.Skv;
+      else return j < ngrp ? key0 : a.Skv;
     } else {
       return j < niter ? (j0 + j) * BN : a.Skv;
     }
@@ -893,10 +909,21 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // group B fetches the K stages and group A the V stages (waves w and w+4
   // share a column), each at the top of its softmax slot.  Sparse: each
   // group fetches its own K/V stream, spread over its matrix cluster.
-  TileDma<NW / 2, L, false, BN> kdma;
-  TileDma<NW / 2, L, true, BN> vdma;
-  kdma.init(a.kss, wave_u & 3, lane);
-  vdma.init(a.vss, wave_u & 3, lane);
+  // Tile masks: each key half of a stage is its own 32-key column, fetched by
+  // the two waves of that half (rq = 0, 1) into rows 32*kh .. 32*kh+31.
+  using KDma = std::conditional_t<kTileMask, TileDma<2, L, false, 32>, TileDma<NW / 2, L, false, BN>>;
+  using VDma = std::conditional_t<kTileMask, TileDma<2, L, true, 32>, TileDma<NW / 2, L, true, BN>>;
+  KDma kdma;
+  VDma vdma;
+  kdma.init(a.kss, kTileMask ? rq : (wave_u & 3), lane);
+  vdma.init(a.vss, kTileMask ? rq : (wave_u & 3), lane);
+  static_assert(!kTileMask || (KDma::kInst == 4 && VDma::kInst == 4), "4 loads of each stream per wave and stage");
+  auto kdst = [&](uint16_t *buf) __attribute__((always_inline)) {
+    return kTileMask ? buf + kh * 32 * (L::kKRow / 2) : buf;
+  };
+  auto vdst = [&](uint16_t *buf) __attribute__((always_inline)) {
+    return kTileMask ? buf + kh * 32 * (L::kVRow / 2) : buf;
+  };
   constexpr int kKI = decltype(kdma)::kInst, kVI = decltype(vdma)::kInst;
   // Sparse stage fetches.  By default one descriptor per (b,h) slice, built
   // here, and each stage's byte offset added to the lanes' offsets: the
@@ -947,11 +974,11 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // Prologue, all waves in step: K(0), V(0), K(1) in; S(0); P(0).  Dense:
   // group B fetches the K stages, group A the V stage.
   const int pkey0 = pro_key(0), pkey1 = pro_key(1);
-  const uint32_t pmask0 = kTileMask ? (uint32_t)pro_entry(0) & 0xffffu : 0u;
+  const uint32_t pmask0 = kTileMask ? (uint32_t)pro_entry(0) & 0xffu : 0u;
   if constexpr (kSparse) {
-    kdma.issue(Kb, a.kss, pkey0, a.Skv, kbuf[0]);
-    vdma.issue(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
-    kdma.issue(Kb, a.kss, pkey1, a.Skv, kbuf[1]);
+    kdma.issue(Kb, a.kss, pkey0, a.Skv, kdst(kbuf[0]));
+    vdma.issue(Vb, a.vss, pkey0, a.Skv, vdst(vbuf[0]));
+    kdma.issue(Kb, a.kss, pkey1, a.Skv, kdst(kbuf[1]));
   } else if (lead) {
     vdma.issue(Vb, a.vss, pkey0, a.Skv, vbuf[0]);
   } else {
@@ -963,8 +990,8 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   f32x16 s[WS];
   u32x4 pf[2 * WS];
   score_tile<L, WS>(kbuf[0], qf, k_rd, s);
-  if constexpr (kTileMask) apply_tile_mask<WS>(s, pmask0, rq, l32, kh);
-  softmax_stage<WS>(s, pkey0 + 32 * kh, a.Skv, g, a.sl2, m, lsum, o, pf);
+  if constexpr (kTileMask) apply_tile_mask<WS>(s, pmask0, rq, l32);
+  softmax_stage<WS>(s, pkey0 + (kTileMask ? 0 : 32 * kh), a.Skv, g, a.sl2, m, lsum, o, pf);
   __syncthreads();  // kbuf[0] is free for K(2)
 
   // Dense, stage j's fetch from the stream cursors: group A's V(j+1) into
@@ -992,8 +1019,8 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   int key_k = 0, key_v = 0;
   uint32_t mw0 = pmask0, mw1 = 0, mw2 = 0, soft_mask = 0;
   if constexpr (kTileMask) {
-    mw1 = (uint32_t)pro_entry(1) & 0xffffu;
-    mw2 = (uint32_t)pro_entry(2) & 0xffffu;
+    mw1 = (uint32_t)pro_entry(1) & 0xffu;
+    mw2 = (uint32_t)pro_entry(2) & 0xffu;
   }
   auto stage_keys = [&](int j) __attribute__((always_inline)) {
     soft_key = lead ? kw1 : kw0;
@@ -1007,7 +1034,7 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
       soft_mask = lead ? mw1 : mw0;
       mw0 = mw1;
       mw1 = mw2;
-      mw2 = (uint32_t)e3 & 0xffffu;
+      mw2 = (uint32_t)e3 & 0xffu;
     }
   };
   auto lut_next = [&](int j) __attribute__((always_inline)) { e3 = lut_entry(j + 4); };
@@ -1062,15 +1089,16 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // from stage_keys) into the buffers the group read in MFMA(j-1).
   auto mfma_fetch = [&](auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
-    DmaSeq<decltype(kdma)> kseq(kdma, k_desc(key_k), kbuf[P], k_soff(key_k));
-    DmaSeq<decltype(vdma)> vseq(vdma, v_desc(key_v), vbuf[P ^ 1], v_soff(key_v));
+    DmaSeq<decltype(kdma)> kseq(kdma, k_desc(key_k), kdst(kbuf[P]), k_soff(key_k));
+    DmaSeq<decltype(vdma)> vseq(vdma, v_desc(key_v), vdst(vbuf[P ^ 1]), v_soff(key_v));
     mfma_dma(par, kseq, vseq);
   };
   // Softmax cluster.  Its results are pinned to the slot (pin), so that the
   // compiler does not sink them past the barrier toward the MFMAs.
   auto soft = [&](int j) __attribute__((always_inline)) {
-    const int key0 = (kSparse ? soft_key : key_base(j + 1)) + 32 * kh;
-    if constexpr (kTileMask) apply_tile_mask<WS>(s, soft_mask, rq, l32, kh);
+    // Tile masks: the keys are already this wave's own column's.
+    const int key0 = (kSparse ? soft_key : key_base(j + 1)) + (kTileMask ? 0 : 32 * kh);
+    if constexpr (kTileMask) apply_tile_mask<WS>(s, soft_mask, rq, l32);
     softmax_stage_stale<WS, kSparse>(s, key0, a.Skv, g, a.sl2, m, lsum, o, pf);
 #pragma unroll
     for (int i = 0; i < 2 * WS; ++i) pin(pf[i]);

@@ -285,17 +285,17 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
 // ---------------------------------------------------------------------------
 // Tile LUTs, for block sizes the native block-sparse kernels do not take (any
 // multiple of 16, in either dimension).  The attention then runs on 64-row
-// query sub-blocks and 64-key stages: the tile LUT row of sub-block qs lists,
-// ascending, every stage holding a kept (query block, key block) pair for some
-// row of qs, as stage << 16 | mask.  Bit 4*i + j of the mask is set when rows
-// 64*qs + 16*i .. +15 and keys 64*stage + 16*j .. +15 lie in a kept pair; both
-// block sizes are multiples of 16, so each 16x16 sub-block lies in exactly one
-// pair.  Sub-blocks past Sq or Skv get no bit.  One wave per LUT row; lane l
-// takes stages 64*c + l, and the kept ones are written in order with one
-// ballot per 64 stages.  Entries past the count are -1.
+// query sub-blocks; the tile LUT row of sub-block qs lists, ascending, every
+// 32-key column holding a kept (query block, key block) pair for some row of
+// qs, as column << 8 | mask.  Bit 2*i + j of the mask is set when rows
+// 64*qs + 16*i .. +15 and keys 32*column + 16*j .. +15 lie in a kept pair;
+// both block sizes are multiples of 16, so each 16x16 sub-block lies in
+// exactly one pair.  Sub-blocks past Sq or Skv get no bit.  One wave per LUT
+// row; lane l takes columns 64*c + l, and the kept ones are written in order
+// with one ballot per 64 columns.  Entries past the count are -1.
 __global__ void __launch_bounds__(256) block_map_to_tile_lut_kernel(const uint8_t *map, int64_t rows, int nsub,
                                                                     int nq, int nk, int Sq, int Skv, int blk_q,
-                                                                    int blk_k, int nstages, int32_t *lut,
+                                                                    int blk_k, int ncols, int32_t *lut,
                                                                     int32_t *counts, int max_tiles) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -312,23 +312,23 @@ __global__ void __launch_bounds__(256) block_map_to_tile_lut_kernel(const uint8_
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   int32_t *out = lut + row * (int64_t)max_tiles;
   int base = 0;
-  for (int c = 0; c < nstages; c += 64) {
-    const int st = c + lane;
+  for (int c = 0; c < ncols; c += 64) {
+    const int col = c + lane;
     uint32_t mask = 0;
-    if (st < nstages) {
+    if (col < ncols) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = 64 * st + 16 * j;
+      for (int j = 0; j < 2; ++j) {
+        const int key = 32 * col + 16 * j;
         if (key >= Skv) break;
         const int kb = key / blk_k;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (mq[i] && mq[i][kb]) mask |= 1u << (4 * i + j);
+          if (mq[i] && mq[i][kb]) mask |= 1u << (2 * i + j);
       }
     }
     const uint64_t m = __builtin_amdgcn_ballot_w64(mask != 0);
     const int pos = base + __builtin_popcountll(m & below);
-    if (mask != 0 && pos < max_tiles) out[pos] = (int32_t)(((uint32_t)st << 16) | mask);
+    if (mask != 0 && pos < max_tiles) out[pos] = (int32_t)(((uint32_t)col << 8) | mask);
     base += __builtin_popcountll(m);
   }
   const int kept = base < max_tiles ? base : max_tiles;
@@ -360,10 +360,10 @@ __global__ void __launch_bounds__(256) lut_scatter_kernel(const int32_t *lut, co
 int launch_block_map_to_tile_lut(const uint8_t *map, int B, int H, int Sq, int Skv, int blk_q, int blk_k,
                                  int32_t *lut, int32_t *counts, int max_tiles, hipStream_t s) {
   const int nsub = (Sq + 63) / 64, nq = (Sq + blk_q - 1) / blk_q, nk = (Skv + blk_k - 1) / blk_k;
-  const int nstages = (Skv + 63) / 64;
+  const int ncols = (Skv + 31) / 32;
   const int64_t rows = (int64_t)B * H * nsub;
   hipLaunchKernelGGL(block_map_to_tile_lut_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, map, rows,
-                     nsub, nq, nk, Sq, Skv, blk_q, blk_k, nstages, lut, counts, max_tiles);
+                     nsub, nq, nk, Sq, Skv, blk_q, blk_k, ncols, lut, counts, max_tiles);
   return check_launch("block_map_to_tile_lut_kernel");
 }
 

@@ -59,8 +59,9 @@ inline bool sparse_block_ok(int blk) { return blk == 64 || blk == 128 || blk == 
 // positive multiple of 16 (each 16x16 sub-block of a 64x64 tile then lies in
 // exactly one block pair).
 inline bool tile_block_ok(int blk) { return blk > 0 && blk % 16 == 0; }
-// Stages a tile LUT entry can name (16 bits): Skv <= kMaxTileStages * 64.
-constexpr int kMaxTileStages = 32767;
+// 32-key columns a tile LUT entry can name (column << 8 | mask stays positive
+// and below 2^24): Skv <= kMaxTileColumns * 32.
+constexpr int kMaxTileColumns = 65534;
 inline int sparse_sub_block_rows(int blk_q) { return blk_q % 128 == 0 ? 128 : 64; }
 
 // Dense split-tail plan for a problem on the current device.

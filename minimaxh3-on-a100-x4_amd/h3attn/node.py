@@ -23,7 +23,7 @@ class H3SLAPatch:
                                    "tooltip": "fraction of key blocks each query block keeps (1 - sparsity)"}),
                 "blk": ("INT", {"default": 64, "min": lo, "max": hi, "step": sla.BLOCK_STEP,
                                 "tooltip": "query and key block size (64, 128, 192 and 256 run the "
-                                           "native kernels, the other sizes 64x64 tiles with sub-block masks)"}),
+                                           "native kernels, the other sizes 32-key columns with sub-block masks)"}),
                 "enabled": ("BOOLEAN", {"default": True}),
             },
             "optional": {

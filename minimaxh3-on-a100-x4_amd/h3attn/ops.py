@@ -269,9 +269,9 @@ def tiles_workspace_bytes(B: int, H: int, Sq: int, Skv: int, max_tiles: int, D: 
 def attn_fwd_blocksparse_tiles(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tile_lut: torch.Tensor,
                                tile_counts: torch.Tensor, scale: float | None = None,
                                out: torch.Tensor | None = None, queues: bool = True) -> torch.Tensor:
-    """Block-sparse attention over 64x64 tiles with 16x16 sub-block masks (block_map_to_tile_lut).
+    """Block-sparse attention over 32-key columns with 16x16 sub-block masks (block_map_to_tile_lut).
 
-    tile_lut: int32 [B,H,ceil(Sq/64),max_tiles], entries stage << 16 | mask;
+    tile_lut: int32 [B,H,ceil(Sq/64),max_tiles], entries column << 8 | mask;
     tile_counts: int32 [B,H,ceil(Sq/64)].  queues: run through
     h3a_attn_fwd_blocksparse_tiles_ws (per-XCD work queues, workspace from
     torch's allocator); False runs h3a_attn_fwd_blocksparse_tiles.
@@ -307,7 +307,7 @@ def block_map_to_tile_lut(block_map: torch.Tensor, blk_q: int, blk_k: int, Sq: i
                           max_tiles: int | None = None):
     """0/1 block map [B,H,ceil(Sq/blk_q),ceil(Skv/blk_k)] at block sizes that are multiples of 16
     -> (tile_lut int32 [B,H,ceil(Sq/64),max_tiles], tile_counts int32 [B,H,ceil(Sq/64)]) for
-    attn_fwd_blocksparse_tiles.  max_tiles defaults to ceil(Skv/64), which always suffices."""
+    attn_fwd_blocksparse_tiles.  max_tiles defaults to ceil(Skv/32), which always suffices."""
     blk_q, blk_k = _check_block_size(blk_q), _check_block_size(blk_k)
     if block_map.dim() != 4 or not block_map.is_cuda:
         raise ValueError("block_map must be a 4-D GPU tensor [B,H,nq,nk]")
@@ -315,8 +315,8 @@ def block_map_to_tile_lut(block_map: torch.Tensor, blk_q: int, blk_k: int, Sq: i
     if (nq, nk) != (-(-Sq // blk_q), -(-Skv // blk_k)):
         raise ValueError(f"block_map [.., {nq}, {nk}] does not match Sq={Sq}/blk_q={blk_q}, Skv={Skv}/blk_k={blk_k}")
     m = block_map.to(torch.uint8).contiguous()
-    nstages = -(-Skv // 64)
-    max_tiles = nstages if max_tiles is None else int(max_tiles)
+    ncols = -(-Skv // 32)
+    max_tiles = ncols if max_tiles is None else int(max_tiles)
     nsub = -(-Sq // 64)
     lut = torch.empty((B, H, nsub, max_tiles), dtype=torch.int32, device=m.device)
     counts = torch.empty((B, H, nsub), dtype=torch.int32, device=m.device)

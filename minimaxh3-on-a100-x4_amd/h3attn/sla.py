@@ -129,7 +129,7 @@ def format_summary(sm: dict) -> str:
 # Block sizes (query and key blocks alike): those the h3_sla node offers, 16 to
 # 256 in steps of 16 (custom_nodes/h3_sla/__init__.py:315).  The multiples of
 # the kernels' 64-key stage (ops.NATIVE_BLOCKS) run the native block-sparse
-# kernels; the others run over 64x64 tiles with 16x16 sub-block masks
+# kernels; the others run over 32-key columns with 16x16 sub-block masks
 # (ops.attn_fwd_blocksparse_tiles).  Anything else is refused up front.
 BLOCK_STEP = 16
 SUPPORTED_BLOCKS = tuple(range(16, 257, BLOCK_STEP))

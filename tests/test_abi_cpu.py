@@ -99,16 +99,16 @@ def test_tile_entry_argument_errors():
     assert tiles(lut=None) == _lib.H3A_ERR_INVALID_ARG
     assert tiles(D=64) == _lib.H3A_ERR_UNSUPPORTED
     assert tiles(maxt=0) == _lib.H3A_ERR_INVALID_ARG
-    assert tiles(maxt=6) == _lib.H3A_ERR_INVALID_ARG  # 300 keys = 5 stages of 64
+    assert tiles(maxt=11) == _lib.H3A_ERR_INVALID_ARG  # 300 keys = 10 columns of 32
     assert b"max_tiles" in L.h3a_last_error()
-    assert tiles(Skv=32768 * 64, maxt=1) == _lib.H3A_ERR_UNSUPPORTED  # past 16-bit stage numbers
+    assert tiles(Skv=65535 * 32, maxt=1) == _lib.H3A_ERR_UNSUPPORTED  # past the columns an entry names
     ws = L.h3a_attn_fwd_blocksparse_tiles_ws
     assert ws(16, 16, 16, 16, 1, 1, 300, 300, 128, z, z, z, ROW, None, 16, 1, 0.1, None, 0, None) == \
         _lib.H3A_ERR_INVALID_ARG
     n = ctypes.c_size_t(7)
     assert L.h3a_attn_fwd_blocksparse_tiles_workspace_size(1, 1, 300, 300, 64, 1, ctypes.byref(n)) == \
         _lib.H3A_ERR_UNSUPPORTED
-    assert L.h3a_attn_fwd_blocksparse_tiles_workspace_size(1, 1, 300, 300, 128, 9, ctypes.byref(n)) == \
+    assert L.h3a_attn_fwd_blocksparse_tiles_workspace_size(1, 1, 300, 300, 128, 11, ctypes.byref(n)) == \
         _lib.H3A_ERR_INVALID_ARG
 
     def conv(m=16, bq=32, bk=48, maxt=5, Sq=300, Skv=300):
@@ -117,8 +117,8 @@ def test_tile_entry_argument_errors():
     assert conv(m=None) == _lib.H3A_ERR_INVALID_ARG
     for bq, bk in ((40, 48), (32, 8), (0, 64), (-16, 64)):
         assert conv(bq=bq, bk=bk) == _lib.H3A_ERR_UNSUPPORTED
-    assert conv(maxt=6) == _lib.H3A_ERR_INVALID_ARG
-    assert conv(Skv=32768 * 64, maxt=1) == _lib.H3A_ERR_UNSUPPORTED
+    assert conv(maxt=11) == _lib.H3A_ERR_INVALID_ARG
+    assert conv(Skv=65535 * 32, maxt=1) == _lib.H3A_ERR_UNSUPPORTED
     assert conv(Sq=0) == _lib.H3A_ERR_INVALID_ARG
     assert L.h3a_lut_to_block_map(None, 16, 1, 1, 2, 2, 1, 16, None) == _lib.H3A_ERR_INVALID_ARG
     assert L.h3a_lut_to_block_map(16, 16, 1, 1, 2, 0, 1, 16, None) == _lib.H3A_ERR_INVALID_ARG

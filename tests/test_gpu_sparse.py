@@ -539,26 +539,26 @@ TILE_SIZES = [16, 32, 48, 80, 96, 112, 144, 160, 176, 208, 224, 240]
 
 
 def _tile_lut_np(bmap, blk_q, blk_k, Sq, Skv):
-    """Restatement of the tile LUT on the CPU: per 64-row query sub-block, the ascending 64-key
-    stages with a kept (query block, key block) pair, as stage << 16 | mask with bit 4*i + j for
-    rows 16i.. and keys 16j.. of the tile."""
+    """Restatement of the tile LUT on the CPU: per 64-row query sub-block, the ascending 32-key
+    columns with a kept (query block, key block) pair, as column << 8 | mask with bit 2*i + j
+    for rows 16i.. of the sub-block and keys 16j.. of the column."""
     B, H, nq, nk = bmap.shape
-    nsub, nst = -(-Sq // 64), -(-Skv // 64)
+    nsub, ncol = -(-Sq // 64), -(-Skv // 32)
     rows = {}
     for b, h, qs in np.ndindex(B, H, nsub):
         ents = []
-        for st in range(nst):
+        for c in range(ncol):
             mask = 0
             for i in range(4):
                 r = 64 * qs + 16 * i
                 if r >= Sq:
                     continue
-                for j in range(4):
-                    key = 64 * st + 16 * j
+                for j in range(2):
+                    key = 32 * c + 16 * j
                     if key < Skv and bmap[b, h, r // blk_q, key // blk_k]:
-                        mask |= 1 << (4 * i + j)
+                        mask |= 1 << (2 * i + j)
             if mask:
-                ents.append((st << 16) | mask)
+                ents.append((c << 8) | mask)
         rows[(b, h, qs)] = ents
     return rows
 
