@@ -56,8 +56,8 @@ struct AttnArgs {
 // blk_k / 64 stages.
 inline bool sparse_block_ok(int blk) { return blk == 64 || blk == 128 || blk == 192 || blk == 256; }
 // Block sizes of a block map that h3a_block_map_to_tile_lut converts: any
-// positive multiple of 16 (each 16x16 sub-block of a 64x64 tile then lies in
-// exactly one block pair).
+// positive multiple of 16 (each 16x16 sub-block of a 32-key column then lies
+// in exactly one block pair).
 inline bool tile_block_ok(int blk) { return blk > 0 && blk % 16 == 0; }
 // 32-key columns a tile LUT entry can name (column << 8 | mask stays positive
 // and below 2^24): Skv <= kMaxTileColumns * 32.
@@ -78,8 +78,8 @@ struct SplitPlan {
 int launch_attn_dense(AttnArgs a, hipStream_t s);  // sets nqt/total from its tile height
 int plan_attn_split(int B, int H, int Sq, int Skv, SplitPlan *plan);
 int launch_attn_dense_split(AttnArgs a, const SplitPlan &plan, void *ws, hipStream_t s);
-// tiles: a.lut is a tile LUT (stage << 16 | sub-block mask per entry) over
-// 64-row query sub-blocks and 64-key stages; blk_q is then ignored.
+// tiles: a.lut is a tile LUT (column << 8 | sub-block mask per entry) over
+// 64-row query sub-blocks and 32-key columns; blk_q is then ignored.
 int launch_attn_sparse(const AttnArgs &a, int blk_q, hipStream_t s, bool tiles = false);
 // Block-sparse split tail: pairs of 128-row query blocks play the part of
 // the dense tiles (no split for other block heights).
