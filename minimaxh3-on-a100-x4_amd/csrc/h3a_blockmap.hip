@@ -189,16 +189,18 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
   // stops early once exactly keep keys are >= the candidate c: the kept set
   // is then {keys >= c}, written as T = c - 1, need = 0.
   //
-  // Rows of up to NC*64 key blocks (NC = 6 or 12): the keys of all of this
-  // wave's rows (wave + 4i) sit in registers, NC per lane per row, and the
-  // rows' searches run interleaved, so their 32 dependent counting rounds
-  // overlap.
-  auto select_rows_regs = [&](auto nc_const) __attribute__((always_inline)) {
+  // Rows of up to NC*64 key blocks: the keys of all of this wave's rows
+  // (wave + 4i, i < RPW) sit in registers, NC per lane per row, and the rows'
+  // searches run interleaved, so their 32 dependent counting rounds overlap.
+  // (NC, RPW) = (6, 4), (12, 4), (24, 2) or (48, 1): at most 48 registers of
+  // keys, and the launch gives a workgroup at most 4*RPW rows.
+  auto select_rows_regs = [&](auto nc_const, auto rpw_const) __attribute__((always_inline)) {
     constexpr int NC = decltype(nc_const)::value;
-    uint32_t T[kSelRowsPerWave], kr[kSelRowsPerWave][NC];
-    int need[kSelRowsPerWave];
+    constexpr int RPW = decltype(rpw_const)::value;
+    uint32_t T[RPW], kr[RPW][NC];
+    int need[RPW];
 #pragma unroll
-    for (int i = 0; i < kSelRowsPerWave; ++i) {
+    for (int i = 0; i < RPW; ++i) {
       const int r = wave + 4 * i;
       const float *row_sc = sc + (r < nrows ? r : 0) * nk;
       T[i] = 0;
@@ -216,12 +218,12 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
       return n;
     };
     if (keep > 0) {
-      bool done[kSelRowsPerWave];
+      bool done[RPW];
 #pragma unroll
-      for (int i = 0; i < kSelRowsPerWave; ++i) done[i] = wave + 4 * i >= nrows;
+      for (int i = 0; i < RPW; ++i) done[i] = wave + 4 * i >= nrows;
       for (int bit = 31; bit >= 0; --bit) {
 #pragma unroll
-        for (int i = 0; i < kSelRowsPerWave; ++i) {
+        for (int i = 0; i < RPW; ++i) {
           if (done[i]) continue;
           const uint32_t cand = T[i] | (1u << bit);
           const int n = count_ge(kr[i], cand);
@@ -233,15 +235,15 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
         }
         bool all = true;
 #pragma unroll
-        for (int i = 0; i < kSelRowsPerWave; ++i) all = all && done[i];
+        for (int i = 0; i < RPW; ++i) all = all && done[i];
         if (all) break;
       }
 #pragma unroll
-      for (int i = 0; i < kSelRowsPerWave; ++i)
+      for (int i = 0; i < RPW; ++i)
         need[i] = done[i] ? 0 : keep - (T[i] == 0xffffffffu ? 0 : count_ge(kr[i], T[i] + 1));
     }
 #pragma unroll
-    for (int i = 0; i < kSelRowsPerWave; ++i)
+    for (int i = 0; i < RPW; ++i)
       if (wave + 4 * i < nrows) write_row(wave + 4 * i, T[i], need[i]);
   };
   // Longer rows: one row at a time, keys re-read from LDS every round.
@@ -274,10 +276,17 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
       write_row(r, T, need);
     }
   };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
   if (nchunks <= 6)
-    select_rows_regs(std::integral_constant<int, 6>{});
+    select_rows_regs(std::integral_constant<int, 6>{}, I4{});
   else if (nchunks <= 12)
-    select_rows_regs(std::integral_constant<int, 12>{});
+    select_rows_regs(std::integral_constant<int, 12>{}, I4{});
+  else if (nchunks <= 24 && nrows <= 8)
+    select_rows_regs(std::integral_constant<int, 24>{}, I2{});
+  else if (nchunks <= 48 && nrows <= 4)
+    select_rows_regs(std::integral_constant<int, 48>{}, I1{});
   else
     select_rows_lds();
 }
@@ -392,7 +401,12 @@ int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, 
                         int force_diag, int blk_q, int blk_k, int32_t *lut, int32_t *counts,
                         int max_k, uint8_t *map, hipStream_t s) {
   int rows = kSelScoreBytes / (nk * (int)sizeof(float));
-  rows = rows < 1 ? 1 : (rows > kSelRowsMax ? kSelRowsMax : rows);
+  // Rows of 13-24 or 25-48 chunks of 64 key blocks are selected from
+  // registers with 2 or 1 rows per wave (select_rows_regs): at most 8 or 4
+  // rows per workgroup.
+  const int nchunks = (nk + 63) / 64;
+  const int cap = nchunks <= 12 ? kSelRowsMax : (nchunks <= 24 ? 8 : (nchunks <= 48 ? 4 : kSelRowsMax));
+  rows = rows < 1 ? 1 : (rows > cap ? cap : rows);
   const size_t lds = ((size_t)rows * nk + 1) * sizeof(float);
   const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
   hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)groups), dim3(kSelThreads), lds, s, pq, pk, nq,
