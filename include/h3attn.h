@@ -193,6 +193,12 @@ int h3a_attn_fwd_blocksparse_ws(const void *q, const void *k, const void *v, voi
  * admitted key gets O = 0.  Skv <= 65534 * 32.  max_tiles in
  * [1, ceil(Skv/32)].  Other arguments as h3a_attn_fwd; _ws and
  * _workspace_size as for h3a_attn_fwd_blocksparse_ws (work queues, no split).
+ * The kernel runs two rows (64-row sub-blocks) per workgroup for as many
+ * stages as the longer of the two; h3a_attn_fwd_blocksparse_tiles pairs rows
+ * 2p and 2p+1, the _ws variant pairs them by length (a kernel sorts each
+ * (b,h)'s rows into the workspace first; up to ceil(Sq/64) = 16384, beyond
+ * that as the plain call).  Results are the same bit for bit; the workspace
+ * is never 0 bytes then.
  * No counterpart in the reference's own code: SLA's Triton kernel takes the
  * same block maps at these sizes.
  */

@@ -135,7 +135,7 @@ void fill_attn_args(AttnArgs &a, const void *q, const void *k, const void *v, vo
   a.sl2 = scale * 1.4426950408889634f;
   a.lut = nullptr; a.counts = nullptr; a.lut_stride = 0; a.sub = 1; a.blk_k = 64;
   a.nkb = 0; a.nqb = 0; a.qmul = 1;
-  a.split_first = INT_MAX; a.split_pieces = 1; a.ws = nullptr; a.sched = nullptr;
+  a.split_first = INT_MAX; a.split_pieces = 1; a.ws = nullptr; a.sched = nullptr; a.pair_map = nullptr;
 }
 
 }  // namespace

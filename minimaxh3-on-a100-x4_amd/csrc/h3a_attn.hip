@@ -759,7 +759,22 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
   // wave's 32-row slice of the group's block and kh = 0.
   const int rq = kKeySplit ? (wave_u & 1) : (wave_u & 3);
   const int kh = kKeySplit ? ((wave_u >> 1) & 1) : 0;
-  const int qrow = kSparse ? (2 * qt + grp) * QB + rq * 32 + l32 : qt * 256 + wave * 32 + l32;
+  // Sparse: the pair's query sub-blocks, this group's (qb) and the other
+  // group's (qo): 2qt and 2qt+1, or (tile path) the pair map's, clamped into
+  // [0, nqt] (sub-block nqt is past the end: no rows, no stages).
+  int qb = 2 * qt + grp, qo = 2 * qt + 1 - grp;
+  if constexpr (kTileMask) {
+    if (a.pair_map) {
+      typedef const __attribute__((address_space(4))) int32_t *ConstInts;
+      const ConstInts pm = (ConstInts)a.pair_map + 2 * (int64_t)w;
+      const int m0 = pm[0], m1 = pm[1];
+      const int s0 = m0 < 0 ? 0 : (m0 > a.nqt ? a.nqt : m0);
+      const int s1 = m1 < 0 ? 0 : (m1 > a.nqt ? a.nqt : m1);
+      qb = grp ? s1 : s0;
+      qo = grp ? s0 : s1;
+    }
+  }
+  const int qrow = kSparse ? qb * QB + rq * 32 + l32 : qt * 256 + wave * 32 + l32;
   // Sparse: this group's stage count and LUT row; both groups run the longer
   // of the two lists.  A piece of a split pair runs stages [gj0, gj0 + ngrp)
   // of the group's list.
@@ -783,7 +798,6 @@ __device__ __forceinline__ void pingpong_item(const AttnArgs &a, const int item,
     // stage j's entry is entry block_of_stage(j) of the row, and an entry at
     // or past the end of the list is never used (its stage's key is Skv).
     typedef const __attribute__((address_space(4))) int32_t *ConstInts;
-    const int qb = 2 * qt + grp, qo = 2 * qt + 1 - grp;
     const ConstInts crow = (ConstInts)a.counts + (int64_t)bh * a.nqb;
     const int cnt_own = crow[(qb < a.nqt ? qb : 0) / a.qmul];
     const int cnt_oth = crow[(qo < a.nqt ? qo : 0) / a.qmul];
@@ -1469,6 +1483,54 @@ __global__ void __launch_bounds__(256) block_map_to_lut_kernel(const uint8_t *ma
 }
 
 // ---------------------------------------------------------------------------
+// Pairs of 64-row query sub-blocks for the tile path.  A pair runs as many
+// stages as the longer of its two lists, so a pair of unequal lists leaves
+// one group idle for the difference: with blk_q 80, 96, 112, 144, ... a block
+// boundary falls inside some sub-blocks and not others, and those hold the
+// union of two blocks' lists.  One workgroup per (b,h) sorts its sub-blocks
+// by stage count, descending (ties by index), in LDS (bitonic), and pairs
+// neighbours: map[bh][p] = sorted entries 2p and 2p+1, an odd count pairing
+// the last with sub-block nsub, which has no rows.  Which sub-blocks share a
+// workgroup does not change any row's arithmetic.
+__global__ void __launch_bounds__(1024) tile_pair_map_kernel(const int32_t *counts, int nsub, int lut_stride,
+                                                             int32_t *map) {
+  __shared__ uint32_t key[kPairSortMax];
+  const int tid = threadIdx.x;
+  const int64_t bh = blockIdx.x;
+  int n = 2;
+  while (n < nsub) n <<= 1;
+  const int32_t *c = counts + bh * nsub;
+  for (int i = tid; i < n; i += 1024) {
+    uint32_t kv = 0xffffffffu;  // padding sorts last
+    if (i < nsub) {
+      const int e = c[i] < 0 ? 0 : (c[i] > lut_stride ? lut_stride : c[i]);
+      const uint32_t st = (uint32_t)(e + 1) / 2;  // stages, <= 32767
+      kv = ((0x7fffu - st) << 16) | (uint32_t)i;
+    }
+    key[i] = kv;
+  }
+  __syncthreads();
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < n; i += 1024) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint32_t x = key[i], y = key[l];
+          if ((i & k) == 0 ? x > y : x < y) {
+            key[i] = y;
+            key[l] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const int npairs = (nsub + 1) / 2;
+  int32_t *out = map + bh * npairs * 2;
+  for (int t = tid; t < 2 * npairs; t += 1024) out[t] = t < nsub ? (int32_t)(key[t] & 0xffffu) : nsub;
+}
+
+// ---------------------------------------------------------------------------
 // 32-key score sub-tiles per 64-key stage, in every attention kernel.
 constexpr int kStageSub = kBN / 32;
 
@@ -1547,10 +1609,23 @@ int plan_attn_sparse_split(int B, int H, int Sq, int blk_q, int blk_k, int max_k
 }
 
 // The same for a tile LUT (64-row sub-blocks, unsplit): max_tiles entries
-// stand in for the stage count.
+// stand in for the stage count.  The workspace starts with the pair map
+// (tile_pair_map_kernel; up to kPairSortMax sub-blocks per (b,h), beyond
+// that pairs 2p, 2p+1), then the queue counters.
 int plan_attn_sparse_tiles(int B, int H, int Sq, int max_tiles, SplitPlan *plan) {
   const int64_t nsub = (Sq + 63) / 64;
-  return plan_tiles((int64_t)B * H * ((nsub + 1) / 2), max_tiles, false, true, plan);
+  const int64_t pairs = (int64_t)B * H * ((nsub + 1) / 2);
+  const int rc = plan_tiles(pairs, max_tiles, false, true, plan);
+  if (rc || nsub > kPairSortMax || pairs > INT_MAX) return rc;
+  const size_t map_bytes = (size_t)pairs * 2 * sizeof(int32_t);
+  plan->pair_map = true;
+  if (plan->dynamic) {
+    plan->sched_off = (map_bytes + 255) & ~(size_t)255;
+    plan->bytes = plan->sched_off + kSchedBytes;
+  } else {
+    plan->bytes = map_bytes;
+  }
+  return H3A_OK;
 }
 
 // Workgroups of a persistent launch of `kernel` (512 threads): every CU
@@ -1626,10 +1701,18 @@ static PingPongKernel sparse_pingpong_kernel(const AttnArgs &a, int rows, bool t
 
 int launch_attn_sparse_split(const AttnArgs &a, int blk_q, const SplitPlan &plan, void *ws, hipStream_t s,
                              bool tiles) {
-  if (plan.pieces < 2 && !plan.dynamic) return launch_attn_sparse(a, blk_q, s, tiles);
+  AttnArgs p = a;
+  if (tiles && plan.pair_map) {
+    int32_t *map = static_cast<int32_t *>(ws);
+    hipLaunchKernelGGL(tile_pair_map_kernel, dim3((unsigned)(a.B * a.H)), dim3(1024), 0, s, a.counts, a.nqt,
+                       a.lut_stride, map);
+    const int rc = check_launch("tile_pair_map_kernel");
+    if (rc) return rc;
+    p.pair_map = map;
+  }
+  if (plan.pieces < 2 && !plan.dynamic) return launch_attn_sparse(p, blk_q, s, tiles);
   const int rows = tiles ? 64 : sparse_sub_block_rows(blk_q);
   if (plan.pieces >= 2 && rows != 128) return fail(H3A_ERR_INVALID_ARG, "split plan for 64-row query blocks");
-  AttnArgs p = a;
   if (plan.pieces >= 2) {
     p.split_first = plan.first;
     p.split_pieces = plan.pieces;

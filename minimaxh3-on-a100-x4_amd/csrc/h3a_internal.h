@@ -48,6 +48,9 @@ struct AttnArgs {
   // dynamic dispatch (persistent grid, per-XCD work queues): the queues'
   // counters, zeroed before the launch; null for one work item per workgroup
   int *sched;
+  // tile path: the two 64-row sub-blocks of each pair, [B*H][pairs][2]
+  // (tile_pair_map_kernel), or null for sub-blocks 2p and 2p+1
+  const int32_t *pair_map;
 };
 
 // Block sizes of the block-sparse path: multiples of the 64-key stage up to
@@ -62,6 +65,9 @@ inline bool tile_block_ok(int blk) { return blk > 0 && blk % 16 == 0; }
 // 32-key columns a tile LUT entry can name (column << 8 | mask stays positive
 // and below 2^24): Skv <= kMaxTileColumns * 32.
 constexpr int kMaxTileColumns = 65534;
+// Query sub-blocks per (b,h) whose pairing by stage count is sorted in one
+// workgroup's LDS (tile path; longer sequences pair sub-blocks 2p, 2p+1).
+constexpr int kPairSortMax = 16384;
 inline int sparse_sub_block_rows(int blk_q) { return blk_q % 128 == 0 ? 128 : 64; }
 
 // Dense split-tail plan for a problem on the current device.
@@ -72,6 +78,7 @@ struct SplitPlan {
   size_t bytes; // workspace bytes (split partials, then the queue counters)
   bool dynamic; // persistent grid with per-XCD work queues
   size_t sched_off;  // byte offset of the queue counters in the workspace
+  bool pair_map;     // tile path: sub-blocks paired by stage count (map at offset 0)
 };
 
 // Launchers implemented in h3a_attn.hip / h3a_prologue.hip.
