@@ -259,7 +259,9 @@ def attn_fwd_blocksparse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lut:
 
 
 def tiles_workspace_bytes(B: int, H: int, Sq: int, Skv: int, max_tiles: int, D: int = HEAD_DIM) -> int:
-    """Workspace bytes h3a_attn_fwd_blocksparse_tiles_ws needs on the current device (0: none)."""
+    """Workspace bytes h3a_attn_fwd_blocksparse_tiles_ws needs on the current device: the pair map
+    (8 bytes per pair of 64-row sub-blocks, up to 16384 sub-blocks per (b,h)) and the work-queue
+    counters of a persistent launch (0: neither)."""
     n = ctypes.c_size_t(0)
     check("h3a_attn_fwd_blocksparse_tiles_workspace_size",
           lib().h3a_attn_fwd_blocksparse_tiles_workspace_size(B, H, Sq, Skv, D, int(max_tiles), ctypes.byref(n)))
@@ -273,8 +275,10 @@ def attn_fwd_blocksparse_tiles(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
 
     tile_lut: int32 [B,H,ceil(Sq/64),max_tiles], entries column << 8 | mask;
     tile_counts: int32 [B,H,ceil(Sq/64)].  queues: run through
-    h3a_attn_fwd_blocksparse_tiles_ws (per-XCD work queues, workspace from
-    torch's allocator); False runs h3a_attn_fwd_blocksparse_tiles.
+    h3a_attn_fwd_blocksparse_tiles_ws (64-row sub-blocks paired by stage count,
+    per-XCD work queues, workspace from torch's allocator); False runs
+    h3a_attn_fwd_blocksparse_tiles (sub-blocks 2p and 2p+1 paired).  Both give
+    the same output bit for bit.
     """
     q, k, v, out, (B, H, Sq, Skv, D) = _prepare_attn(q, k, v, out)
     nsub = -(-Sq // 64)
