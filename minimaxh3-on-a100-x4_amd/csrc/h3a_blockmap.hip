@@ -66,8 +66,18 @@ constexpr int kSelRowsPerWave = 4;
 constexpr int kSelRowsMax = kSelRowsPerWave * (kSelThreads / 64);  // query blocks per workgroup
 // LDS per workgroup caps the score rows (R rows of nk floats, plus one spare
 // float) at 40 KiB, so that four workgroups fit on a CU: 16 rows up to
-// nk = 639, 15 at 659, 10 at 1000, 1 at the 7000 maximum.
+// nk = 639, 15 at 659, 4 at 2000, 1 at the 7000 maximum.
 constexpr int kSelScoreBytes = 40960 - 4;
+// Rows of 1025 to 3072 key blocks (17 to 48 chunks of 64) run in one
+// 16-wave workgroup per CU instead, one row per wave with its keys in
+// registers, over static LDS for up to 16 rows of scores (16 rows up to
+// nk = 2499, 15 at 2633, 13 at 3072), so that the head's pooled keys are
+// read once per 13-16 rows instead of once per 3-8.  Below 1025 key blocks
+// four workgroups per CU measured faster: one workgroup's score phase then
+// overlaps another's selection.
+constexpr int kSelWideWaves = 16;
+constexpr int kSelWideMinChunks = 17;
+constexpr int kSelWideScoreFloats = 40000;
 constexpr int kSelKeyTile = 16;  // key blocks per score tile (one MFMA output tile)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -80,21 +90,32 @@ __device__ __forceinline__ void load_score_operand(f32x4 (&x)[8], const float *r
   for (int j = 0; j < 8; ++j) x[j] = *(const f32x4 *)(row + 16 * j + 4 * slot);
 }
 
-// R (<= kSelRowsMax = 16) query blocks of one (b,h) per workgroup, so each
-// pooled key vector is read from memory once per R rows.  Scores: the 16
-// rows x 16 key blocks of a tile are one chain of 32 v_mfma_f32_16x16x4f32
-// (fp32 products and sums); wave w takes key tiles w, w+4, ..., its pooled
-// keys loaded straight into registers one tile ahead, and writes the tile's
-// scores to LDS.  Then wave
-// w selects rows w, w+4, ..., with lane l on key blocks j = 64c + l: a bitwise
+// R (<= kSelRowsMax = 16) query blocks of one (b,h) per workgroup of NW
+// waves, so each pooled key vector is read from memory once per R rows.
+// Scores: the 16 rows x 16 key blocks of a tile are one chain of 32
+// v_mfma_f32_16x16x4f32 (fp32 products and sums); wave w takes key tiles w,
+// w+NW, ..., its pooled keys loaded straight into registers one tile ahead,
+// and writes the tile's scores to LDS.  Then wave
+// w selects rows w, w+NW, ..., with lane l on key blocks j = 64c + l: a bitwise
 // search over order-preserving keys finds the row's keep-th largest score in
 // 32 counting rounds (ballot + popcount), which fixes the kept set under
 // (score desc, index asc) order without ranking every pair.  Kept indices are
 // written in ascending order with one ballot per 64-key chunk.
-__global__ void __launch_bounds__(kSelThreads) block_select_kernel(
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) block_select_kernel(
     const float *pq, const float *pk, int nq, int nk, int rows_per_wg, int keep, int force_diag,
     int blk_q, int blk_k, int32_t *lut, int32_t *counts, int max_k, uint8_t *map) {
-  extern __shared__ float sc[];  // [R][nk] scores, then one spare slot
+  static_assert(NW == kSelThreads / 64 || NW == kSelWideWaves, "a 4-wave or a 16-wave workgroup");
+  // [R][nk] scores, then one spare slot: dynamic LDS (4 waves), or static
+  // LDS sized for the longest rows of the 16-wave form.
+  float *sc;
+  if constexpr (NW == kSelWideWaves) {
+    __shared__ float sc_wide[kSelWideScoreFloats];
+    sc = sc_wide;
+  } else {
+    extern __shared__ float sc_dyn[];
+    sc = sc_dyn;
+  }
   // The wave index as a scalar, so the loops over a wave's tiles and rows are uniform.
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R = rows_per_wg;
@@ -138,13 +159,13 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
   // scheduling barriers keep the loads ahead of the MFMA chain they overlap).
   f32x4 k0[8], k1[8];
   load_score_operand(k0, key_row(wave < ntiles ? wave : ntiles - 1), slot);
-  for (int t = wave; t < ntiles; t += 8) {
-    load_score_operand(k1, key_row(t + 4 < ntiles ? t + 4 : ntiles - 1), slot);
+  for (int t = wave; t < ntiles; t += 2 * NW) {
+    load_score_operand(k1, key_row(t + NW < ntiles ? t + NW : ntiles - 1), slot);
     __builtin_amdgcn_sched_barrier(0);
     score_tile(t, k0);
-    load_score_operand(k0, key_row(t + 8 < ntiles ? t + 8 : ntiles - 1), slot);
+    load_score_operand(k0, key_row(t + 2 * NW < ntiles ? t + 2 * NW : ntiles - 1), slot);
     __builtin_amdgcn_sched_barrier(0);
-    if (t + 4 < ntiles) score_tile(t + 4, k1);
+    if (t + NW < ntiles) score_tile(t + NW, k1);
   }
   __syncthreads();
 
@@ -190,10 +211,11 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
   // is then {keys >= c}, written as T = c - 1, need = 0.
   //
   // Rows of up to NC*64 key blocks: the keys of all of this wave's rows
-  // (wave + 4i, i < RPW) sit in registers, NC per lane per row, and the rows'
-  // searches run interleaved, so their 32 dependent counting rounds overlap.
-  // (NC, RPW) = (6, 4), (12, 4), (24, 2) or (48, 1): at most 48 registers of
-  // keys, and the launch gives a workgroup at most 4*RPW rows.
+  // (wave + NW*i, i < RPW) sit in registers, NC per lane per row, and the
+  // rows' searches run interleaved, so their 32 dependent counting rounds
+  // overlap.  (NC, RPW) = (6, 4), (12, 4) or (24, 2) with 4 waves (the launch
+  // gives a workgroup at most 8 rows for the last), (24, 1) or (48, 1) with
+  // 16: at most 48 registers of keys.
   auto select_rows_regs = [&](auto nc_const, auto rpw_const) __attribute__((always_inline)) {
     constexpr int NC = decltype(nc_const)::value;
     constexpr int RPW = decltype(rpw_const)::value;
@@ -201,7 +223,7 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     int need[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-      const int r = wave + 4 * i;
+      const int r = wave + NW * i;
       const float *row_sc = sc + (r < nrows ? r : 0) * nk;
       T[i] = 0;
       need[i] = 0;
@@ -220,7 +242,7 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     if (keep > 0) {
       bool done[RPW];
 #pragma unroll
-      for (int i = 0; i < RPW; ++i) done[i] = wave + 4 * i >= nrows;
+      for (int i = 0; i < RPW; ++i) done[i] = wave + NW * i >= nrows;
       for (int bit = 31; bit >= 0; --bit) {
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
@@ -244,11 +266,11 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
     }
 #pragma unroll
     for (int i = 0; i < RPW; ++i)
-      if (wave + 4 * i < nrows) write_row(wave + 4 * i, T[i], need[i]);
+      if (wave + NW * i < nrows) write_row(wave + NW * i, T[i], need[i]);
   };
   // Longer rows: one row at a time, keys re-read from LDS every round.
   auto select_rows_lds = [&]() __attribute__((always_inline)) {
-    for (int r = wave; r < nrows; r += kSelThreads / 64) {
+    for (int r = wave; r < nrows; r += NW) {
       const float *row_sc = sc + r * nk;
       auto count_ge = [&](uint32_t t) __attribute__((always_inline)) -> int {
         int n = 0;
@@ -279,16 +301,23 @@ __global__ void __launch_bounds__(kSelThreads) block_select_kernel(
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I4 = std::integral_constant<int, 4>;
-  if (nchunks <= 6)
-    select_rows_regs(std::integral_constant<int, 6>{}, I4{});
-  else if (nchunks <= 12)
-    select_rows_regs(std::integral_constant<int, 12>{}, I4{});
-  else if (nchunks <= 24 && nrows <= 8)
-    select_rows_regs(std::integral_constant<int, 24>{}, I2{});
-  else if (nchunks <= 48 && nrows <= 4)
-    select_rows_regs(std::integral_constant<int, 48>{}, I1{});
-  else
-    select_rows_lds();
+  if constexpr (NW == kSelWideWaves) {
+    if (nchunks <= 24 && nrows <= NW)
+      select_rows_regs(std::integral_constant<int, 24>{}, I1{});
+    else if (nchunks <= 48 && nrows <= NW)
+      select_rows_regs(std::integral_constant<int, 48>{}, I1{});
+    else
+      select_rows_lds();
+  } else {
+    if (nchunks <= 6)
+      select_rows_regs(std::integral_constant<int, 6>{}, I4{});
+    else if (nchunks <= 12)
+      select_rows_regs(std::integral_constant<int, 12>{}, I4{});
+    else if (nchunks <= 24 && nrows <= 8)
+      select_rows_regs(std::integral_constant<int, 24>{}, I2{});
+    else
+      select_rows_lds();
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -400,17 +429,24 @@ int launch_block_pool(const uint16_t *x, const int64_t st[3], int B, int H, int 
 int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, int nk, int keep,
                         int force_diag, int blk_q, int blk_k, int32_t *lut, int32_t *counts,
                         int max_k, uint8_t *map, hipStream_t s) {
-  int rows = kSelScoreBytes / (nk * (int)sizeof(float));
-  // Rows of 13-24 or 25-48 chunks of 64 key blocks are selected from
-  // registers with 2 or 1 rows per wave (select_rows_regs): at most 8 or 4
-  // rows per workgroup.
   const int nchunks = (nk + 63) / 64;
-  const int cap = nchunks <= 12 ? kSelRowsMax : (nchunks <= 24 ? 8 : (nchunks <= 48 ? 4 : kSelRowsMax));
+  if (nchunks >= kSelWideMinChunks && nchunks <= 48) {
+    int rows = (kSelWideScoreFloats - 1) / nk;
+    rows = rows > kSelRowsMax ? kSelRowsMax : rows;  // >= 13 for nk <= 3072
+    const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
+    hipLaunchKernelGGL(block_select_kernel<kSelWideWaves>, dim3((unsigned)groups), dim3(kSelWideWaves * 64), 0,
+                       s, pq, pk, nq, nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);
+    return check_launch("block_select_kernel<16 waves>");
+  }
+  // Rows of 13-16 chunks are selected from registers, 2 per wave: at most 8
+  // rows per workgroup.
+  const int cap = nchunks > 12 ? 8 : kSelRowsMax;
+  int rows = kSelScoreBytes / (nk * (int)sizeof(float));
   rows = rows < 1 ? 1 : (rows > cap ? cap : rows);
   const size_t lds = ((size_t)rows * nk + 1) * sizeof(float);
   const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
-  hipLaunchKernelGGL(block_select_kernel, dim3((unsigned)groups), dim3(kSelThreads), lds, s, pq, pk, nq,
-                     nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);
+  hipLaunchKernelGGL(block_select_kernel<kSelThreads / 64>, dim3((unsigned)groups), dim3(kSelThreads), lds, s,
+                     pq, pk, nq, nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);
   return check_launch("block_select_kernel");
 }
 

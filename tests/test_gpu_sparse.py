@@ -456,19 +456,22 @@ def _select_ref(pq, pk, keep, blk_q, blk_k, diag, max_k):
 @pytest.mark.parametrize("nq,nk,keep,diag,max_k", [
     (9, 700, 37, True, 38), (17, 65, 1, False, 1), (1, 64, 64, False, 64), (9, 1, 1, True, 1),
     (17, 700, 100, True, 50), (16, 200, 20, False, 20), (5, 384, 96, True, 97),
-    (3, 769, 10, False, 10), (5, 1000, 150, True, 151), (9, 1536, 200, True, 201),
-    (5, 1537, 30, False, 30), (6, 2500, 300, True, 301), (4, 3072, 64, False, 64),
+    (3, 769, 10, False, 10), (5, 1000, 150, True, 151), (17, 1024, 100, True, 101),
+    (17, 1025, 60, False, 60), (9, 1536, 200, True, 201), (5, 1537, 30, False, 30),
+    (33, 2000, 90, True, 91), (6, 2500, 300, True, 301), (4, 3072, 64, False, 64),
     (4, 3073, 10, True, 11), (3, 5000, 40, True, 41), (2, 7000, 100, False, 100)])
 def test_block_select_exact_ties(gpu, nq, nk, keep, diag, max_k):
     """Integer pooled vectors make every score an exact fp32 integer, with many ties:
     the kept set, its order and the truncation to max_k_blocks must match exactly.
     Covers row groups of up to 16 query blocks per workgroup (fewer where the score
-    rows fill LDS or the register paths cap them: 14 at nk 700, 8 at nk 769-1536, 4 at
-    1537-3072, 3 at 3073, 2 at 5000, 1 at the 7000 maximum; the score MFMAs' rows past
-    a group's end are computed and dropped), key tiles past nk (nk 65, 1, 769, 1000,
-    1537, 2500, 3073), and all five counting paths: keys held in registers, 4 rows per
-    wave in 6 (nk <= 384) or 12 (nk <= 768), 2 rows in 24 (nk <= 1536), 1 row in 48
-    (nk <= 3072), and re-read from LDS (3073 and above), each at its boundaries."""
+    rows fill LDS or the register paths cap them: 14 at nk 700, 8 at nk 769-1024, 16 at
+    1025-2499 and 13 at 3072 in the 16-wave form, 3 at 3073, 2 at 5000, 1 at the 7000
+    maximum; the score MFMAs' rows past a group's end are computed and dropped), partial
+    last groups (nq 17, 33), key tiles past nk (nk 65, 1, 769, 1000, 1025, 1537, 2500,
+    3073), and all five counting paths: keys held in registers, 4 rows per wave in 6
+    (nk <= 384) or 12 (nk <= 768), 2 rows in 24 (nk <= 1024), 1 row per wave of a
+    16-wave workgroup in 24 (nk 1025-1536) or 48 (nk 1537-3072), and re-read from LDS
+    (3073 and above), each at its boundaries."""
     rng = np.random.default_rng(50 + nq + nk)
     pq = rng.integers(-2, 3, (1, 2, nq, 128)).astype(np.float32)
     pk = rng.integers(-2, 3, (1, 2, nk, 128)).astype(np.float32)
