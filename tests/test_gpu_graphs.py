@@ -57,23 +57,26 @@ def test_graph_replay_matches_eager(gpu):
             assert torch.equal(o, w), f"replay {r}, layer {i} differs from the eager run"
 
 
-def test_graph_capture_of_wide_block_select(gpu):
-    """Block select over 700 key blocks per row (44 score tiles per row, 14 query blocks
-    per workgroup, keys counted in 12 registers per lane): captured into a graph, every
-    replay equals the eager call."""
+@pytest.mark.parametrize("nk", [700, 2000])
+def test_graph_capture_of_wide_block_select(gpu, nk):
+    """Block select over long rows: 700 key blocks (44 score tiles per row, 14 query blocks
+    per 4-wave workgroup, keys counted in 12 registers per lane) and 2000 (the 16-wave
+    workgroup over static LDS, 16 query blocks each, 48 registers per lane): captured into
+    a graph, every replay equals the eager call."""
     g = torch.Generator(device=gpu).manual_seed(41)
     pq = torch.randn(1, 2, 20, 128, generator=g, device=gpu)
-    pk = torch.randn(1, 2, 700, 128, generator=g, device=gpu)
-    want = [t.clone() for t in ops.block_select(pq, pk, 175, 64, 64)]
+    pk = torch.randn(1, 2, nk, 128, generator=g, device=gpu)
+    keep = nk // 4
+    want = [t.clone() for t in ops.block_select(pq, pk, keep, 64, 64)]
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        ops.block_select(pq, pk, 175, 64, 64)  # warm-up off the default stream
+        ops.block_select(pq, pk, keep, 64, 64)  # warm-up off the default stream
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        outs = ops.block_select(pq, pk, 175, 64, 64)
+        outs = ops.block_select(pq, pk, keep, 64, 64)
     other = torch.randn(1, 2, 300, 128, device=gpu, dtype=torch.bfloat16)
     for r in range(3):
         h3attn.attn_fwd(other, other, other)  # unrelated eager work between replays
