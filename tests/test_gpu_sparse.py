@@ -669,28 +669,37 @@ def test_sparse_tiles_pair_map(gpu, H, S, blk):
     assert_close_absmax(got, ref, what=f"tiles pair map blk {blk}")
 
 
-def test_sparse_tiles_pair_map_limit(gpu):
+@pytest.mark.parametrize("extra", [0, 1])
+def test_sparse_tiles_pair_map_limit(gpu, extra):
     """Up to 16384 sub-blocks per (b,h) the workspace holds the pair map (8 bytes a pair) and
-    the queue counters; one more and the pairs stay consecutive (counters only).  The call
-    just past the limit (S = 64 * 16384 + 1, one column per sub-block: its own diagonal 32
-    keys, rows 64s .. 64s+31 only) runs and matches fp32 attention on rows of the first,
-    a middle and the last sub-block."""
+    the queue counters; one more and the pairs stay consecutive (counters only).  At the
+    limit (S = 64 * 16384, the sort over 16384 sub-blocks of random lengths) and just past
+    it (S = 64 * 16384 + 1), the queued call equals the plain one bit for bit and fp32
+    attention on rows of the first, a middle and the last sub-block.  Sub-block s lists
+    its own diagonal column 2s with rows 0-31 admitted, and 0-3 more columns 2s+1 .. with
+    no row admitted (they load and mask a whole column), so list lengths differ."""
     lim = 64 * 16384
-    with_map = ops.tiles_workspace_bytes(1, 1, lim, lim, 1)
-    assert with_map >= 8 * 8192
-    S = lim + 1
-    without = ops.tiles_workspace_bytes(1, 1, S, S, 1)
-    assert 0 < without < 8 * 8192
+    S = lim + extra
+    nbytes = ops.tiles_workspace_bytes(1, 1, S, S, 4)
+    if extra:
+        assert 0 < nbytes < 8 * 8192
+    else:
+        assert nbytes >= 8 * 8192
     nsub = -(-S // 64)
-    g = torch.Generator(device=gpu).manual_seed(17)
+    g = torch.Generator(device=gpu).manual_seed(17 + extra)
     q, k, v = (torch.randn(1, 1, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
-    sb = torch.arange(nsub, device=gpu, dtype=torch.int32)
-    # column 2s, mask bits 0-3: rows 0-31 of the sub-block against the column's 32 keys
-    lut = ((2 * sb) << 8 | 0xf).view(1, 1, nsub, 1).contiguous()
-    cnt = torch.ones(1, 1, nsub, dtype=torch.int32, device=gpu)
-    o = torch.full_like(q, 7.0)
-    ops.attn_fwd_blocksparse_tiles(q, k, v, lut, cnt, out=o, queues=True)
+    sb = torch.arange(nsub, device=gpu, dtype=torch.int32).view(1, 1, nsub, 1)
+    ncol = -(-S // 32)
+    cols = torch.clamp(2 * sb + torch.arange(4, device=gpu, dtype=torch.int32).view(1, 1, 1, 4), max=ncol - 1)
+    lut = (cols << 8).contiguous()
+    lut[..., 0] |= 0xf  # the diagonal column: rows 0-31 of the sub-block against its 32 keys
+    cnt = torch.randint(1, 5, (1, 1, nsub), generator=g, device=gpu, dtype=torch.int32)
+    a = torch.full_like(q, 7.0)
+    b = torch.full_like(q, -7.0)
+    ops.attn_fwd_blocksparse_tiles(q, k, v, lut, cnt, out=a, queues=True)
+    ops.attn_fwd_blocksparse_tiles(q, k, v, lut, cnt, out=b, queues=False)
     torch.cuda.synchronize()
+    assert torch.equal(a, b)
     scale = 1.0 / math.sqrt(128)
     for s in (0, nsub // 2, nsub - 1):
         r0 = 64 * s
@@ -698,10 +707,10 @@ def test_sparse_tiles_pair_map_limit(gpu):
         kk, vv = k[0, 0, r0:r0 + 32].float(), v[0, 0, r0:r0 + 32].float()
         p = torch.softmax((q[0, 0, r0:r0 + rows].float() @ kk.t().contiguous()) * scale, -1)
         ref = p @ vv
-        got = o[0, 0, r0:r0 + rows].float()
+        got = a[0, 0, r0:r0 + rows].float()
         assert (got - ref).abs().max().item() <= 2e-2 * ref.abs().max().item() + 1e-3, s
-        if s < nsub - 1:  # rows 32-63 see no key: O = 0
-            assert torch.count_nonzero(o[0, 0, r0 + 32:r0 + 64]).item() == 0
+        if r0 + 32 < S:  # rows 32-63 see no key: O = 0
+            assert torch.count_nonzero(a[0, 0, r0 + 32:r0 + 64]).item() == 0
 
 
 def test_sparse_tiles_queued_matches_static(gpu):
