@@ -30,6 +30,7 @@ FLOP_PER_CLK = 256 * 4096  # dense bf16 MFMA, whole chip
 # "roofline.traffic = <bytes> B" is read at run time.
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_h56_s42120_counters.txt")
 SPARSE_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_sparse_h56_s42120_counters.txt")
+TILES_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_tiles_h56_s42120_counters.txt")
 PROLOGUE_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "prologue_s8192_h56.txt")
 B, H, S, D, LAYERS = 1, 56, 42120, 128, 50
 
@@ -359,7 +360,7 @@ def run_sparse(args, torch, h3attn, dev):
                 {"workload": f"block-sparse attention, {L} layers per step", "B": B, "H": H, "S": S,
                  "D": D, "blk_q": blk, "blk_k": blk,
                  "keep": f"{int(0.25 * nk)} of {nk} key tiles + diagonal"})
-    traffic, traffic_src = measured_traffic(SPARSE_TRAFFIC_SUMMARY, f"sparse{blk}")
+    traffic, traffic_src = measured_traffic(TILES_TRAFFIC_SUMMARY if tiles else SPARSE_TRAFFIC_SUMMARY, f"sparse{blk}")
     res.update({
         "ms_per_layer": round(avg_kernel_ms, 3),
         "kept_fraction": round(flops / flops_per_layer(), 4),
