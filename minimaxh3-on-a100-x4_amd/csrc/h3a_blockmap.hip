@@ -66,7 +66,8 @@ constexpr int kSelRowsPerWave = 4;
 constexpr int kSelRowsMax = kSelRowsPerWave * (kSelThreads / 64);  // query blocks per workgroup
 // LDS per workgroup caps the score rows (R rows of nk floats, plus one spare
 // float) at 40 KiB, so that four workgroups fit on a CU: 16 rows up to
-// nk = 639, 15 at 659, 4 at 2000, 1 at the 7000 maximum.
+// nk = 639, 15 at 659, 8 from 769 to 1024 (the register path's cap), 3 at
+// 3073, 1 at the 7000 maximum.
 constexpr int kSelScoreBytes = 40960 - 4;
 // Rows of 1025 to 3072 key blocks (17 to 48 chunks of 64) run in one
 // 16-wave workgroup per CU instead, one row per wave with its keys in
