@@ -453,6 +453,30 @@ def _select_ref(pq, pk, keep, blk_q, blk_k, diag, max_k):
     return bmap, lut, cnt
 
 
+@pytest.mark.parametrize("nq,nk,diag", [(40, 1025, True), (33, 2633, False), (17, 3072, True)])
+def test_block_select_long_rows_real_scores(gpu, nq, nk, diag):
+    """Rows of 1025-3072 key blocks (the 16-wave workgroup) on real-valued pooled vectors
+    against a float64 selection: the kept set may differ only where a score is within
+    fp32 rounding of the keep-th largest; the LUT and counts follow the map."""
+    rng = np.random.default_rng(nq + nk)
+    keep = nk // 4
+    pq = rng.standard_normal((1, 2, nq, 128)).astype(np.float32)
+    pk = rng.standard_normal((1, 2, nk, 128)).astype(np.float32)
+    bmap, lut, cnt = ops.block_select(torch.from_numpy(pq).to(gpu), torch.from_numpy(pk).to(gpu), keep,
+                                      16, 16, force_diag=diag)
+    rmap, _, _ = _select_ref(pq, pk, keep, 16, 16, diag, lut.shape[-1])
+    got = bmap.cpu().numpy()
+    sc = np.einsum("bhid,bhjd->bhij", pq.astype(np.float64), pk.astype(np.float64))
+    diff = np.argwhere(got != rmap)
+    assert len(diff) <= 4 * nq, len(diff)
+    for b, h, i, j in diff:
+        thr = np.sort(sc[b, h, i])[::-1][keep - 1]
+        assert abs(sc[b, h, i, j] - thr) <= 1e-4 * max(1.0, abs(thr)), (b, h, i, j)
+    rl, rc = _lut_np(got, lut.shape[-1])
+    assert np.array_equal(cnt.cpu().numpy(), rc)
+    assert np.array_equal(lut.cpu().numpy(), rl)
+
+
 @pytest.mark.parametrize("nq,nk,keep,diag,max_k", [
     (9, 700, 37, True, 38), (17, 65, 1, False, 1), (1, 64, 64, False, 64), (9, 1, 1, True, 1),
     (17, 700, 100, True, 50), (16, 200, 20, False, 20), (5, 384, 96, True, 97),
