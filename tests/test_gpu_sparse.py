@@ -661,35 +661,36 @@ def test_sla_sparse_attention_at_tile_sizes(gpu, blk):
     assert_close_absmax(got, ref, what=f"sla blk={blk}")
 
 
-@pytest.mark.parametrize("H,S,blk", [(2, 1950, 96), (3, 4100, 80), (40, 8192, 112), (1, 64, 48)])
-def test_sparse_tiles_pair_map(gpu, H, S, blk):
+@pytest.mark.parametrize("B,H,S,blk", [(1, 2, 1950, 96), (1, 3, 4100, 80), (1, 40, 8192, 112), (1, 1, 64, 48),
+                                       (3, 2, 3000, 144)])
+def test_sparse_tiles_pair_map(gpu, B, H, S, blk):
     """The workspace entry point pairs 64-row sub-blocks by stage count (tile_pair_map_kernel);
     the plain one pairs 2p and 2p+1.  Every row's arithmetic is the same either way, so the two
     outputs are equal bit for bit, over outputs pre-filled with different values so that a
     sub-block left out or run twice shows.  Block heights that put block boundaries inside
-    some sub-blocks (80, 96, 112: lists of unequal length), an odd sub-block count (1950: 31,
-    64: 1), a static launch with the map and a queued one (H=40, S=8192), and the masked
-    oracle on the first 192 rows of one head."""
+    some sub-blocks (80, 96, 112, 144: lists of unequal length), an odd sub-block count (1950:
+    31, 64: 1), a static launch with the map and a queued one (H=40, S=8192), B=3, and the
+    masked oracle on the first 192 rows of one head of the last batch."""
     rng = np.random.default_rng(90 + blk)
     g = torch.Generator(device=gpu).manual_seed(90 + blk)
-    q, k, v = (torch.randn(1, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    q, k, v = (torch.randn(B, H, S, 128, generator=g, device=gpu, dtype=torch.bfloat16) for _ in range(3))
     nb = -(-S // blk)
-    bmap_np = (rng.random((1, H, nb, nb)) < 0.25).astype(np.uint8)
+    bmap_np = (rng.random((B, H, nb, nb)) < 0.25).astype(np.uint8)
     bmap_np[..., np.arange(nb), np.arange(nb)] = 1
     tlut, tcnt = ops.block_map_to_tile_lut(torch.from_numpy(bmap_np).to(gpu), blk, blk, S, S)
     nsub = -(-S // 64)
-    assert ops.tiles_workspace_bytes(1, H, S, S, tlut.shape[3]) >= 8 * H * ((nsub + 1) // 2)
+    assert ops.tiles_workspace_bytes(B, H, S, S, tlut.shape[3]) >= 8 * B * H * ((nsub + 1) // 2)
     a = torch.full_like(q, 1000.0)
     b = torch.full_like(q, -1000.0)
     ops.attn_fwd_blocksparse_tiles(q, k, v, tlut, tcnt, out=a, queues=True)
     ops.attn_fwd_blocksparse_tiles(q, k, v, tlut, tcnt, out=b, queues=False)
     assert torch.equal(a, b)
-    h, rows = H - 1, min(192, S)
+    bb, h, rows = B - 1, H - 1, min(192, S)
     nr = -(-rows // blk)
-    qh = from_dev_bf16(q[:, h:h + 1, :rows])
-    kh, vh = (from_dev_bf16(t[:, h:h + 1]) for t in (k, v))
-    ref = oracle.attn_fwd(qh, kh, vh, block_map=bmap_np[:, h:h + 1, :nr], blk_q=blk, blk_k=blk)
-    got = oracle.bf16_to_f32(from_dev_bf16(a[:, h:h + 1, :rows])).reshape(ref.shape)
+    qh = from_dev_bf16(q[bb:bb + 1, h:h + 1, :rows])
+    kh, vh = (from_dev_bf16(t[bb:bb + 1, h:h + 1]) for t in (k, v))
+    ref = oracle.attn_fwd(qh, kh, vh, block_map=bmap_np[bb:bb + 1, h:h + 1, :nr], blk_q=blk, blk_k=blk)
+    got = oracle.bf16_to_f32(from_dev_bf16(a[bb:bb + 1, h:h + 1, :rows])).reshape(ref.shape)
     assert_close_absmax(got, ref, what=f"tiles pair map blk {blk}")
 
 
