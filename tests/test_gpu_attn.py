@@ -245,11 +245,11 @@ def test_full_h3_shape(gpu, H):
 def test_concurrent_host_threads_on_separate_streams(gpu):
     """Two host threads, each on its own stream, run queued dense and block-sparse
     launches at once (each call has its own workspace from torch's allocator on its
-    stream, so its own queue counters and split partials).  Every result equals the
-    same call made alone, bit for bit."""
+    stream, so its own queue counters, split partials and tile pair map).  Every result
+    equals the same call made alone, bit for bit."""
     import threading
 
-    from h3attn import sla
+    from h3attn import ops, sla
 
     g = torch.Generator(device=gpu).manual_seed(21)
     H, S = 16, 16384  # 16 x 64 = 1024 dense tiles: a queued persistent launch
@@ -257,6 +257,9 @@ def test_concurrent_host_threads_on_separate_streams(gpu):
               for _ in range(2)]
     maps = [{blk: sla.get_block_map(q, k, 0.25, blk, blk, force_diag=True, want_map=False)[1:]
              for blk in (128, 64)} for q, k, _ in inputs]
+    for i, (q, k, _) in enumerate(inputs):  # the tile path at 96x96 blocks
+        bmap = sla.get_block_map(q, k, 0.25, 96, 96, force_diag=True, want_map=True)[0]
+        maps[i][96] = ops.block_map_to_tile_lut(bmap, 96, 96, S, S)
 
     def calls(i):
         q, k, v = inputs[i]
@@ -264,6 +267,7 @@ def test_concurrent_host_threads_on_separate_streams(gpu):
         for blk in (128, 64):
             lut, cnt = maps[i][blk]
             outs.append(h3attn.attn_fwd_blocksparse(q, k, v, lut, cnt, blk, blk))
+        outs.append(ops.attn_fwd_blocksparse_tiles(q, k, v, *maps[i][96], queues=True))
         return outs
 
     alone = []
@@ -285,7 +289,7 @@ def test_concurrent_host_threads_on_separate_streams(gpu):
         except Exception as e:  # surfaced in the main thread below
             errors.append(e)
 
-    print("[threads] 2 host threads x 3 rounds of dense + sparse 128/64 at H=16 S=16384", flush=True)
+    print("[threads] 2 host threads x 3 rounds of dense + sparse 128/64/96 at H=16 S=16384", flush=True)
     threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
     for t in threads:
         t.start()
