@@ -64,20 +64,22 @@ __global__ void __launch_bounds__(256) block_pool_kernel(const uint16_t *x, int6
 constexpr int kSelThreads = 256;
 constexpr int kSelRowsPerWave = 4;
 constexpr int kSelRowsMax = kSelRowsPerWave * (kSelThreads / 64);  // query blocks per workgroup
-// LDS per workgroup caps the score rows (R rows of nk floats, plus one spare
-// float) at 40 KiB, so that four workgroups fit on a CU: 16 rows up to
-// nk = 639, 15 at 659, 8 from 769 to 1024 (the register path's cap), 3 at
-// 3073, 1 at the 7000 maximum.
+// Rows of up to 768 key blocks (12 chunks of 64) and of more than 3072 run in
+// 4-wave workgroups whose dynamic LDS caps the score rows (R rows of nk floats,
+// plus one spare float) at 40 KiB, so that four workgroups fit on a CU: 16
+// rows up to nk = 639, 15 at 659, 3 at 3073, 1 at the 7000 maximum.
 constexpr int kSelScoreBytes = 40960 - 4;
-// Rows of 1025 to 3072 key blocks (17 to 48 chunks of 64) run in one
-// 16-wave workgroup per CU instead, one row per wave with its keys in
-// registers, over static LDS for up to 16 rows of scores (16 rows up to
-// nk = 2499, 15 at 2633, 13 at 3072), so that the head's pooled keys are
-// read once per 13-16 rows instead of once per 3-8.  Below 1025 key blocks
-// four workgroups per CU measured faster: one workgroup's score phase then
-// overlaps another's selection.
+// Rows of 769 to 1536 key blocks (13 to 24 chunks) run in 8-wave workgroups,
+// two per CU, over 80,000 bytes of static LDS each (16 rows up to nk = 1249,
+// 15 at 1317, 13 at 1536), two rows per wave in registers; rows of 1537 to
+// 3072 (25 to 48 chunks) in one 16-wave workgroup per CU over 160,000 bytes
+// (16 rows up to nk = 2499, 15 at 2633, 13 at 3072), one row per wave.  The
+// head's pooled keys are then read once per 13-16 rows instead of once per
+// 3-8; two workgroups per CU where they fit, so that one workgroup's score
+// phase overlaps another's selection.
+constexpr int kSelMidWaves = 8;
+constexpr int kSelMidScoreFloats = 20000;
 constexpr int kSelWideWaves = 16;
-constexpr int kSelWideMinChunks = 17;
 constexpr int kSelWideScoreFloats = 40000;
 constexpr int kSelKeyTile = 16;  // key blocks per score tile (one MFMA output tile)
 
@@ -103,16 +105,19 @@ __device__ __forceinline__ void load_score_operand(f32x4 (&x)[8], const float *r
 // (score desc, index asc) order without ranking every pair.  Kept indices are
 // written in ascending order with one ballot per 64-key chunk.
 template <int NW>
-__global__ void __launch_bounds__(NW * 64) block_select_kernel(
+__global__ void __launch_bounds__(NW * 64, NW == kSelMidWaves ? 4 : 1) block_select_kernel(
     const float *pq, const float *pk, int nq, int nk, int rows_per_wg, int keep, int force_diag,
     int blk_q, int blk_k, int32_t *lut, int32_t *counts, int max_k, uint8_t *map) {
-  static_assert(NW == kSelThreads / 64 || NW == kSelWideWaves, "a 4-wave or a 16-wave workgroup");
+  static_assert(NW == kSelThreads / 64 || NW == kSelMidWaves || NW == kSelWideWaves, "4, 8 or 16 waves");
   // [R][nk] scores, then one spare slot: dynamic LDS (4 waves), or static
   // LDS sized for the longest rows of the 16-wave form.
   float *sc;
   if constexpr (NW == kSelWideWaves) {
     __shared__ float sc_wide[kSelWideScoreFloats];
     sc = sc_wide;
+  } else if constexpr (NW == kSelMidWaves) {
+    __shared__ float sc_mid[kSelMidScoreFloats];
+    sc = sc_mid;
   } else {
     extern __shared__ float sc_dyn[];
     sc = sc_dyn;
@@ -214,9 +219,8 @@ __global__ void __launch_bounds__(NW * 64) block_select_kernel(
   // Rows of up to NC*64 key blocks: the keys of all of this wave's rows
   // (wave + NW*i, i < RPW) sit in registers, NC per lane per row, and the
   // rows' searches run interleaved, so their 32 dependent counting rounds
-  // overlap.  (NC, RPW) = (6, 4), (12, 4) or (24, 2) with 4 waves (the launch
-  // gives a workgroup at most 8 rows for the last), (24, 1) or (48, 1) with
-  // 16: at most 48 registers of keys.
+  // overlap.  (NC, RPW) = (6, 4) or (12, 4) with 4 waves, (24, 2) with 8,
+  // (48, 1) with 16: at most 48 registers of keys, for 16 rows.
   auto select_rows_regs = [&](auto nc_const, auto rpw_const) __attribute__((always_inline)) {
     constexpr int NC = decltype(nc_const)::value;
     constexpr int RPW = decltype(rpw_const)::value;
@@ -302,10 +306,13 @@ __global__ void __launch_bounds__(NW * 64) block_select_kernel(
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I4 = std::integral_constant<int, 4>;
-  if constexpr (NW == kSelWideWaves) {
-    if (nchunks <= 24 && nrows <= NW)
-      select_rows_regs(std::integral_constant<int, 24>{}, I1{});
-    else if (nchunks <= 48 && nrows <= NW)
+  if constexpr (NW == kSelMidWaves) {
+    if (nchunks <= 24 && nrows <= 2 * NW)
+      select_rows_regs(std::integral_constant<int, 24>{}, I2{});
+    else
+      select_rows_lds();
+  } else if constexpr (NW == kSelWideWaves) {
+    if (nchunks <= 48 && nrows <= NW)
       select_rows_regs(std::integral_constant<int, 48>{}, I1{});
     else
       select_rows_lds();
@@ -314,8 +321,6 @@ __global__ void __launch_bounds__(NW * 64) block_select_kernel(
       select_rows_regs(std::integral_constant<int, 6>{}, I4{});
     else if (nchunks <= 12)
       select_rows_regs(std::integral_constant<int, 12>{}, I4{});
-    else if (nchunks <= 24 && nrows <= 8)
-      select_rows_regs(std::integral_constant<int, 24>{}, I2{});
     else
       select_rows_lds();
   }
@@ -431,7 +436,15 @@ int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, 
                         int force_diag, int blk_q, int blk_k, int32_t *lut, int32_t *counts,
                         int max_k, uint8_t *map, hipStream_t s) {
   const int nchunks = (nk + 63) / 64;
-  if (nchunks >= kSelWideMinChunks && nchunks <= 48) {
+  if (nchunks > 12 && nchunks <= 24) {
+    int rows = (kSelMidScoreFloats - 1) / nk;
+    rows = rows > kSelRowsMax ? kSelRowsMax : rows;  // >= 13 for nk <= 1536
+    const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
+    hipLaunchKernelGGL(block_select_kernel<kSelMidWaves>, dim3((unsigned)groups), dim3(kSelMidWaves * 64), 0,
+                       s, pq, pk, nq, nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);
+    return check_launch("block_select_kernel<8 waves>");
+  }
+  if (nchunks > 24 && nchunks <= 48) {
     int rows = (kSelWideScoreFloats - 1) / nk;
     rows = rows > kSelRowsMax ? kSelRowsMax : rows;  // >= 13 for nk <= 3072
     const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
@@ -439,11 +452,8 @@ int launch_block_select(const float *pq, const float *pk, int B, int H, int nq, 
                        s, pq, pk, nq, nk, rows, keep, force_diag, blk_q, blk_k, lut, counts, max_k, map);
     return check_launch("block_select_kernel<16 waves>");
   }
-  // Rows of 13-16 chunks are selected from registers, 2 per wave: at most 8
-  // rows per workgroup.
-  const int cap = nchunks > 12 ? 8 : kSelRowsMax;
   int rows = kSelScoreBytes / (nk * (int)sizeof(float));
-  rows = rows < 1 ? 1 : (rows > cap ? cap : rows);
+  rows = rows < 1 ? 1 : (rows > kSelRowsMax ? kSelRowsMax : rows);
   const size_t lds = ((size_t)rows * nk + 1) * sizeof(float);
   const int64_t groups = (int64_t)B * H * ((nq + rows - 1) / rows);
   hipLaunchKernelGGL(block_select_kernel<kSelThreads / 64>, dim3((unsigned)groups), dim3(kSelThreads), lds, s,

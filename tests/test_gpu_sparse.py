@@ -455,7 +455,7 @@ def _select_ref(pq, pk, keep, blk_q, blk_k, diag, max_k):
 
 @pytest.mark.parametrize("nq,nk,diag", [(40, 1025, True), (33, 2633, False), (17, 3072, True)])
 def test_block_select_long_rows_real_scores(gpu, nq, nk, diag):
-    """Rows of 1025-3072 key blocks (the 16-wave workgroup) on real-valued pooled vectors
+    """Rows of 1025-3072 key blocks (the 8- and 16-wave workgroups) on real-valued pooled vectors
     against a float64 selection: the kept set may differ only where a score is within
     fp32 rounding of the keep-th largest; the LUT and counts follow the map."""
     rng = np.random.default_rng(nq + nk)
@@ -488,14 +488,14 @@ def test_block_select_exact_ties(gpu, nq, nk, keep, diag, max_k):
     """Integer pooled vectors make every score an exact fp32 integer, with many ties:
     the kept set, its order and the truncation to max_k_blocks must match exactly.
     Covers row groups of up to 16 query blocks per workgroup (fewer where the score
-    rows fill LDS or the register paths cap them: 14 at nk 700, 8 at nk 769-1024, 16 at
-    1025-2499 and 13 at 3072 in the 16-wave form, 3 at 3073, 2 at 5000, 1 at the 7000
-    maximum; the score MFMAs' rows past a group's end are computed and dropped), partial
-    last groups (nq 17, 33), key tiles past nk (nk 65, 1, 769, 1000, 1025, 1537, 2500,
-    3073), and all five counting paths: keys held in registers, 4 rows per wave in 6
-    (nk <= 384) or 12 (nk <= 768), 2 rows in 24 (nk <= 1024), 1 row per wave of a
-    16-wave workgroup in 24 (nk 1025-1536) or 48 (nk 1537-3072), and re-read from LDS
-    (3073 and above), each at its boundaries."""
+    rows fill LDS: 14 at nk 700, 13 at 1536 in the 8-wave form, 13 at 3072 in the 16-wave
+    form, 3 at 3073, 2 at 5000, 1 at the 7000 maximum; the score MFMAs' rows past a
+    group's end are computed and dropped), partial last groups (nq 17, 33), key tiles
+    past nk (nk 65, 1, 769, 1000, 1025, 1537, 2500, 3073), and all four counting paths,
+    each at its boundaries: keys held in registers, 4 rows per wave of a 4-wave
+    workgroup in 6 (nk <= 384) or 12 (nk <= 768), 2 rows per wave of an 8-wave one in 24
+    (nk 769-1536), 1 row per wave of a 16-wave one in 48 (nk 1537-3072), and re-read
+    from LDS (3073 and above)."""
     rng = np.random.default_rng(50 + nq + nk)
     pq = rng.integers(-2, 3, (1, 2, nq, 128)).astype(np.float32)
     pk = rng.integers(-2, 3, (1, 2, nk, 128)).astype(np.float32)
