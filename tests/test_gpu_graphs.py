@@ -57,12 +57,13 @@ def test_graph_replay_matches_eager(gpu):
             assert torch.equal(o, w), f"replay {r}, layer {i} differs from the eager run"
 
 
-@pytest.mark.parametrize("nk", [700, 2000])
+@pytest.mark.parametrize("nk", [700, 1300, 2000])
 def test_graph_capture_of_wide_block_select(gpu, nk):
     """Block select over long rows: 700 key blocks (44 score tiles per row, 14 query blocks
-    per 4-wave workgroup, keys counted in 12 registers per lane) and 2000 (the 16-wave
-    workgroup over static LDS, 16 query blocks each, 48 registers per lane): captured into
-    a graph, every replay equals the eager call."""
+    per 4-wave workgroup, keys counted in 12 registers per lane), 1300 (8-wave workgroups
+    over static LDS, 15 query blocks each, 2 rows per wave in 24 registers) and 2000 (the
+    16-wave workgroup, 16 query blocks, 48 registers per lane): captured into a graph,
+    every replay equals the eager call."""
     g = torch.Generator(device=gpu).manual_seed(41)
     pq = torch.randn(1, 2, 20, 128, generator=g, device=gpu)
     pk = torch.randn(1, 2, nk, 128, generator=g, device=gpu)
