@@ -201,6 +201,9 @@ def _parse():
     ap.add_argument("--blk", type=int, default=128, choices=list(range(16, 257, 16)),
                     help="sparse: query and key tile size (128: the 128x128 workload; 64: the SLA "
                          "block size default)")
+    ap.add_argument("--topk", type=float, default=0.25,
+                    help="sparse: fraction of key tiles kept per query tile by score, plus the diagonal "
+                         "(0.25: the 128x128 workload; 0.35: the SLA node's default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-clock", action="store_true",
                     help="dense: skip the shader-clock measurement (one profiled layer after the timed steps)")
@@ -308,10 +311,12 @@ def run_dense(args, torch, h3attn, dev, heads=H):
 
 def run_sparse(args, torch, h3attn, dev):
     """Block-sparse (h3_sla path): blk x blk tiles (128 by default: 330 per head at S=42120),
-    top floor(0.25*nk) key tiles per query tile from mean-pooled scores plus the diagonal
-    (82 of 330 at 128); FLOPs counted exactly from the map."""
+    top floor(topk*nk) key tiles per query tile from mean-pooled scores plus the diagonal
+    (82 of 330 at 128 and topk 0.25); FLOPs counted exactly from the map."""
     from h3attn import ops, sla
-    L, blk = args.layers, args.blk
+    L, blk, topk = args.layers, args.blk, args.topk
+    if not 0.0 < topk <= 1.0:
+        raise SystemExit(f"--topk {topk}: must lie in (0, 1]")
     nk = (S + blk - 1) // blk
     tiles = blk not in ops.NATIVE_BLOCKS
     items = []
@@ -323,7 +328,7 @@ def run_sparse(args, torch, h3attn, dev):
         v = torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16).mul_(4)
         a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        bmap, lut, cnt = sla.get_block_map(q, k, 0.25, blk, blk, force_diag=True, smooth_k=False)
+        bmap, lut, cnt = sla.get_block_map(q, k, topk, blk, blk, force_diag=True, smooth_k=False)
         if tiles:  # block sizes outside the native kernels': 32-key columns with sub-block masks
             lut, cnt = ops.block_map_to_tile_lut(bmap, blk, blk, S, S)
         b_.record()
@@ -356,17 +361,22 @@ def run_sparse(args, torch, h3attn, dev):
     value = flops * L * args.steps / wall / 1e12
     achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
     res = _base(args, "block-sparse attn TFLOP/s (exact kept-tile FLOPs) at H=56,S=42120,D=128, "
-                      f"{blk}x{blk} tiles, top-25%+diagonal", value, "TFLOP/s", wall * 1e3 / args.steps,
+                      f"{blk}x{blk} tiles, top-{round(100 * topk)}%+diagonal", value, "TFLOP/s",
+                wall * 1e3 / args.steps,
                 {"workload": f"block-sparse attention, {L} layers per step", "B": B, "H": H, "S": S,
                  "D": D, "blk_q": blk, "blk_k": blk,
-                 "keep": f"{int(0.25 * nk)} of {nk} key tiles + diagonal"})
-    traffic, traffic_src = measured_traffic(TILES_TRAFFIC_SUMMARY if tiles else SPARSE_TRAFFIC_SUMMARY, f"sparse{blk}")
+                 "keep": f"{sla.keep_count(topk, nk)} of {nk} key tiles + diagonal"})
+    if topk == 0.25:  # the counter summaries were measured at this keep ratio
+        traffic, traffic_src = measured_traffic(TILES_TRAFFIC_SUMMARY if tiles else SPARSE_TRAFFIC_SUMMARY,
+                                                f"sparse{blk}")
+    else:
+        traffic, traffic_src = None, "counters measured at --topk 0.25 only"
     res.update({
         "ms_per_layer": round(avg_kernel_ms, 3),
         "kept_fraction": round(flops / flops_per_layer(), 4),
         "dense_equivalent_tflops": round(flops_per_layer() / (avg_kernel_ms * 1e-3) / 1e12, 1),
         "block_map_ms": round(sum(map_ms[1:]) / max(1, len(map_ms) - 1), 3),
-        "block_map_pooled_in_prologue": fused_pool_cost(torch, h3attn, dev, blk),
+        "block_map_pooled_in_prologue": fused_pool_cost(torch, h3attn, dev, blk, topk),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
@@ -386,7 +396,7 @@ def run_sparse(args, torch, h3attn, dev):
     return res
 
 
-def fused_pool_cost(torch, h3attn, dev, blk, reps=10):
+def fused_pool_cost(torch, h3attn, dev, blk, topk=0.25, reps=10):
     """Block-map cost when the prologue pools (h3a_qk_rmsnorm_rope_pool), at H=56, S=42120: median
     ms of the prologue alone, of the prologue with pooling at `blk`, and of the selection from
     those means (top 25 % + diagonal), each over `reps` launches on fused [S,3HD] views."""
@@ -410,7 +420,7 @@ def fused_pool_cost(torch, h3attn, dev, blk, reps=10):
 
     plain, _ = med(lambda: ops.qk_rmsnorm_rope_(q, k, rope, qw, kw, rot_dim=128))
     pooled, (pq, pk) = med(lambda: ops.qk_rmsnorm_rope_(q, k, rope, qw, kw, rot_dim=128, pool_blk=blk))
-    select, _ = med(lambda: ops.block_select(pq, pk, sla.keep_count(0.25, nk), blk, blk, force_diag=True,
+    select, _ = med(lambda: ops.block_select(pq, pk, sla.keep_count(topk, nk), blk, blk, force_diag=True,
                                              want_map=blk not in ops.NATIVE_BLOCKS))
     del qkv
     return {"prologue_ms": round(plain, 3), "prologue_pool_ms": round(pooled, 3),
